@@ -1,0 +1,486 @@
+#!/usr/bin/env python3
+"""Throughput of the fused fragment kernels on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--all] [--no-cpu]
+
+A step is one call of the fragment (one pass of the hot path over one batch
+of synthetic input, already resident in HBM).  Workloads are the
+BASELINE.json configurations:
+
+  c1   RMSNorm forward        x [4096, 4096]              -> y bf16, rstd fp32
+  c2   RMSNorm backward       x, dy [8192, 4096]          -> dx bf16, dw fp32   (default: configs[1])
+  c3f  embedding forward      table [128256, 4096], ids [8, 2048] Zipf(1.1) -> [8, 2048, 4096]
+  c3b  embedding backward     grad [8, 2048, 4096]        -> dense fp32 [128256, 4096]
+  c4   RoPE rotate-half       q [4, 4096, 32, 128], k [4, 4096, 8, 128], pos 0..4095, theta 5e5
+  c5f  add + RMSNorm forward  x, res [16384, 8192]        -> h, y bf16
+  c5b  add + RMSNorm backward x, res, dy [16384, 8192]    -> dx bf16, dw fp32
+
+Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
+~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
+find its operands in cache from the previous call.  The timed loop calls the
+C ABI directly through pre-bound ctypes arguments.  value = algorithmic
+bytes per call * steps / wall time.  roofline.achieved = the dominant
+kernel's algorithmic bytes / its mean duration, timed with HIP events that
+the library records around that kernel (kp_profile_dominant_kernel) in the
+same timed loop.  The cpu_baseline is the torch CPU eager restatement of the
+fragment (oracle/torch_ref.py) on the same seeded inputs.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+PEAK_GBS = 8000.0  # MI355X HBM3E
+MIN_ROTATION_BYTES = 1 << 30
+
+
+def _u16():
+    import torch
+    return torch.bfloat16
+
+
+class Workload:
+    """Inputs, pre-bound ABI calls and byte counts of one configuration."""
+
+    name = ""
+    description = ""
+    bytes_per_call = 0       # algorithmic bytes of the whole fragment call
+    dominant_bytes = 0       # algorithmic bytes moved by the dominant kernel
+    dominant_kernel = ""
+    cpu_sample = ""
+
+    def __init__(self, dev):
+        self.dev = dev
+        self.sets = []  # per rotation set: (fn, args, keepalive)
+
+    def rotations(self, per_set_bytes):
+        return max(2, math.ceil(MIN_ROTATION_BYTES / max(per_set_bytes, 1)))
+
+    def step(self, i):
+        fn, args, _ = self.sets[i % len(self.sets)]
+        st = fn(*args)
+        if st != 0:
+            from kernelproblems_amd import _lib as L
+            raise L.KPError(fn.__name__, st, L.lib().kp_last_error_message().decode())
+
+    def cpu_run(self):
+        raise NotImplementedError
+
+
+def _gen(seed=0):
+    import torch
+    return torch.Generator().manual_seed(seed)
+
+
+def _randn(shape, g, mean=0.0, std=1.0):
+    import torch
+    return (torch.randn(shape, generator=g) * std + mean).to(torch.bfloat16)
+
+
+def _zipf(n, vocab, s, g):
+    import torch
+    r = torch.arange(1, vocab + 1, dtype=torch.float64)
+    p = r.pow(-s)
+    p /= p.sum()
+    return torch.multinomial(p, n, replacement=True, generator=g).to(torch.int64)
+
+
+# ------------------------------------------------------------------ RMSNorm
+class RmsFwd(Workload):
+    def __init__(self, dev, M=4096, N=4096, eps=1e-6, name="c1", residual=False, rstd=True):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        g = _gen(0)
+        self.x = _randn((M, N), g)
+        self.res = _randn((M, N), g) if residual else None
+        self.w = _randn(N, g, 1.0, 0.02)
+        self.eps, self.M, self.N = eps, M, N
+        n_in = 2 if residual else 1
+        n_out = 2 if residual else 1
+        self.bytes_per_call = (n_in + n_out) * M * N * 2 + N * 2 + (M * 4 if rstd else 0)
+        self.dominant_bytes = self.bytes_per_call
+        self.dominant_kernel = "rms_fwd_vec"
+        if residual:
+            self.description = f"C5 residual add + RMSNorm forward: x, res [{M},{N}] bf16 -> h, y bf16 (eps={eps})"
+        else:
+            self.description = f"C1 RMSNorm forward: x [{M},{N}] bf16 -> y bf16, rstd fp32 (eps={eps})"
+        per_set = self.bytes_per_call
+        R = self.rotations(per_set)
+        xd, wd = self.x.to(dev), self.w.to(dev)
+        rd = self.res.to(dev) if residual else None
+        fn = L.lib().kp_rmsnorm_fwd_bf16
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for r in range(R):
+            xs = xd.clone()
+            rs = rd.clone() if residual else None
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            h = torch.empty((M, N), dtype=torch.bfloat16, device=dev) if residual else None
+            rstd_t = torch.empty(M, dtype=torch.float32, device=dev) if rstd else None
+            terms = [xs] + ([rs] if residual else [])
+            pa, sa = L.ptr_array([t.data_ptr() for t in terms]), L.i64_array([N] * len(terms))
+            args = (pa, sa, len(terms), wd.data_ptr(), N, N, None if h is None else h.data_ptr(), N, y.data_ptr(),
+                    N, None if rstd_t is None else rstd_t.data_ptr(), M, N, eps, stream)
+            self.sets.append((fn, args, (xs, rs, y, h, rstd_t, pa, sa, wd)))
+        self.cpu_sample = f"full [{M},{N}] call"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        if self.res is not None:
+            torch_ref.add_rms_norm_fwd(self.x, self.res, self.w, self.eps)
+        else:
+            torch_ref.rms_norm_fwd(self.x, self.w, self.eps)
+
+
+class RmsBwd(Workload):
+    def __init__(self, dev, M=8192, N=4096, eps=1e-6, name="c2", residual=False):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        g = _gen(0)
+        self.x = _randn((M, N), g)
+        self.res = _randn((M, N), g) if residual else None
+        self.w = _randn(N, g, 1.0, 0.02)
+        self.dy = _randn((M, N), g)
+        self.eps, self.M, self.N = eps, M, N
+        n_in = 3 if residual else 2
+        self.dominant_bytes = (n_in + 1) * M * N * 2 + N * 2
+        self.bytes_per_call = self.dominant_bytes + N * 4
+        self.dominant_kernel = "rms_bwd_vec"
+        if residual:
+            self.description = (f"C5 residual add + RMSNorm backward: x, res, dy [{M},{N}] bf16 -> dx bf16, dw fp32 "
+                                f"(h, rstd recomputed; eps={eps})")
+        else:
+            self.description = (f"C2 RMSNorm backward: x, dy [{M},{N}] bf16 -> dx bf16, dw fp32 "
+                                f"(rstd recomputed; eps={eps})")
+        R = self.rotations(self.bytes_per_call)
+        xd, wd, dyd = self.x.to(dev), self.w.to(dev), self.dy.to(dev)
+        rd = self.res.to(dev) if residual else None
+        fn = L.lib().kp_rmsnorm_bwd_bf16
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws_bytes = int(L.lib().kp_rmsnorm_bwd_workspace_size(M, N))
+        for r in range(R):
+            xs, dys = xd.clone(), dyd.clone()
+            rs = rd.clone() if residual else None
+            dx = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            dw = torch.empty(N, dtype=torch.float32, device=dev)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            xterms = [xs] + ([rs] if residual else [])
+            dpa, dsa = L.ptr_array([dys.data_ptr()]), L.i64_array([N])
+            xpa, xsa = L.ptr_array([t.data_ptr() for t in xterms]), L.i64_array([N] * len(xterms))
+            args = (dpa, dsa, 1, xpa, xsa, len(xterms), None, wd.data_ptr(), N, N, None, N, dx.data_ptr(), N,
+                    dw.data_ptr(), None, 0, M, N, eps, ws.data_ptr(), ws_bytes, stream)
+            self.sets.append((fn, args, (xs, dys, rs, dx, dw, ws, dpa, dsa, xpa, xsa, wd)))
+        self.cpu_sample = f"full [{M},{N}] call"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        if self.res is not None:
+            torch_ref.add_rms_norm_bwd(self.x, self.res, self.dy, self.w, self.eps)
+        else:
+            torch_ref.rms_norm_bwd(self.x, self.dy, self.w, self.eps)
+
+
+# ---------------------------------------------------------------- embedding
+class EmbFwd(Workload):
+    def __init__(self, dev, V=128256, D=4096, B=8, S=2048, name="c3f"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        self.ids = _zipf(B * S, V, 1.1, _gen(0)).view(B, S)
+        self.table = _randn((V, D), _gen(1), 0.0, 0.02)
+        T = B * S
+        self.bytes_per_call = 2 * T * D * 2 + T * 8
+        self.dominant_bytes = self.bytes_per_call
+        self.dominant_kernel = "emb_fwd"
+        uniq = int(torch.unique(self.ids).numel())
+        self.description = (f"C3 embedding forward: table [{V},{D}] bf16, ids [{B},{S}] int64 Zipf(1.1) "
+                            f"({uniq} distinct) -> [{B},{S},{D}] bf16, bit-exact gather")
+        # per call: the distinct rows read + the output written; rotate whole tables
+        R = max(2, math.ceil(MIN_ROTATION_BYTES / (uniq * D * 2 + T * D * 2)))
+        tab_d, ids_d = self.table.to(dev), self.ids.to(dev)
+        fn = L.lib().kp_embedding_fwd_bf16
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for r in range(R):
+            tab = tab_d if r == 0 else tab_d.clone()
+            out = torch.empty((B, S, D), dtype=torch.bfloat16, device=dev)
+            args = (tab.data_ptr(), V, D, D, ids_d.data_ptr(), 8, T, out.data_ptr(), D, None, stream)
+            self.sets.append((fn, args, (tab, out)))
+        self.cpu_sample = f"full [{B},{S}] gather"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        torch_ref.embedding_fwd(self.table, self.ids)
+
+
+class EmbBwd(Workload):
+    def __init__(self, dev, V=128256, D=4096, B=8, S=2048, name="c3b"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        self.ids = _zipf(B * S, V, 1.1, _gen(0)).view(B, S)  # the same ids as the forward
+        self.grad = _randn((B, S, D), _gen(2))
+        self.V = V
+        T = B * S
+        self.bytes_per_call = T * D * 2 + T * 8 + V * D * 4
+        self.dominant_bytes = self.bytes_per_call
+        self.dominant_kernel = "emb_dense"
+        uniq = int(torch.unique(self.ids).numel())
+        self.description = (f"C3 embedding backward: grad [{B},{S},{D}] bf16, ids Zipf(1.1) ({uniq} distinct) -> "
+                            f"dense fp32 [{V},{D}], sort-and-segment, each row written once")
+        R = self.rotations(self.bytes_per_call)
+        gd, idd = self.grad.to(dev), self.ids.to(dev)
+        fn = L.lib().kp_embedding_bwd_bf16
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        ws_bytes = int(L.lib().kp_embedding_bwd_workspace_size(T, V, D))
+        for r in range(R):
+            gs = gd.clone()
+            out = torch.empty((V, D), dtype=torch.float32, device=dev)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            args = (gs.data_ptr(), D, idd.data_ptr(), 8, T, V, D, -1, 0, out.data_ptr(), 0, 0, ws.data_ptr(),
+                    ws_bytes, None, stream)
+            self.sets.append((fn, args, (gs, out, ws)))
+        self.cpu_sample = f"full [{B},{S}] x {D} scatter into [{V},{D}]"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        torch_ref.embedding_bwd(self.grad, self.ids, self.V)
+
+
+# --------------------------------------------------------------------- RoPE
+class Rope(Workload):
+    def __init__(self, dev, B=4, S=4096, Hq=32, Hk=8, D=128, theta=500000.0, name="c4"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        g = _gen(0)
+        self.q = _randn((B, S, Hq, D), g)
+        self.k = _randn((B, S, Hk, D), g)
+        self.pos = torch.arange(S, dtype=torch.int64).expand(B, S).contiguous()
+        self.theta = theta
+        nq, nk = B * S * Hq * D, B * S * Hk * D
+        self.bytes_per_call = 2 * (nq + nk) * 2 + B * S * 8
+        self.dominant_bytes = self.bytes_per_call
+        self.dominant_kernel = "rope_kernel"
+        self.description = (f"C4 RoPE rotate-half: q [{B},{S},{Hq},{D}], k [{B},{S},{Hk},{D}] bf16, positions "
+                            f"[{B},{S}] int64 0..{S - 1}, theta={theta:g}, cos/sin in fp32 in-kernel")
+        R = self.rotations(self.bytes_per_call)
+        qd, kd, pd = self.q.to(dev), self.k.to(dev), self.pos.to(dev)
+        fn = L.lib().kp_rope_bf16
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for r in range(R):
+            qs, ks = qd.clone(), kd.clone()
+            qo, ko = torch.empty_like(qs), torch.empty_like(ks)
+            sq = L.i64_array(list(qs.stride()[:3]))
+            sk = L.i64_array(list(ks.stride()[:3]))
+            args = (qs.data_ptr(), qo.data_ptr(), Hq, sq, sq, ks.data_ptr(), ko.data_ptr(), Hk, sk, sk, B, S, D,
+                    pd.data_ptr(), 8, S, 1, 0, theta, None, 0, 0, 0, None, stream)
+            self.sets.append((fn, args, (qs, ks, qo, ko, sq, sk, pd)))
+        self.cpu_sample = f"full [{B},{S}] q and k"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        torch_ref.rope_half(self.q, self.k, self.pos, self.theta)
+
+
+def make_workload(name, dev):
+    if name == "c1":
+        return RmsFwd(dev, 4096, 4096, 1e-6, "c1")
+    if name == "c2":
+        return RmsBwd(dev, 8192, 4096, 1e-6, "c2")
+    if name == "c3f":
+        return EmbFwd(dev)
+    if name == "c3b":
+        return EmbBwd(dev)
+    if name == "c4":
+        return Rope(dev)
+    if name == "c5f":
+        return RmsFwd(dev, 16384, 8192, 1e-5, "c5f", residual=True, rstd=False)
+    if name == "c5b":
+        return RmsBwd(dev, 16384, 8192, 1e-5, "c5b", residual=True)
+    raise SystemExit(f"unknown workload {name!r}")
+
+
+ALL = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
+
+
+# ------------------------------------------------------------------ measure
+def measure_gpu(wl, steps, warmup):
+    import torch
+    from kernelproblems_amd import _lib as L
+    lib = L.lib()
+    for i in range(warmup):
+        wl.step(i)
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in starts + stops:  # materialise the hipEvent_t handles
+        e.record()
+    t0e, t1e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    t0e.record()
+    for i in range(steps):
+        lib.kp_profile_dominant_kernel(starts[i].cuda_event, stops[i].cuda_event)
+        wl.step(warmup + i)
+    lib.kp_profile_dominant_kernel(None, None)
+    t1e.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    gpu_ms = t0e.elapsed_time(t1e)
+    dom = [starts[i].elapsed_time(stops[i]) for i in range(steps)]
+    dom_ms = sum(dom) / len(dom)
+    ms_per_step = wall * 1e3 / steps
+    value = wl.bytes_per_call * steps / wall / 1e9
+    achieved = wl.dominant_bytes / (dom_ms * 1e-3) / 1e9
+    return {
+        "ms_per_step": ms_per_step,
+        "gpu_ms_per_step": gpu_ms / steps,
+        "value": value,
+        "dominant_ms": dom_ms,
+        "dominant_ms_min": min(dom),
+        "achieved": achieved,
+    }
+
+
+def measure_cpu(wl, seconds):
+    import torch
+    wl.cpu_run()  # warm-up
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter()
+        wl.cpu_run()
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_all >= seconds or len(times) >= 50:
+            break
+    times.sort()
+    med = times[len(times) // 2]
+    return {
+        "value": wl.bytes_per_call / med / 1e9,
+        "unit": "GB/s",
+        "ms_per_call": med * 1e3,
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"torch CPU eager restatement of the fragment (oracle/torch_ref.py), {wl.cpu_sample}, "
+                   f"median of {len(times)} timed calls after 1 warm-up"),
+    }
+
+
+def load_traffic(name):
+    p = ROOT / "profiles" / "traffic.json"
+    try:
+        return json.loads(p.read_text()).get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="c2", choices=ALL)
+    ap.add_argument("--all", action="store_true", help="also measure every other workload (GPU only)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
+              "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+        return 2
+
+    import torch
+    import kernelproblems_amd as kp
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device visible", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+
+    def run(name, with_cpu):
+        print(f"[bench] preparing {name}", file=sys.stderr, flush=True)
+        wl = make_workload(name, dev)
+        r = measure_gpu(wl, args.steps, args.warmup)
+        print(f"[bench] {name}: {r['ms_per_step'] * 1e3:.1f} us/call, {r['value']:.0f} GB/s, dominant kernel "
+              f"{r['dominant_ms'] * 1e3:.1f} us -> {r['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+        cpu = None
+        if with_cpu:
+            print(f"[bench] cpu baseline {name}", file=sys.stderr, flush=True)
+            cpu = measure_cpu(wl, args.cpu_seconds)
+        wl.sets.clear()
+        torch.cuda.empty_cache()
+        return wl, r, cpu
+
+    wl, r, cpu = run(args.workload, not args.no_cpu)
+    line = {
+        "metric": "achieved HBM GB/s and % of 8 TB/s peak per fragment; us/call vs CPU eager",
+        "value": round(r["value"], 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(r["ms_per_step"], 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {
+            "workload": wl.description,
+            "io_dtype": "bf16",
+            "algorithmic_bytes_per_call": wl.bytes_per_call,
+            "gpu_ms_per_step": round(r["gpu_ms_per_step"], 6),
+            "pct_of_hbm_peak": round(100 * r["value"] / PEAK_GBS, 2),
+            "device": torch.cuda.get_device_name(dev),
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(r["achieved"], 2),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(r["achieved"] / PEAK_GBS, 4),
+            "traffic": load_traffic(args.workload),
+            "kernel": wl.dominant_kernel,
+            "kernel_us": round(r["dominant_ms"] * 1e3, 3),
+            "kernel_bytes": wl.dominant_bytes,
+        },
+        "cpu_baseline": cpu,
+    }
+    if args.all:
+        frags = {}
+        for name in ALL:
+            if name == args.workload:
+                continue
+            w2, r2, _ = run(name, False)
+            frags[name] = {
+                "workload": w2.description,
+                "us_per_call": round(r2["ms_per_step"] * 1e3, 3),
+                "GBps": round(r2["value"], 1),
+                "pct_of_peak": round(100 * r2["value"] / PEAK_GBS, 2),
+                "kernel": w2.dominant_kernel,
+                "kernel_us": round(r2["dominant_ms"] * 1e3, 3),
+                "kernel_GBps": round(r2["achieved"], 1),
+                "bytes_per_call": w2.bytes_per_call,
+            }
+        line["fragments"] = frags
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,202 @@
+/*
+ * kp.h -- C ABI of the MI355X (gfx950) fused graph-fragment kernels.
+ *
+ * The reference (SherlockNoMad/KernelProblems) is a corpus of torch graph
+ * fragments; each fragment's drop-in contract is a Python
+ * `kernel_function(*inputs) -> outputs` whose results must match the
+ * fragment's `Model.forward` (e.g. v8/7884328a5557/optimized_kernel.py:37-55
+ * against v8/7884328a5557/problem.py:9-33).  The aten operators those
+ * fragments are built from are what this library replaces; the Python layer in
+ * kernelproblems_amd/ binds these entry points with ctypes and rebuilds each
+ * fragment's exact signature on top of them.
+ *
+ * Conventions shared by every entry point:
+ *  - All pointers are device pointers (HIP global memory) except the small
+ *    host arrays `*_terms` / `*_strides`, which are read before return.
+ *  - bf16 tensors are passed as raw 16-bit storage (`void*`); strides are in
+ *    elements, never bytes.  The innermost dimension is always unit-stride.
+ *  - `stream` is a hipStream_t (NULL = the legacy default stream).  Every call
+ *    only enqueues work: no host synchronisation, no allocation; scratch memory
+ *    comes from the caller through (workspace, workspace_bytes).
+ *  - Calls on distinct streams with distinct workspaces are independent;
+ *    calls that share a workspace must be ordered by the caller.
+ *  - Return value: KP_OK or one of the KP_E* codes below; on KP_EHIP,
+ *    kp_last_hip_error() returns the hipError_t of the failed launch.
+ */
+#ifndef KP_H_
+#define KP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KP_OK 0
+#define KP_EINVAL 1        /* rejected argument: null pointer, shape, stride, alignment, dtype code */
+#define KP_EUNSUPPORTED 2  /* valid call outside what this build implements (message via kp_last_error_message) */
+#define KP_EHIP 3          /* a HIP runtime call or launch failed */
+#define KP_EWORKSPACE 4    /* workspace_bytes smaller than the matching *_workspace_size() */
+
+#define KP_DTYPE_F32 0
+#define KP_DTYPE_BF16 1
+
+#define KP_ROPE_HALF 0        /* rotate-half pairing: (i, i + D/2) */
+#define KP_ROPE_INTERLEAVED 1 /* complex pairing: (2i, 2i + 1) */
+
+/* Library identification and error reporting (per calling thread). */
+const char* kp_version(void);
+int kp_last_hip_error(void);
+const char* kp_last_error_message(void);
+
+/* Benchmark timing hook (no counterpart in the reference, whose timing lives
+ * in an external harness).  While set, every entry point records start_event
+ * (a hipEvent_t) immediately before and stop_event immediately after the
+ * launch of its dominant kernel, on the call's stream: the row kernel of the
+ * RMSNorm entry points, the gather kernel of kp_embedding_fwd_bf16, the
+ * dense-write kernel of kp_embedding_bwd_bf16 and the kernel of kp_rope_bf16.
+ * Pass NULL, NULL to clear.  Per calling thread. */
+void kp_profile_dominant_kernel(void* start_event, void* stop_event);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm forward, optionally fused with the residual add in front of it.
+ *
+ * Replaces torch.ops.aten._fused_rms_norm.default as called at
+ *   v7/59f786beb25f/problem.py:16      (returns y and rstd)
+ *   v8/4b90e2d83144/problem.py:16      (y only, returned as views)
+ *   v7/215dd2e6a519/problem.py:16-25   (weight = strided [8,512] view of an FSDP flat buffer)
+ * and the add.Tensor -> _fused_rms_norm region of
+ *   v8/7884328a5557/problem.py:20-33   (h = add_61 + mm_220, y = rms(h)).
+ *
+ * x_terms[0..n_x), 1 <= n_x <= 3: bf16 [M, N] tensors with row strides
+ *   x_strides[]; the normalised row is h = bf16(bf16(x0 + x1) + x2), each add
+ *   computed in fp32 and rounded to bf16 (eager bf16 add.Tensor), or x0.
+ * h_out (bf16 [M, N], row stride h_stride): receives h when n_x > 1; may be NULL.
+ * weight: bf16; element i is weight[(i / w_seg_len) * w_seg_stride + i % w_seg_len]
+ *   (a contiguous weight has w_seg_len = N); NULL means no weight.
+ * y (bf16 [M, N], row stride y_stride) = bf16(fp32(h) * rstd * fp32(w)).
+ * rstd (fp32 [M], may be NULL) = 1 / sqrt(sum(h^2) / N + eps).
+ */
+int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, int n_x,
+                        const void* weight, int64_t w_seg_len, int64_t w_seg_stride,
+                        void* h_out, int64_t h_stride,
+                        void* y, int64_t y_stride,
+                        float* rstd,
+                        int64_t M, int64_t N, float eps, void* stream);
+
+/* ------------------------------------------------------------------------
+ * RMSNorm backward with its neighbouring elementwise ops fused in.
+ *
+ * Replaces torch.ops.aten._fused_rms_norm_backward.default (+ _to_copy of the
+ * weight gradient) as called at
+ *   v7/45990c83cfd6/problem.py:17-28   (rstd recomputed by a forward; dx, dw bf16)
+ *   v8/d8f596b3df34/problem.py:26-45   (dy = mm_664 + mm_666; out = add_218 + dx; dw -> f32)
+ *   v7/ed20955ec34b/problem.py          (dy = (view_1794 + mm_672) + mm_674)
+ *   v8/3c6c589cdf81/problem.py:22-53   (x = (add_61 + mm_220) + mm_223 recomputed, rstd recomputed)
+ * following the decomposition torch/_decomp/decompositions.py:1815-1887.
+ *
+ * dy = bf16 running sum of dy_terms[0..n_dy), x = bf16 running sum of
+ * x_terms[0..n_x) (both 1..3 terms, rounding as in kp_rmsnorm_fwd_bf16).
+ * rstd: fp32 [M] as produced by the forward; NULL = recompute from x with eps.
+ * dx = bf16((g - xhat * sum(xhat * g) / N) * rstd), g = dy * w, xhat = x * rstd;
+ *   if dx_residual != NULL the stored value is bf16(dx_residual + bf16(dx)).
+ * dw[j] = sum over rows of dy * xhat, accumulated in fp32 with a fixed
+ *   two-stage order (run-to-run bitwise deterministic).  Written to dw_f32
+ *   (fp32 [N]; rounded to bf16 first when dw_f32_round_bf16 != 0, the
+ *   reference's bf16 -> _to_copy(f32)) and/or dw_bf16 (bf16 [N]).  Both may be
+ *   NULL; weight must be non-NULL whenever either is requested.
+ * workspace: at least kp_rmsnorm_bwd_workspace_size(M, N) bytes, 16-byte aligned.
+ */
+size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N);
+int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
+                        const void* const* x_terms, const int64_t* x_strides, int n_x,
+                        const float* rstd,
+                        const void* weight, int64_t w_seg_len, int64_t w_seg_stride,
+                        const void* dx_residual, int64_t dxr_stride,
+                        void* dx, int64_t dx_stride,
+                        float* dw_f32, void* dw_bf16, int dw_f32_round_bf16,
+                        int64_t M, int64_t N, float eps,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Embedding forward: out[t, :] = table[indices[t], :] (bit copy).
+ *
+ * Replaces torch.ops.aten.embedding.default at v7/1e49beb8a123/problem.py:23
+ * (table = [128256, 4096] view of an FSDP flat buffer, ids i64 [1, 8192]).
+ * indices: T integers of index_bytes (4 or 8) each, contiguous.
+ * An index outside [0, V) reads nothing: its output row is zero-filled and,
+ * when error_flag != NULL, *error_flag is set to 1 (never cleared here).
+ */
+int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table_row_stride,
+                          const void* indices, int index_bytes, int64_t T,
+                          void* out, int64_t out_row_stride,
+                          int32_t* error_flag, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Embedding backward, dense: G[v, :] = sum over {t : indices[t] == v,
+ * v != padding_idx} of grad[t, :] (divided by the id's count when
+ * scale_grad_by_freq), accumulated in fp32, every row of G written exactly
+ * once (rows without contributions are written as zeros).
+ *
+ * Replaces torch.ops.aten.embedding_dense_backward.default (+ _to_copy f32)
+ * at v7/a12a160cb11b/problem.py:16-20, following the decomposition
+ * torch/_decomp/decompositions.py:1245-1275.
+ *
+ * Deterministic sort-and-segment: (id, t) keys are sorted, each id's
+ * contributions are summed in ascending t, in fixed-size runs whose fp32
+ * partial sums are then added in run order.  No float atomics; the result is
+ * bitwise reproducible run to run.
+ * grad: bf16 [T, D] with row stride grad_row_stride.  indices as above.
+ * grad_table: [V, D] contiguous, out_dtype KP_DTYPE_F32 or KP_DTYPE_BF16; with
+ *   KP_DTYPE_F32 and out_round_bf16 != 0 every value is first rounded to bf16.
+ * padding_idx < 0 means none.  Out-of-range ids are skipped and flagged.
+ * Limits of this build: T <= 32768 and ceil(log2 V) + ceil(log2 T) <= 32
+ *   (KP_EUNSUPPORTED otherwise).
+ */
+size_t kp_embedding_bwd_workspace_size(int64_t T, int64_t V, int64_t D);
+int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride,
+                          const void* indices, int index_bytes, int64_t T,
+                          int64_t V, int64_t D, int64_t padding_idx, int scale_grad_by_freq,
+                          void* grad_table, int out_dtype, int out_round_bf16,
+                          void* workspace, size_t workspace_bytes,
+                          int32_t* error_flag, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Rotary position embedding on up to two tensors (q and k) in one launch.
+ *
+ * Replaces the _to_copy f32 -> view_as_complex -> mul -> view_as_real ->
+ * _to_copy bf16 chain of
+ *   v7/e29b92927600/problem.py:16-37   (k, freqs_cis given per position)
+ *   v8/c8c60d8f7015/problem.py:18-71   (q and k, freqs_cis gathered by position ids)
+ *   v7/5c65f62b0422/problem.py:16-40   (backward: grad given as a transposed view)
+ * and the rotate-half form of the north-star configuration.
+ *
+ * Tensor i (i = 0, 1; tensor 1 optional, x1 == NULL): x_i and out_i are bf16
+ *   [B, S, H_i, D] with element strides {b, s, h} in x_strides_i[3] /
+ *   out_strides_i[3] and unit stride on D (D even).
+ * positions: NULL (position of (b, s) is s) or B*S integers of pos_bytes
+ *   (4 or 8) at positions[b * pos_stride_b + s * pos_stride_s].
+ * Angles: when freqs_cis == NULL, inv_freq[i] = fp32(theta^(-2i/D)) and the
+ *   rotation of pair i at position p is (cos a, sin a), a = fp32(fp32(p) *
+ *   inv_freq[i]), evaluated in fp32 in-kernel.  Otherwise freqs_cis is a
+ *   complex64 table (interleaved float pairs) [freq_rows, D/2] with row
+ *   stride freq_row_stride (complex elements) and pair i of position p uses
+ *   freqs_cis[p, i] (p must lie in [0, freq_rows)).
+ * pairing KP_ROPE_HALF pairs (i, i + D/2); KP_ROPE_INTERLEAVED pairs (2i, 2i+1).
+ * out = bf16(x_a * c - x_b * s, x_b * c + x_a * s) computed in fp32; conj != 0
+ *   uses (c, -s) (the backward of the forward rotation).
+ */
+int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides, const int64_t* out0_strides,
+                 const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,
+                 int64_t B, int64_t S, int64_t D,
+                 const void* positions, int pos_bytes, int64_t pos_stride_b, int64_t pos_stride_s,
+                 int pairing, double theta,
+                 const float* freqs_cis, int64_t freq_rows, int64_t freq_row_stride,
+                 int conj, int32_t* error_flag, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KP_H_ */

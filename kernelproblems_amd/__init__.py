@@ -1,0 +1,39 @@
+"""MI355X (gfx950) kernels for the memory-bound fused graph fragments of
+SherlockNoMad/KernelProblems: RMSNorm forward/backward (with residual-add and
+gradient epilogues), embedding gather and its dense deterministic backward,
+and rotary position embedding on q/k.
+
+Layers:
+  * ``include/kp.h`` + ``csrc/*.hip``  -- the C ABI and the HIP kernels;
+  * ``_lib``      -- ctypes binding of ``libkp_hip.so`` (no fallback path);
+  * ``fused``     -- tensor-level fused operations over the C ABI;
+  * ``aten``      -- drop-ins for the aten operators used by the fragments;
+  * ``fragments`` -- ``kernel_function`` drop-ins for individual reference
+    fragments, keyed by their reference id.
+"""
+from . import aten, fused
+from ._lib import KPError, LIB_PATH, version
+from .fused import (
+    embedding,
+    embedding_dense_backward,
+    index_checking,
+    rms_norm,
+    rms_norm_backward,
+    rope,
+    set_index_checking,
+)
+
+__all__ = [
+    "KPError",
+    "LIB_PATH",
+    "aten",
+    "embedding",
+    "embedding_dense_backward",
+    "fused",
+    "index_checking",
+    "rms_norm",
+    "rms_norm_backward",
+    "rope",
+    "set_index_checking",
+    "version",
+]

@@ -1,0 +1,665 @@
+// RMSNorm forward / backward for gfx950.
+//
+// Layout: row-major bf16 [M, N], unit stride along N.  A row is processed by
+// WPR wave64s, each owning a contiguous segment of 512*VPL columns; lane l of
+// a wave holds the 8-element chunks at column offsets (v*64 + l)*8, v < VPL,
+// so every load/store instruction of the wave moves 1 KiB of consecutive
+// bytes.  Row sums are wave DPP trees (kp::wave_sum); the WPR > 1 case
+// combines the per-wave sums through 32 bytes of LDS in a fixed order.
+//
+// Backward weight gradient: each block accumulates its rows' dy * xhat
+// contributions in registers (per lane, per column), combines its waves in
+// LDS in wave order and writes one fp32 partial row; a second small kernel
+// sums the partial rows in a fixed order.  No float atomics anywhere, so
+// results are bitwise reproducible for a given device and shape.
+#include <stdlib.h>
+
+#include "kp_common.hpp"
+#include "kp_internal.hpp"
+
+namespace kp {
+namespace {
+
+constexpr int kThreads = 256;  // 4 waves per block
+
+struct RmsFwdArgs {
+  const uint16_t* x[3];
+  int64_t xs[3];
+  int n_x;
+  const uint16_t* w;
+  int64_t w_seg_len, w_seg_stride;
+  uint16_t* h;
+  int64_t hs;
+  uint16_t* y;
+  int64_t ys;
+  float* rstd;
+  int64_t M, N;
+  float eps;
+};
+
+struct RmsBwdArgs {
+  const uint16_t* dy[3];
+  int64_t dys[3];
+  int n_dy;
+  const uint16_t* x[3];
+  int64_t xs[3];
+  int n_x;
+  const float* rstd;
+  const uint16_t* w;
+  int64_t w_seg_len, w_seg_stride;
+  const uint16_t* dxr;
+  int64_t dxrs;
+  uint16_t* dx;
+  int64_t dxs;
+  float* partial;  // [gridDim.x, N] fp32, or nullptr when no weight gradient is wanted
+  int64_t M, N;
+  float eps;
+};
+
+__device__ __forceinline__ int64_t w_index(int64_t c, int64_t seg_len, int64_t seg_stride) {
+  return (c / seg_len) * seg_stride + (c % seg_len);
+}
+
+// Loads VPL chunks of the bf16 running sum of up to three row terms.
+template <int VPL>
+__device__ __forceinline__ void load_terms(u32x4 (&v)[VPL], const uint16_t* const* base, const int64_t* strides,
+                                           int n, int64_t row, int64_t col) {
+  const uint16_t* p0 = base[0] + row * strides[0] + col;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) v[i] = ld16(p0 + i * 512);
+  if (n > 1) {
+    const uint16_t* p1 = base[1] + row * strides[1] + col;
+    u32x4 t[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) t[i] = ld16(p1 + i * 512);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) v[i] = add_bf8(v[i], t[i]);
+    if (n > 2) {
+      const uint16_t* p2 = base[2] + row * strides[2] + col;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) t[i] = ld16(p2 + i * 512);
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) v[i] = add_bf8(v[i], t[i]);
+    }
+  }
+}
+
+template <int VPL>
+__device__ __forceinline__ void load_weight(u32x4 (&wv)[VPL], const uint16_t* w, int64_t seg_len, int64_t seg_stride,
+                                            int64_t col) {
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    if (w) {
+      wv[i] = ld16(w + w_index(col + i * 512, seg_len, seg_stride));
+    } else {
+      wv[i] = u32x4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u};  // bf16 1.0
+    }
+  }
+}
+
+// ------------------------------------------------------------------ forward
+template <int VPL, int WPR>
+__global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
+  constexpr int RB = 4 / WPR;
+  constexpr int SEG = 512 * VPL;
+  __shared__ float red[2][4];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % WPR, rloc = wave / WPR;
+  const int64_t col = (int64_t)part * SEG + lane * 8;
+
+  u32x4 wv[VPL];
+  load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
+
+  const int64_t ngroups = ceil_div_dev(a.M, RB);
+  int it = 0;
+  for (int64_t g = blockIdx.x; g < ngroups; g += gridDim.x, ++it) {
+    const int64_t row = g * RB + rloc;
+    const bool valid = row < a.M;
+    u32x4 hv[VPL];
+    if (valid) {
+      load_terms<VPL>(hv, a.x, a.xs, a.n_x, row, col);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) hv[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float f[8];
+      unpack8(hv[i], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+    }
+    ss = wave_sum(ss);
+    if constexpr (WPR > 1) {
+      if (lane == 0) red[it & 1][wave] = ss;
+      __syncthreads();
+      float t = 0.f;
+#pragma unroll
+      for (int p = 0; p < WPR; ++p) t += red[it & 1][rloc * WPR + p];
+      ss = t;
+    }
+    const float r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
+    if (valid) {
+      uint16_t* yrow = a.y + row * a.ys + col;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        float f[8], wf[8], o[8];
+        unpack8(hv[i], f);
+        unpack8(wv[i], wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (f[e] * r) * wf[e];
+        st16(yrow + i * 512, pack8(o));
+      }
+      if (a.h != nullptr && a.n_x > 1) {
+        uint16_t* hrow = a.h + row * a.hs + col;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) st16(hrow + i * 512, hv[i]);
+      }
+      if (a.rstd != nullptr && part == 0 && lane == 0) a.rstd[row] = r;
+    }
+  }
+}
+
+// Any N, any alignment: one block per row, scalar accesses, two passes.
+__device__ __forceinline__ float term_sum_scalar(const uint16_t* const* base, const int64_t* strides, int n,
+                                                 int64_t row, int64_t c) {
+  float v = bf_to_f(base[0][row * strides[0] + c]);
+  if (n > 1) v = round_bf(v + bf_to_f(base[1][row * strides[1] + c]));
+  if (n > 2) v = round_bf(v + bf_to_f(base[2][row * strides[2] + c]));
+  return v;
+}
+
+__device__ __forceinline__ float block_sum(float v, float* red4) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  v = wave_sum(v);
+  __syncthreads();  // red4 may still be read from the previous call
+  if (lane == 0) red4[wave] = v;
+  __syncthreads();
+  return (red4[0] + red4[1]) + (red4[2] + red4[3]);
+}
+
+__global__ __launch_bounds__(kThreads) void rms_fwd_generic(RmsFwdArgs a) {
+  __shared__ float red[4];
+  for (int64_t row = blockIdx.x; row < a.M; row += gridDim.x) {
+    float ss = 0.f;
+    for (int64_t c = threadIdx.x; c < a.N; c += kThreads) {
+      const float v = term_sum_scalar(a.x, a.xs, a.n_x, row, c);
+      ss = fmaf(v, v, ss);
+    }
+    ss = block_sum(ss, red);
+    const float r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
+    for (int64_t c = threadIdx.x; c < a.N; c += kThreads) {
+      const float v = term_sum_scalar(a.x, a.xs, a.n_x, row, c);
+      const float wf = a.w ? bf_to_f(a.w[w_index(c, a.w_seg_len, a.w_seg_stride)]) : 1.0f;
+      a.y[row * a.ys + c] = f_to_bf((v * r) * wf);
+      if (a.h != nullptr && a.n_x > 1) a.h[row * a.hs + c] = f_to_bf(v);
+    }
+    if (a.rstd != nullptr && threadIdx.x == 0) a.rstd[row] = r;
+  }
+}
+
+// ----------------------------------------------------------------- backward
+// LDS image of one wave's per-column accumulators, same column layout as the row.
+template <int VPL>
+__device__ __forceinline__ void stash_acc(float* buf, int lane, const float (&acc)[VPL * 8]) {
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    *reinterpret_cast<f32x4*>(buf + i * 512 + lane * 8) = f32x4{acc[i * 8], acc[i * 8 + 1], acc[i * 8 + 2], acc[i * 8 + 3]};
+    *reinterpret_cast<f32x4*>(buf + i * 512 + lane * 8 + 4) =
+        f32x4{acc[i * 8 + 4], acc[i * 8 + 5], acc[i * 8 + 6], acc[i * 8 + 7]};
+  }
+}
+template <int VPL>
+__device__ __forceinline__ void add_acc(const float* buf, int lane, float (&acc)[VPL * 8]) {
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    const f32x4 u = *reinterpret_cast<const f32x4*>(buf + i * 512 + lane * 8);
+    const f32x4 v = *reinterpret_cast<const f32x4*>(buf + i * 512 + lane * 8 + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc[i * 8 + e] += u[e];
+      acc[i * 8 + 4 + e] += v[e];
+    }
+  }
+}
+
+template <int VPL, int WPR>
+__global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
+  constexpr int RB = 4 / WPR;
+  constexpr int SEG = 512 * VPL;
+  extern __shared__ float smem[];  // [2][SEG] weight-gradient combine (only when a.partial)
+  __shared__ float red[2][4][2];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int part = wave % WPR, rloc = wave / WPR;
+  const int64_t col = (int64_t)part * SEG + lane * 8;
+
+  u32x4 wv[VPL];
+  load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
+
+  float acc[VPL * 8];
+#pragma unroll
+  for (int i = 0; i < VPL * 8; ++i) acc[i] = 0.f;
+
+  const float inv_n = 1.0f / (float)a.N;
+  const int64_t ngroups = ceil_div_dev(a.M, RB);
+  int it = 0;
+  for (int64_t g = blockIdx.x; g < ngroups; g += gridDim.x, ++it) {
+    const int64_t row = g * RB + rloc;
+    const bool valid = row < a.M;
+    u32x4 xv[VPL], dv[VPL];
+    if (valid) {
+      load_terms<VPL>(xv, a.x, a.xs, a.n_x, row, col);
+      load_terms<VPL>(dv, a.dy, a.dys, a.n_dy, row, col);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) xv[i] = dv[i] = u32x4{0u, 0u, 0u, 0u};
+    }
+    // sum(x * g) and, when rstd is not supplied, sum(x^2), in one sweep.
+    float sxg = 0.f, ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float xf[8], df[8], wf[8];
+      unpack8(xv[i], xf);
+      unpack8(dv[i], df);
+      unpack8(wv[i], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        sxg = fmaf(xf[e], df[e] * wf[e], sxg);
+        ss = fmaf(xf[e], xf[e], ss);
+      }
+    }
+    sxg = wave_sum(sxg);
+    if (a.rstd == nullptr) ss = wave_sum(ss);
+    if constexpr (WPR > 1) {
+      if (lane == 0) {
+        red[it & 1][wave][0] = sxg;
+        red[it & 1][wave][1] = ss;
+      }
+      __syncthreads();
+      float t0 = 0.f, t1 = 0.f;
+#pragma unroll
+      for (int p = 0; p < WPR; ++p) {
+        t0 += red[it & 1][rloc * WPR + p][0];
+        t1 += red[it & 1][rloc * WPR + p][1];
+      }
+      sxg = t0;
+      ss = t1;
+    }
+    float r;
+    if (a.rstd != nullptr) {
+      r = valid ? a.rstd[row] : 0.f;
+    } else {
+      r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
+    }
+    // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
+    const float cN = (r * sxg) * inv_n;
+    if (valid) {
+      uint16_t* dxrow = a.dx + row * a.dxs + col;
+      const uint16_t* rrow = a.dxr ? a.dxr + row * a.dxrs + col : nullptr;
+      u32x4 rv[VPL];
+      if (rrow) {
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) rv[i] = ld16(rrow + i * 512);
+      }
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        float xf[8], df[8], wf[8], o[8];
+        unpack8(xv[i], xf);
+        unpack8(dv[i], df);
+        unpack8(wv[i], wf);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float xh = xf[e] * r;
+          const float gg = df[e] * wf[e];
+          o[e] = (gg - xh * cN) * r;
+          acc[i * 8 + e] = fmaf(df[e], xh, acc[i * 8 + e]);
+        }
+        u32x4 ov = pack8(o);
+        if (rrow) ov = add_bf8(rv[i], ov);
+        st16(dxrow + i * 512, ov);
+      }
+    }
+  }
+
+  if (a.partial == nullptr) return;
+  // Combine the column partials of the waves that share a column segment
+  // (fixed order: ((w0 + w2) + (w1 + w3)) for WPR 1, (w0 + w2) / (w1 + w3) for
+  // WPR 2) through at most 2*SEG floats of LDS, then write one partial row.
+  if constexpr (RB >= 2) {
+    if (wave >= 2) stash_acc<VPL>(smem + (wave - 2) * SEG, lane, acc);
+    __syncthreads();
+    if (wave < 2) add_acc<VPL>(smem + wave * SEG, lane, acc);
+  }
+  if constexpr (RB == 4) {
+    __syncthreads();
+    if (wave == 1) stash_acc<VPL>(smem, lane, acc);
+    __syncthreads();
+    if (wave == 0) add_acc<VPL>(smem, lane, acc);
+  }
+  if (wave < WPR) {
+    float* prow = a.partial + (int64_t)blockIdx.x * a.N + col;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      *reinterpret_cast<f32x4*>(prow + i * 512) = f32x4{acc[i * 8], acc[i * 8 + 1], acc[i * 8 + 2], acc[i * 8 + 3]};
+      *reinterpret_cast<f32x4*>(prow + i * 512 + 4) = f32x4{acc[i * 8 + 4], acc[i * 8 + 5], acc[i * 8 + 6], acc[i * 8 + 7]};
+    }
+  }
+}
+
+// Any N, any alignment: one block per row, scalar accesses.  The block's
+// weight-gradient partial row lives directly in `partial` (read-modify-write,
+// owned by this block only).
+__global__ __launch_bounds__(kThreads) void rms_bwd_generic(RmsBwdArgs a) {
+  __shared__ float red[4];
+  float* prow = a.partial ? a.partial + (int64_t)blockIdx.x * a.N : nullptr;
+  if (prow)
+    for (int64_t c = threadIdx.x; c < a.N; c += kThreads) prow[c] = 0.f;
+  const float inv_n = 1.0f / (float)a.N;
+  for (int64_t row = blockIdx.x; row < a.M; row += gridDim.x) {
+    float sxg = 0.f, ss = 0.f;
+    for (int64_t c = threadIdx.x; c < a.N; c += kThreads) {
+      const float xf = term_sum_scalar(a.x, a.xs, a.n_x, row, c);
+      const float df = term_sum_scalar(a.dy, a.dys, a.n_dy, row, c);
+      const float wf = a.w ? bf_to_f(a.w[w_index(c, a.w_seg_len, a.w_seg_stride)]) : 1.0f;
+      sxg = fmaf(xf, df * wf, sxg);
+      ss = fmaf(xf, xf, ss);
+    }
+    sxg = block_sum(sxg, red);
+    float r;
+    if (a.rstd != nullptr) {
+      r = a.rstd[row];
+    } else {
+      ss = block_sum(ss, red);
+      r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
+    }
+    const float cN = (r * sxg) * inv_n;
+    for (int64_t c = threadIdx.x; c < a.N; c += kThreads) {
+      const float xf = term_sum_scalar(a.x, a.xs, a.n_x, row, c);
+      const float df = term_sum_scalar(a.dy, a.dys, a.n_dy, row, c);
+      const float wf = a.w ? bf_to_f(a.w[w_index(c, a.w_seg_len, a.w_seg_stride)]) : 1.0f;
+      const float xh = xf * r;
+      float o = round_bf((df * wf - xh * cN) * r);
+      if (a.dxr) o = bf_to_f(a.dxr[row * a.dxrs + c]) + o;
+      a.dx[row * a.dxs + c] = f_to_bf(o);
+      if (prow) prow[c] = fmaf(df, xh, prow[c]);
+    }
+  }
+}
+
+// dw[c] = sum_{p < P} partial[p, c].  Block = 64 columns x 16 row groups; row
+// group q sums rows [q*P/16, (q+1)*P/16) in order, then the 16 group sums are
+// added in group order.
+__global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restrict__ partial, int P, int64_t N,
+                                                            float* dw_f32, uint16_t* dw_bf16, int round_f32) {
+  __shared__ float s[16][64];
+  const int cq = threadIdx.x & 15, q = threadIdx.x >> 4;
+  const int64_t c0 = (int64_t)blockIdx.x * 64 + cq * 4;
+  const int p0 = (int)(((int64_t)P * q) / 16), p1 = (int)(((int64_t)P * (q + 1)) / 16);
+  f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if ((N & 3) == 0) {
+    if (c0 < N) {
+      for (int p = p0; p < p1; ++p) acc += *reinterpret_cast<const f32x4*>(partial + (int64_t)p * N + c0);
+    }
+  } else {
+    for (int k = 0; k < 4; ++k) {
+      if (c0 + k < N) {
+        float t = 0.f;
+        for (int p = p0; p < p1; ++p) t += partial[(int64_t)p * N + c0 + k];
+        acc[k] = t;
+      }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 4; ++k) s[q][cq * 4 + k] = acc[k];
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int64_t c = (int64_t)blockIdx.x * 64 + threadIdx.x;
+    if (c < N) {
+      float t = s[0][threadIdx.x];
+#pragma unroll
+      for (int g = 1; g < 16; ++g) t += s[g][threadIdx.x];
+      if (dw_bf16) dw_bf16[c] = f_to_bf(t);
+      if (dw_f32) dw_f32[c] = round_f32 ? round_bf(t) : t;
+    }
+  }
+}
+
+// ------------------------------------------------------------------- dispatch
+// Fast path shape: N = 512 * VPL * WPR with WPR in {1, 2, 4}.  Fewer chunks
+// per lane (VPL <= 4, at most ~120 VGPRs) keep 4 waves per SIMD resident; a
+// wider row is split over more waves instead.  VPL up to 8 is the fallback.
+int vpl_limit() {
+  static const int lim = [] {
+    const char* e = getenv("KP_RMS_VPL_MAX");
+    const int v = e ? atoi(e) : 4;
+    return (v >= 1 && v <= 8) ? v : 4;
+  }();
+  return lim;
+}
+bool pick_vec(int64_t N, int* vpl, int* wpr) {
+  if (N <= 0 || N % 512 != 0) return false;
+  const int64_t k = N / 512;
+  for (int vmax : {vpl_limit(), 8}) {
+    for (int w : {1, 2, 4}) {
+      if (k % w == 0 && k / w <= vmax) {
+        *vpl = (int)(k / w);
+        *wpr = w;
+        return true;
+      }
+    }
+  }
+  return false;
+}
+
+typedef void (*FwdKernel)(RmsFwdArgs);
+typedef void (*BwdKernel)(RmsBwdArgs);
+
+template <int WPR>
+FwdKernel fwd_kernel_for(int vpl) {
+  switch (vpl) {
+    case 1: return rms_fwd_vec<1, WPR>;
+    case 2: return rms_fwd_vec<2, WPR>;
+    case 3: return rms_fwd_vec<3, WPR>;
+    case 4: return rms_fwd_vec<4, WPR>;
+    case 5: return rms_fwd_vec<5, WPR>;
+    case 6: return rms_fwd_vec<6, WPR>;
+    case 7: return rms_fwd_vec<7, WPR>;
+    case 8: return rms_fwd_vec<8, WPR>;
+  }
+  return nullptr;
+}
+template <int WPR>
+BwdKernel bwd_kernel_for(int vpl) {
+  switch (vpl) {
+    case 1: return rms_bwd_vec<1, WPR>;
+    case 2: return rms_bwd_vec<2, WPR>;
+    case 3: return rms_bwd_vec<3, WPR>;
+    case 4: return rms_bwd_vec<4, WPR>;
+    case 5: return rms_bwd_vec<5, WPR>;
+    case 6: return rms_bwd_vec<6, WPR>;
+    case 7: return rms_bwd_vec<7, WPR>;
+    case 8: return rms_bwd_vec<8, WPR>;
+  }
+  return nullptr;
+}
+FwdKernel fwd_kernel(int vpl, int wpr) {
+  return wpr == 1 ? fwd_kernel_for<1>(vpl) : wpr == 2 ? fwd_kernel_for<2>(vpl) : fwd_kernel_for<4>(vpl);
+}
+BwdKernel bwd_kernel(int vpl, int wpr) {
+  return wpr == 1 ? bwd_kernel_for<1>(vpl) : wpr == 2 ? bwd_kernel_for<2>(vpl) : bwd_kernel_for<4>(vpl);
+}
+
+bool rows_vec_ok(const void* const* p, const int64_t* s, int n) {
+  for (int i = 0; i < n; ++i)
+    if (!aligned16(p[i]) || (s[i] & 7) != 0) return false;
+  return true;
+}
+
+// Term pointers may be NULL only when there are no rows (empty tensors).
+int check_terms(const char* who, const char* name, const void* const* p, const int64_t* s, int n, int64_t M) {
+  if (p == nullptr || s == nullptr || n < 1 || n > 3) return fail(KP_EINVAL, "%s: %s needs 1..3 terms", who, name);
+  for (int i = 0; i < n; ++i) {
+    if (p[i] == nullptr && M > 0) return fail(KP_EINVAL, "%s: %s term %d is NULL", who, name, i);
+    if (s[i] < 0) return fail(KP_EINVAL, "%s: %s term %d has a negative row stride", who, name, i);
+  }
+  return KP_OK;
+}
+
+// Row blocks for the backward: a fixed number per CU so that the partial row
+// count (and hence the summation order) depends only on device and shape.
+int bwd_blocks(int64_t M, int rows_per_block_step) {
+  const int64_t groups = ceil_div(M, rows_per_block_step);
+  const int64_t want = (int64_t)cu_count() * 2;
+  return (int)(groups < want ? (groups > 0 ? groups : 1) : want);
+}
+
+}  // namespace
+}  // namespace kp
+
+using namespace kp;
+
+extern "C" {
+
+int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, int n_x, const void* weight,
+                        int64_t w_seg_len, int64_t w_seg_stride, void* h_out, int64_t h_stride, void* y,
+                        int64_t y_stride, float* rstd, int64_t M, int64_t N, float eps, void* stream) {
+  static const char* who = "kp_rmsnorm_fwd_bf16";
+  int st = check_terms(who, "x", x_terms, x_strides, n_x, M);
+  if (st != KP_OK) return st;
+  if (M < 0 || N <= 0) return fail(KP_EINVAL, "%s: need M >= 0 and N > 0 (M=%lld N=%lld)", who, (long long)M, (long long)N);
+  if ((y == nullptr && M > 0) || y_stride < 0) return fail(KP_EINVAL, "%s: y is NULL or has a negative stride", who);
+  if (weight != nullptr && (w_seg_len <= 0 || w_seg_stride < 0))
+    return fail(KP_EINVAL, "%s: weight segment length must be > 0", who);
+  if (M == 0) return KP_OK;
+
+  RmsFwdArgs a{};
+  for (int i = 0; i < n_x; ++i) {
+    a.x[i] = static_cast<const uint16_t*>(x_terms[i]);
+    a.xs[i] = x_strides[i];
+  }
+  a.n_x = n_x;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.w_seg_len = weight ? w_seg_len : N;
+  a.w_seg_stride = weight ? w_seg_stride : N;
+  a.h = static_cast<uint16_t*>(h_out);
+  a.hs = h_stride;
+  a.y = static_cast<uint16_t*>(y);
+  a.ys = y_stride;
+  a.rstd = rstd;
+  a.M = M;
+  a.N = N;
+  a.eps = eps;
+
+  int vpl = 0, wpr = 0;
+  bool vec = pick_vec(N, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) && aligned16(y) && (y_stride & 7) == 0;
+  if (vec && h_out) vec = aligned16(h_out) && (h_stride & 7) == 0;
+  if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
+  hipStream_t s = as_stream(stream);
+  if (vec) {
+    const int rb = 4 / wpr;
+    const int64_t groups = ceil_div(M, rb);
+    const int64_t cap = (int64_t)cu_count() * 8;
+    const int grid = (int)(groups < cap ? groups : cap);
+    void* args[] = {&a};
+    prof_begin(s);
+    (void)hipLaunchKernel(reinterpret_cast<const void*>(fwd_kernel(vpl, wpr)), dim3(grid), dim3(kThreads), args, 0, s);
+    prof_end(s);
+  } else {
+    const int64_t cap = (int64_t)cu_count() * 8;
+    const int grid = (int)(M < cap ? M : cap);
+    prof_begin(s);
+    hipLaunchKernelGGL(rms_fwd_generic, dim3(grid), dim3(kThreads), 0, s, a);
+    prof_end(s);
+  }
+  return check_launch(who);
+}
+
+size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return 16;
+  // Partial rows: at most one per row block; the block count never exceeds 2 per CU.
+  const int64_t blocks = (int64_t)cu_count() * 2;
+  const int64_t rows = M < blocks ? M : blocks;
+  return (size_t)(rows * N * (int64_t)sizeof(float));
+}
+
+int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy, const void* const* x_terms,
+                        const int64_t* x_strides, int n_x, const float* rstd, const void* weight, int64_t w_seg_len,
+                        int64_t w_seg_stride, const void* dx_residual, int64_t dxr_stride, void* dx,
+                        int64_t dx_stride, float* dw_f32, void* dw_bf16, int dw_f32_round_bf16, int64_t M, int64_t N,
+                        float eps, void* workspace, size_t workspace_bytes, void* stream) {
+  static const char* who = "kp_rmsnorm_bwd_bf16";
+  int st = check_terms(who, "dy", dy_terms, dy_strides, n_dy, M);
+  if (st != KP_OK) return st;
+  st = check_terms(who, "x", x_terms, x_strides, n_x, M);
+  if (st != KP_OK) return st;
+  if (M < 0 || N <= 0) return fail(KP_EINVAL, "%s: need M >= 0 and N > 0 (M=%lld N=%lld)", who, (long long)M, (long long)N);
+  if ((dx == nullptr && M > 0) || dx_stride < 0) return fail(KP_EINVAL, "%s: dx is NULL or has a negative stride", who);
+  if (dx_residual != nullptr && dxr_stride < 0) return fail(KP_EINVAL, "%s: negative dx_residual stride", who);
+  const bool want_dw = dw_f32 != nullptr || dw_bf16 != nullptr;
+  if (want_dw && weight == nullptr) return fail(KP_EINVAL, "%s: a weight gradient needs a weight", who);
+  if (weight != nullptr && (w_seg_len <= 0 || w_seg_stride < 0))
+    return fail(KP_EINVAL, "%s: weight segment length must be > 0", who);
+  const size_t need = kp_rmsnorm_bwd_workspace_size(M, N);
+  if (want_dw && M > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+    return fail(KP_EWORKSPACE, "%s: workspace needs %zu bytes, 16-byte aligned (got %zu)", who, need, workspace_bytes);
+
+  hipStream_t s = as_stream(stream);
+  RmsBwdArgs a{};
+  for (int i = 0; i < n_dy; ++i) {
+    a.dy[i] = static_cast<const uint16_t*>(dy_terms[i]);
+    a.dys[i] = dy_strides[i];
+  }
+  a.n_dy = n_dy;
+  for (int i = 0; i < n_x; ++i) {
+    a.x[i] = static_cast<const uint16_t*>(x_terms[i]);
+    a.xs[i] = x_strides[i];
+  }
+  a.n_x = n_x;
+  a.rstd = rstd;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.w_seg_len = weight ? w_seg_len : N;
+  a.w_seg_stride = weight ? w_seg_stride : N;
+  a.dxr = static_cast<const uint16_t*>(dx_residual);
+  a.dxrs = dxr_stride;
+  a.dx = static_cast<uint16_t*>(dx);
+  a.dxs = dx_stride;
+  a.partial = want_dw ? static_cast<float*>(workspace) : nullptr;
+  a.M = M;
+  a.N = N;
+  a.eps = eps;
+
+  int blocks = 0;
+  if (M > 0) {
+    int vpl = 0, wpr = 0;
+    bool vec = pick_vec(N, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) &&
+               rows_vec_ok(dy_terms, dy_strides, n_dy) && aligned16(dx) && (dx_stride & 7) == 0;
+    if (vec && dx_residual) vec = aligned16(dx_residual) && (dxr_stride & 7) == 0;
+    if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
+    if (vec) {
+      blocks = bwd_blocks(M, 4 / wpr);
+      const size_t lds = (want_dw && wpr < 4) ? (size_t)2 * 512 * vpl * sizeof(float) : 0;
+      void* args[] = {&a};
+      prof_begin(s);
+      (void)hipLaunchKernel(reinterpret_cast<const void*>(bwd_kernel(vpl, wpr)), dim3(blocks), dim3(kThreads), args,
+                            lds, s);
+      prof_end(s);
+    } else {
+      blocks = bwd_blocks(M, 1);
+      prof_begin(s);
+      hipLaunchKernelGGL(rms_bwd_generic, dim3(blocks), dim3(kThreads), 0, s, a);
+      prof_end(s);
+    }
+    st = check_launch(who);
+    if (st != KP_OK) return st;
+  }
+  if (want_dw) {
+    hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, 64)), dim3(kThreads), 0, s,
+                       static_cast<const float*>(workspace), blocks, N, dw_f32, static_cast<uint16_t*>(dw_bf16),
+                       dw_f32_round_bf16);
+    st = check_launch(who);
+  }
+  return st;
+}
+
+}  // extern "C"

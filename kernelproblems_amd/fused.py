@@ -1,0 +1,388 @@
+"""Tensor-level entry points over the C ABI: the fused hot-path operations.
+
+Each function validates its tensors (device, dtype, shapes), allocates the
+outputs and any workspace with torch's caching allocator, and enqueues the
+HIP kernels on the current stream of the input's device.  Nothing here
+computes on the CPU and nothing falls back to torch ops: a CPU tensor, an
+unsupported dtype or a missing library raises.
+
+The aten-compatible drop-ins (``kernelproblems_amd.aten``) and the
+per-fragment ``kernel_function``s (``kernelproblems_amd.fragments``) are
+thin compositions of these.
+"""
+from __future__ import annotations
+
+import math
+import os
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib as L
+
+_index_checking = os.environ.get("KP_CHECK_INDICES", "0") not in ("", "0")
+
+
+def set_index_checking(enabled: bool) -> None:
+    """When enabled, index-taking ops synchronise after the launch and raise
+    IndexError if an id/position was out of range (the kernels never read out
+    of bounds; unchecked, such rows come out as zeros)."""
+    global _index_checking
+    _index_checking = bool(enabled)
+
+
+def index_checking() -> bool:
+    return _index_checking
+
+
+# ---------------------------------------------------------------- helpers
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _need_gpu(name: str, t: torch.Tensor, dtype: Optional[torch.dtype] = torch.bfloat16) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name}: expected a GPU tensor, got device {t.device} (no CPU path exists)")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
+
+
+def _as_rows(t: torch.Tensor, n: int):
+    """Returns (tensor, row_stride, rows) for t viewed as [rows, n] with unit
+    inner stride; copies to contiguous only if no such view exists."""
+    if t.numel() % n != 0:
+        raise RuntimeError(f"tensor of {t.numel()} elements is not a whole number of rows of {n}")
+    m = t.numel() // n
+    if m == 0:
+        return t, n, 0
+    try:
+        v = t.view(m, n)
+        if n == 1 or v.stride(1) == 1:
+            return t, v.stride(0), m
+    except RuntimeError:
+        pass
+    t = t.contiguous()
+    return t, n, m
+
+
+def _weight_segments(w: torch.Tensor, n: int):
+    """(tensor, seg_len, seg_stride): element i of the flattened weight sits at
+    (i // seg_len) * seg_stride + i % seg_len.  Covers contiguous vectors and
+    2-D row-strided views such as an [8, 512] slice of an FSDP flat buffer."""
+    if w.numel() != n:
+        raise RuntimeError(f"weight has {w.numel()} elements, expected {n}")
+    if w.dim() == 1 and (w.stride(0) == 1 or n == 1):
+        return w, n, n
+    if w.dim() == 2 and (w.stride(1) == 1 or w.shape[1] == 1):
+        return w, w.shape[1], w.stride(0)
+    if w.is_contiguous():
+        return w, n, n
+    w = w.contiguous()
+    return w, n, n
+
+
+def _flag(device: torch.device):
+    """A zeroed int32 error flag when index checking is on, else None."""
+    if not _index_checking:
+        return None
+    return torch.zeros(1, dtype=torch.int32, device=device)
+
+
+def _raise_if_flagged(flag, what: str) -> None:
+    if flag is not None and int(flag.item()) != 0:
+        raise IndexError(f"{what}: index out of range")
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+# ---------------------------------------------------------------- RMSNorm
+def rms_norm(
+    x_terms: Sequence[torch.Tensor],
+    weight: Optional[torch.Tensor],
+    eps: float,
+    n: int,
+    *,
+    return_h: bool = False,
+    return_rstd: bool = True,
+):
+    """Fused (residual add +) RMSNorm forward.
+
+    h = bf16 running sum of x_terms (eager bf16 add.Tensor rounding), y =
+    bf16(h * rstd * w), rstd = 1/sqrt(mean(h^2) + eps) over the trailing n
+    elements.  Returns (h or None, y, rstd[M] or None); y has x_terms[0]'s shape.
+    """
+    if not 1 <= len(x_terms) <= 3:
+        raise RuntimeError("rms_norm: 1..3 input terms")
+    x0 = x_terms[0]
+    _need_gpu("rms_norm input", x0)
+    shape, dev = x0.shape, x0.device
+    rows, strides, m = [], [], None
+    for i, t in enumerate(x_terms):
+        _need_gpu(f"rms_norm input {i}", t)
+        if t.numel() != x0.numel() or t.device != dev:
+            raise RuntimeError("rms_norm: input terms must have the same number of elements and device")
+        tt, rs, mm = _as_rows(t, n)
+        rows.append(tt)
+        strides.append(rs)
+        m = mm
+    w_t, seg_len, seg_stride = (None, n, n)
+    if weight is not None:
+        _need_gpu("rms_norm weight", weight)
+        w_t, seg_len, seg_stride = _weight_segments(weight, n)
+    y = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(shape, dtype=torch.bfloat16, device=dev) if (return_h and len(x_terms) > 1) else None
+    rstd = torch.empty(m, dtype=torch.float32, device=dev) if return_rstd else None
+    L.call(
+        "kp_rmsnorm_fwd_bf16",
+        L.ptr_array([t.data_ptr() for t in rows]), L.i64_array(strides), len(rows),
+        _ptr(w_t), seg_len, seg_stride,
+        _ptr(h), n, y.data_ptr(), n, _ptr(rstd),
+        m, n, float(eps), _stream(dev),
+    )
+    if return_h and h is None:
+        h = x0
+    return h, y, rstd
+
+
+def rms_norm_backward(
+    dy_terms: Sequence[torch.Tensor],
+    x_terms: Sequence[torch.Tensor],
+    rstd: Optional[torch.Tensor],
+    weight: Optional[torch.Tensor],
+    eps: float,
+    n: int,
+    *,
+    dx_residual: Optional[torch.Tensor] = None,
+    want_dx: bool = True,
+    dw: Optional[str] = "f32",
+):
+    """Fused RMSNorm backward.
+
+    dy / x are bf16 running sums of their terms; rstd (fp32, M values) is
+    recomputed from x with eps when None.  dx = bf16(dx_residual + bf16(dx))
+    when dx_residual is given.  ``dw`` selects the weight gradient: "f32"
+    (fp32 sum), "f32_bf16" (the reference's bf16 rounding widened to fp32),
+    "bf16", or None.  Returns (dx, dw).
+    """
+    dy0 = dy_terms[0]
+    _need_gpu("rms_norm_backward grad_out", dy0)
+    dev, shape = dy0.device, x_terms[0].shape
+    dyr, dys = [], []
+    m = None
+    for i, t in enumerate(dy_terms):
+        _need_gpu(f"rms_norm_backward grad term {i}", t)
+        if t.numel() != dy0.numel():
+            raise RuntimeError("rms_norm_backward: grad terms must have the same number of elements")
+        tt, rs, m = _as_rows(t, n)
+        dyr.append(tt)
+        dys.append(rs)
+    xr, xs = [], []
+    for i, t in enumerate(x_terms):
+        _need_gpu(f"rms_norm_backward input term {i}", t)
+        if t.numel() != dy0.numel():
+            raise RuntimeError("rms_norm_backward: input and grad must have the same number of elements")
+        tt, rs, _ = _as_rows(t, n)
+        xr.append(tt)
+        xs.append(rs)
+    rstd_t = None
+    if rstd is not None:
+        _need_gpu("rms_norm_backward rstd", rstd, torch.float32)
+        if rstd.numel() != m:
+            raise RuntimeError(f"rms_norm_backward: rstd has {rstd.numel()} values, expected {m}")
+        rstd_t = rstd.contiguous()
+    w_t, seg_len, seg_stride = (None, n, n)
+    if weight is not None:
+        _need_gpu("rms_norm_backward weight", weight)
+        w_t, seg_len, seg_stride = _weight_segments(weight, n)
+    res_t, res_s = None, n
+    if dx_residual is not None:
+        _need_gpu("rms_norm_backward residual", dx_residual)
+        res_t, res_s, _ = _as_rows(dx_residual, n)
+    dx = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    dw_f32 = dw_bf16 = None
+    if dw is not None:
+        if weight is None:
+            raise RuntimeError("rms_norm_backward: no weight, no weight gradient")
+        if dw in ("f32", "f32_bf16"):
+            dw_f32 = torch.empty(n, dtype=torch.float32, device=dev)
+        elif dw == "bf16":
+            dw_bf16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        else:
+            raise ValueError(f"rms_norm_backward: unknown dw mode {dw!r}")
+    ws_bytes = int(L.lib().kp_rmsnorm_bwd_workspace_size(m, n)) if dw is not None else 0
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev) if dw is not None else None
+    L.call(
+        "kp_rmsnorm_bwd_bf16",
+        L.ptr_array([t.data_ptr() for t in dyr]), L.i64_array(dys), len(dyr),
+        L.ptr_array([t.data_ptr() for t in xr]), L.i64_array(xs), len(xr),
+        _ptr(rstd_t), _ptr(w_t), seg_len, seg_stride,
+        _ptr(res_t), res_s, dx.data_ptr(), n,
+        _ptr(dw_f32), _ptr(dw_bf16), 1 if dw == "f32_bf16" else 0,
+        m, n, float(eps), _ptr(ws), ws_bytes, _stream(dev),
+    )
+    out_dw = dw_f32 if dw_f32 is not None else dw_bf16
+    if weight is not None and out_dw is not None:
+        out_dw = out_dw.view(weight.shape)
+    return (dx if want_dx else None), out_dw
+
+
+# ---------------------------------------------------------------- embedding
+def _index_info(indices: torch.Tensor):
+    if indices.device.type != "cuda":
+        raise RuntimeError(f"indices must be a GPU tensor, got {indices.device}")
+    if indices.dtype not in (torch.int64, torch.int32):
+        raise RuntimeError(f"indices must be int64 or int32, got {indices.dtype}")
+    idx = indices.contiguous()
+    return idx, idx.element_size()
+
+
+def embedding(table: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
+    """out[..., :] = table[indices[...], :] (bit copy), shape indices.shape + [D]."""
+    _need_gpu("embedding weight", table)
+    if table.dim() != 2:
+        raise RuntimeError("embedding: weight must be 2-D")
+    idx, ib = _index_info(indices)
+    V, D = table.shape
+    tt, trs, _ = _as_rows(table, D)
+    out = torch.empty((*indices.shape, D), dtype=torch.bfloat16, device=table.device)
+    flag = _flag(table.device)
+    L.call(
+        "kp_embedding_fwd_bf16",
+        tt.data_ptr(), V, D, trs, idx.data_ptr(), ib, idx.numel(), out.data_ptr(), D,
+        _ptr(flag), _stream(table.device),
+    )
+    _raise_if_flagged(flag, "embedding")
+    return out
+
+
+def embedding_dense_backward(
+    grad_output: torch.Tensor,
+    indices: torch.Tensor,
+    num_weights: int,
+    padding_idx: int = -1,
+    scale_grad_by_freq: bool = False,
+    *,
+    out_dtype: torch.dtype = torch.float32,
+    round_to_bf16: bool = False,
+) -> torch.Tensor:
+    """Dense [num_weights, D] gradient of an embedding, fp32 accumulation,
+    deterministic sort-and-segment, every row written once."""
+    _need_gpu("embedding_dense_backward grad_output", grad_output)
+    idx, ib = _index_info(indices)
+    T = idx.numel()
+    D = grad_output.shape[-1]
+    if grad_output.numel() != T * D:
+        raise RuntimeError(
+            f"embedding_dense_backward: grad_output {tuple(grad_output.shape)} does not match {T} indices")
+    g, grs, _ = _as_rows(grad_output, D)
+    if out_dtype == torch.float32:
+        code = L.KP_DTYPE_F32
+    elif out_dtype == torch.bfloat16:
+        code = L.KP_DTYPE_BF16
+    else:
+        raise RuntimeError(f"embedding_dense_backward: unsupported out_dtype {out_dtype}")
+    dev = grad_output.device
+    out = torch.empty((num_weights, D), dtype=out_dtype, device=dev)
+    ws_bytes = int(L.lib().kp_embedding_bwd_workspace_size(T, num_weights, D))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    flag = _flag(dev)
+    L.call(
+        "kp_embedding_bwd_bf16",
+        g.data_ptr(), grs, idx.data_ptr(), ib, T, num_weights, D,
+        -1 if padding_idx is None else int(padding_idx), 1 if scale_grad_by_freq else 0,
+        out.data_ptr(), code, 1 if round_to_bf16 else 0, ws.data_ptr(), ws_bytes,
+        _ptr(flag), _stream(dev),
+    )
+    _raise_if_flagged(flag, "embedding_dense_backward")
+    return out
+
+
+# ---------------------------------------------------------------- RoPE
+def _rope_strides(t: torch.Tensor):
+    if t.dim() != 4:
+        raise RuntimeError(f"rope: expected [B, S, H, D], got shape {tuple(t.shape)}")
+    if t.shape[3] > 1 and t.stride(3) != 1:
+        t = t.contiguous()
+    return t, [t.stride(0), t.stride(1), t.stride(2)]
+
+
+def rope(
+    q: torch.Tensor,
+    k: Optional[torch.Tensor] = None,
+    *,
+    positions: Optional[torch.Tensor] = None,
+    theta: Optional[float] = None,
+    freqs_cis: Optional[torch.Tensor] = None,
+    pairing: str = "half",
+    conj: bool = False,
+):
+    """Rotary embedding of q (and k) laid out [B, S, H, D] (unit stride on D).
+
+    Angles come from ``theta`` (inv_freq_i = theta^(-2i/D), angle =
+    fp32(pos * inv_freq_i), cos/sin evaluated in fp32 in-kernel) or from the
+    complex64 table ``freqs_cis`` whose last dim is D/2 (row p used for
+    position p).  positions: [B, S] or [S] integer tensor, default s.
+    pairing "half" = (i, i + D/2), "interleaved" = (2i, 2i+1).  conj=True
+    rotates by the conjugate (backward).  Returns contiguous (q_out, k_out).
+    """
+    _need_gpu("rope q", q)
+    dev = q.device
+    q, qs = _rope_strides(q)
+    B, S, Hq, D = q.shape
+    q_out = torch.empty((B, S, Hq, D), dtype=torch.bfloat16, device=dev)
+    k_out = None
+    k_args = [None, None, 0, None, None]
+    if k is not None:
+        _need_gpu("rope k", k)
+        k, ks = _rope_strides(k)
+        if k.shape[0] != B or k.shape[1] != S or k.shape[3] != D:
+            raise RuntimeError("rope: q and k must agree on B, S and D")
+        k_out = torch.empty(k.shape, dtype=torch.bfloat16, device=dev)
+        k_args = [k.data_ptr(), k_out.data_ptr(), k.shape[2], L.i64_array(ks),
+                  L.i64_array(list(k_out.stride()[:3]))]
+    pos_ptr, pos_bytes, psb, pss = None, 0, 0, 0
+    if positions is not None:
+        if positions.device != dev or positions.dtype not in (torch.int32, torch.int64):
+            raise RuntimeError("rope: positions must be an int32/int64 tensor on the same device")
+        if positions.dim() == 1:
+            if positions.shape[0] != S:
+                raise RuntimeError("rope: 1-D positions must have S entries")
+            psb, pss = 0, positions.stride(0)
+        elif positions.dim() == 2:
+            if positions.shape[1] != S or positions.shape[0] not in (1, B):
+                raise RuntimeError("rope: 2-D positions must be [B, S] or [1, S]")
+            psb = positions.stride(0) if positions.shape[0] == B else 0
+            pss = positions.stride(1)
+        else:
+            raise RuntimeError("rope: positions must be 1-D or 2-D")
+        pos_ptr, pos_bytes = positions.data_ptr(), positions.element_size()
+    mode = {"half": L.KP_ROPE_HALF, "interleaved": L.KP_ROPE_INTERLEAVED}.get(pairing)
+    if mode is None:
+        raise ValueError(f"rope: pairing must be 'half' or 'interleaved', got {pairing!r}")
+    f_ptr, frows, frs = None, 0, 0
+    th = 0.0
+    if freqs_cis is not None:
+        if freqs_cis.device != dev or freqs_cis.dtype != torch.complex64:
+            raise RuntimeError("rope: freqs_cis must be complex64 on the same device")
+        if freqs_cis.shape[-1] != D // 2:
+            raise RuntimeError(f"rope: freqs_cis last dim must be D/2={D // 2}")
+        fc, frs, frows = _as_rows(freqs_cis, D // 2)
+        f_ptr = torch.view_as_real(fc).data_ptr() if fc.numel() else fc.data_ptr()
+    else:
+        if theta is None or not (theta > 0) or not math.isfinite(theta):
+            raise RuntimeError("rope: need theta > 0 or freqs_cis")
+        th = float(theta)
+    flag = _flag(dev) if freqs_cis is not None else None
+    L.call(
+        "kp_rope_bf16",
+        q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(qs), L.i64_array(list(q_out.stride()[:3])),
+        *k_args,
+        B, S, D, pos_ptr, pos_bytes, psb, pss, mode, th, f_ptr, frows, frs, 1 if conj else 0,
+        _ptr(flag), _stream(dev),
+    )
+    _raise_if_flagged(flag, "rope")
+    return q_out, k_out

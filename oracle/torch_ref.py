@@ -1,0 +1,97 @@
+"""Torch eager restatement of the hot-path fragments -- TEST INFRASTRUCTURE ONLY.
+
+Each function restates, with torch eager ops, the aten op sequence of the
+reference fragment(s) it cites, for inputs on any device.  On a GPU this is
+the "reference torch eager fragment" (torch-ROCm kernels); on the CPU it is
+the reference CPU eager path that bench.py times as the cpu_baseline.
+
+``_fused_rms_norm_backward`` has no CPU kernel
+(torchgen/packaged/ATen/native/native_functions.yaml:3347-3349), so on the
+CPU the backward runs torch's own Python decomposition of that operator
+(torch/_decomp/decompositions.py:1815-1887).
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+from torch._decomp import decompositions as _dec
+
+aten = torch.ops.aten
+
+
+def _rms_bwd(dy, x, n, rstd, w):
+    if x.device.type == "cuda":
+        return aten._fused_rms_norm_backward.default(dy, x, [n], rstd, w, [True, True])
+    return _dec._fused_rms_norm_backward(dy, x, [n], rstd, w, [True, True])
+
+
+def rms_norm_fwd(x: torch.Tensor, w: torch.Tensor, eps: float):
+    """C1 / v7/59f786beb25f/problem.py:16-21: _fused_rms_norm -> (y, rstd)."""
+    return aten._fused_rms_norm.default(x, [x.shape[-1]], w, eps)
+
+
+def rms_norm_bwd(x: torch.Tensor, dy: torch.Tensor, w: torch.Tensor, eps: float):
+    """C2 / v7/45990c83cfd6/problem.py:17-28: rstd recomputed by the forward,
+    _fused_rms_norm_backward, weight gradient widened with _to_copy(f32)
+    (v8/d8f596b3df34/problem.py:41-44)."""
+    n = x.shape[-1]
+    _, rstd = aten._fused_rms_norm.default(x, [n], w, eps)
+    dx, dw = _rms_bwd(dy, x, n, rstd, w)
+    return dx, dw.to(torch.float32)
+
+
+def add_rms_norm_fwd(x: torch.Tensor, res: torch.Tensor, w: torch.Tensor, eps: float):
+    """C5 forward / v8/7884328a5557/problem.py:20-33: h = add.Tensor(res, x), y = rms(h)."""
+    h = aten.add.Tensor(res, x)
+    y, _ = aten._fused_rms_norm.default(h, [h.shape[-1]], w, eps)
+    return h, y
+
+
+def add_rms_norm_bwd(x: torch.Tensor, res: torch.Tensor, dy: torch.Tensor, w: torch.Tensor, eps: float):
+    """C5 backward / v8/3c6c589cdf81/problem.py:22-53: h recomputed from the
+    adds, rstd recomputed, backward, weight gradient to f32."""
+    h = aten.add.Tensor(res, x)
+    n = h.shape[-1]
+    _, rstd = aten._fused_rms_norm.default(h, [n], w, eps)
+    dx, dw = _rms_bwd(dy, h, n, rstd, w)
+    return dx, dw.to(torch.float32)
+
+
+def embedding_fwd(table: torch.Tensor, ids: torch.Tensor):
+    """C3 forward / v7/1e49beb8a123/problem.py:23."""
+    return aten.embedding.default(table, ids)
+
+
+def embedding_bwd(grad: torch.Tensor, ids: torch.Tensor, num_weights: int, padding_idx: int = -1):
+    """C3 backward / v7/a12a160cb11b/problem.py:16-20: embedding_dense_backward then _to_copy(f32)."""
+    g = aten.embedding_dense_backward.default(grad, ids, num_weights, padding_idx, False)
+    return aten._to_copy.default(g, dtype=torch.float32)
+
+
+def rope_half(q: torch.Tensor, k: torch.Tensor, positions: Optional[torch.Tensor], theta: float):
+    """C4: rotate-half RoPE, inv_freq = theta^(-2i/D) in fp32, angle = pos * inv_freq
+    in fp32, cos/sin in fp32, rotation in fp32, output cast to bf16."""
+    B, S, _, D = q.shape
+    dev = q.device
+    inv = (theta ** (-torch.arange(0, D, 2, dtype=torch.float64, device=dev) / D)).to(torch.float32)
+    pos = torch.arange(S, device=dev).expand(B, S) if positions is None else positions
+    ang = pos.to(torch.float32)[..., None] * inv  # [B, S, D/2]
+    cos = torch.cos(ang)[:, :, None, :]
+    sin = torch.sin(ang)[:, :, None, :]
+
+    def rot(x):
+        xf = x.to(torch.float32)
+        x1, x2 = xf[..., : D // 2], xf[..., D // 2:]
+        return torch.cat([x1 * cos - x2 * sin, x2 * cos + x1 * sin], dim=-1).to(torch.bfloat16)
+
+    return rot(q), rot(k)
+
+
+def rope_complex(x: torch.Tensor, freqs_cis: torch.Tensor):
+    """Interleaved complex RoPE as in v7/e29b92927600/problem.py:16-37:
+    _to_copy f32 -> view_as_complex -> mul(freqs_cis) -> view_as_real -> _to_copy bf16.
+    x: [B, S, H, D]; freqs_cis broadcastable to [B, S, 1, D/2]."""
+    B, S, H, D = x.shape
+    xc = torch.view_as_complex(x.to(torch.float32).reshape(B, S, H, D // 2, 2))
+    return torch.view_as_real(xc * freqs_cis).reshape(B, S, H, D).to(torch.bfloat16)

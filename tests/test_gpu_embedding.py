@@ -1,0 +1,142 @@
+"""GPU parity: embedding gather (bit-exact) and dense deterministic backward vs the C oracle."""
+import numpy as np
+import pytest
+import torch
+
+import kernelproblems_amd as kp
+from tests._util import bf, gen, randn_bf16, to_u16, zipf_ids
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("V,D,T", [(1000, 4096, 777), (50, 64, 300), (128256, 4096, 2048), (300, 100, 129)])
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+def test_embedding_fwd_bit_exact(gpu, oracle_lib, V, D, T, idx_dtype):
+    g = gen(V + D + T)
+    table = randn_bf16((V, D), g, 0.0, 0.02)
+    ids = zipf_ids(T, V, 1.1, g)
+    ids[0], ids[-1] = 0, V - 1  # first and last rows
+    out = kp.embedding(table.to(gpu), ids.to(idx_dtype).to(gpu))
+    exp, bad = oracle_lib.embedding_fwd(to_u16(table), ids.numpy())
+    assert bad == 0
+    assert out.shape == (T, D)
+    assert np.array_equal(to_u16(out).reshape(T, D), exp)
+
+
+def test_embedding_fwd_flat_buffer_view(gpu, oracle_lib):
+    """Table = [V, D] view of a flat FSDP buffer (v7/1e49beb8a123/problem.py:16-20), ids [1, T]."""
+    g = gen(9)
+    V, D = 4096, 1024
+    flat = randn_bf16(V * D, g, 0.0, 0.02)
+    ids = torch.randint(0, 100, (1, 512), generator=g)
+    out = kp.aten.embedding(flat.to(gpu).view(8, -1).view(V, D), ids.to(gpu))
+    exp, _ = oracle_lib.embedding_fwd(to_u16(flat).reshape(V, D), ids.numpy())
+    assert out.shape == (1, 512, D)
+    assert np.array_equal(to_u16(out).reshape(512, D), exp)
+
+
+def test_embedding_fwd_out_of_range_flagged(gpu):
+    table = torch.ones((10, 64), dtype=torch.bfloat16, device=gpu)
+    ids = torch.tensor([1, 10, 3], device=gpu)
+    with pytest.raises(IndexError):
+        kp.embedding(table, ids)
+
+
+def _check_bwd(gpu, O, V, D, ids, grad, padding_idx=-1, scale=False):
+    T = ids.numel()
+    out = kp.embedding_dense_backward(grad.to(gpu), ids.to(gpu), V, padding_idx, scale)
+    torch.cuda.synchronize()
+    rid, rows, absrows, counts, bad = O.embedding_bwd_rows(to_u16(grad), ids.numpy(), V, padding_idx, scale)
+    assert bad == 0
+    o = out.cpu().numpy().astype(np.float64)
+    touched = np.zeros(V, bool)
+    touched[rid] = True
+    # untouched rows (incl. padding) are exactly zero
+    assert not np.any(o[~touched]), "rows without contributions must be exactly 0"
+    # touched rows: fp32 summation error bound gamma_{n-1} * sum|x| plus the final fp32 rounding
+    got = o[rid]
+    u = 2.0 ** -24
+    n = counts[:, None].astype(np.float64)
+    bound = (n * u / (1 - n * u)) * absrows + u * np.abs(rows) + 1e-30
+    err = np.abs(got - rows)
+    assert np.all(err <= bound), f"max err/bound {np.max(err / bound):.3f}"
+    # column sums of the dense gradient equal the column sums of the contributing rows
+    return out
+
+
+@pytest.mark.parametrize("V,D,T", [(1000, 4096, 777), (64, 128, 4000), (5000, 512, 2048), (37, 100, 250)])
+def test_embedding_bwd_matches_oracle(gpu, oracle_lib, V, D, T):
+    g = gen(V * 3 + T)
+    ids = zipf_ids(T, V, 1.1, g)
+    grad = randn_bf16((T, D), g)
+    _check_bwd(gpu, oracle_lib, V, D, ids, grad)
+
+
+def test_embedding_bwd_hot_row_and_padding(gpu, oracle_lib):
+    g = gen(21)
+    V, D, T = 300, 256, 3000
+    ids = torch.randint(0, V, (T,), generator=g)
+    ids[::3] = 7  # one id with ~1000 contributions (many parts)
+    ids[1::5] = 5  # padding id
+    grad = randn_bf16((T, D), g)
+    out = _check_bwd(gpu, oracle_lib, V, D, ids, grad, padding_idx=5)
+    assert torch.count_nonzero(out[5]) == 0
+
+
+def test_embedding_bwd_scale_grad_by_freq(gpu, oracle_lib):
+    g = gen(22)
+    V, D, T = 200, 64, 1500
+    ids = zipf_ids(T, V, 1.1, g)
+    grad = randn_bf16((T, D), g)
+    _check_bwd(gpu, oracle_lib, V, D, ids, grad, scale=True)
+
+
+def test_embedding_bwd_all_same_id(gpu, oracle_lib):
+    g = gen(23)
+    V, D, T = 16, 512, 4096
+    ids = torch.full((T,), 3, dtype=torch.int64)
+    grad = randn_bf16((T, D), g)
+    _check_bwd(gpu, oracle_lib, V, D, ids, grad)
+
+
+def test_embedding_bwd_deterministic_and_dtypes(gpu):
+    g = gen(24)
+    V, D, T = 4000, 1024, 4096
+    ids = zipf_ids(T, V, 1.1, g).to(gpu)
+    grad = randn_bf16((T, D), g).to(gpu)
+    a = kp.embedding_dense_backward(grad, ids, V)
+    b = kp.embedding_dense_backward(grad, ids, V)
+    assert torch.equal(a, b)
+    r = kp.embedding_dense_backward(grad, ids, V, round_to_bf16=True)
+    assert torch.equal(r, a.to(torch.bfloat16).float())
+    h = kp.aten.embedding_dense_backward(grad, ids, V, -1, False)
+    assert h.dtype == torch.bfloat16 and torch.equal(h, a.to(torch.bfloat16))
+
+
+def test_embedding_bwd_vs_torch_eager(gpu, oracle_lib):
+    """torch-ROCm eager embedding_dense_backward (the reference op, bf16 output)
+    on the reference's own id distribution (randint(0, 100), v7/a12a160cb11b).
+    Eager rounds to bf16 between index batches, so it is the less accurate of
+    the two: ours must be at least as close to the exact sums everywhere, and
+    both must agree on which rows are untouched."""
+    g = gen(25)
+    V, D, T = 1000, 512, 2048
+    ids = torch.randint(0, 100, (1, T), generator=g)
+    grad = randn_bf16((1, T, D), g)
+    ref = torch.ops.aten.embedding_dense_backward.default(grad.to(gpu), ids.to(gpu), V, -1, False)
+    out = kp.embedding_dense_backward(grad.to(gpu), ids.to(gpu), V, -1, False)
+    exact = np.zeros((V, D))
+    rid, rows, _, _, _ = oracle_lib.embedding_bwd_rows(to_u16(grad), ids.numpy(), V)
+    exact[rid] = rows
+    o = out.cpu().numpy().astype(np.float64)
+    r = ref.float().cpu().numpy().astype(np.float64)
+    untouched = np.ones(V, bool)
+    untouched[rid] = False
+    assert not np.any(r[untouched]) and not np.any(o[untouched])
+    assert np.all(np.abs(o - exact) <= np.abs(r - exact) + 2.0 ** -20 * np.abs(exact) + 1e-6)
+
+
+def test_embedding_bwd_empty(gpu):
+    out = kp.embedding_dense_backward(torch.empty((0, 64), dtype=torch.bfloat16, device=gpu),
+                                      torch.empty(0, dtype=torch.int64, device=gpu), 10)
+    assert out.shape == (10, 64) and torch.count_nonzero(out) == 0

@@ -1,0 +1,75 @@
+"""GPU parity: RoPE (rotate-half and interleaved; theta and table angles) vs the C oracle."""
+import numpy as np
+import pytest
+import torch
+
+import kernelproblems_amd as kp
+from tests._util import assert_bf16_close, gen, randn_bf16, to_u16
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("pairing", ["half", "interleaved"])
+@pytest.mark.parametrize("B,S,Hq,Hk,D", [(2, 64, 32, 8, 128), (1, 33, 4, 2, 64), (1, 16, 3, 1, 96)])
+@pytest.mark.parametrize("conj", [False, True])
+def test_rope_theta_matches_oracle(gpu, oracle_lib, pairing, B, S, Hq, Hk, D, conj):
+    g = gen(B * S + Hq + D)
+    q = randn_bf16((B, S, Hq, D), g)
+    k = randn_bf16((B, S, Hk, D), g)
+    pos = (torch.arange(S) * 61 % 4096).repeat(B, 1)  # large angles
+    qo, ko = kp.rope(q.to(gpu), k.to(gpu), positions=pos.to(gpu), theta=500000.0, pairing=pairing, conj=conj)
+    torch.cuda.synchronize()
+    eq = oracle_lib.rope(to_u16(q), pos.numpy(), pairing=pairing, theta=500000.0, conj=conj)
+    ek = oracle_lib.rope(to_u16(k), pos.numpy(), pairing=pairing, theta=500000.0, conj=conj)
+    # |x| <= ~5: fp32 evaluation error of x_a*c - x_b*s is below 4e-6 absolute
+    assert_bf16_close(to_u16(qo), eq, what="q", max_ulp=1, min_exact=0.99, ulp_abs_slack=4e-6)
+    assert_bf16_close(to_u16(ko), ek, what="k", max_ulp=1, min_exact=0.99, ulp_abs_slack=4e-6)
+
+
+@pytest.mark.parametrize("idx_dtype", [torch.int32, torch.int64, None])
+def test_rope_table_interleaved(gpu, oracle_lib, idx_dtype):
+    """freqs_cis table gathered by position ids (v8/c8c60d8f7015) or by s (v7/e29b92927600)."""
+    g = gen(31)
+    S, Hq, Hk, D, P = 96, 8, 2, 128, 200
+    q = randn_bf16((1, S, Hq, D), g)
+    k = randn_bf16((1, S, Hk, D), g)
+    freqs = torch.complex(torch.randn(P, D // 2, generator=g), torch.randn(P, D // 2, generator=g))
+    pos = torch.randint(0, P, (1, S), generator=g)
+    posa = None if idx_dtype is None else pos.to(idx_dtype).to(gpu)
+    qo, ko = kp.rope(q.to(gpu), k.to(gpu), positions=posa, freqs_cis=freqs.to(gpu), pairing="interleaved")
+    torch.cuda.synchronize()
+    pn = None if idx_dtype is None else pos.numpy()
+    eq = oracle_lib.rope(to_u16(q), pn, pairing="interleaved", freqs=freqs.numpy())
+    ek = oracle_lib.rope(to_u16(k), pn, pairing="interleaved", freqs=freqs.numpy())
+    assert_bf16_close(to_u16(qo), eq, what="q", max_ulp=1, min_exact=0.99, ulp_abs_slack=4e-6)
+    assert_bf16_close(to_u16(ko), ek, what="k", max_ulp=1, min_exact=0.99, ulp_abs_slack=4e-6)
+
+
+def test_rope_strided_transposed_input(gpu, oracle_lib):
+    """Input given as a transposed view ([B, H, S, D] memory read as [B, S, H, D])."""
+    g = gen(32)
+    B, S, H, D = 1, 40, 8, 128
+    base = randn_bf16((B, H, S, D), g)
+    x = base.to(gpu).transpose(1, 2)  # [B, S, H, D] view, strides (H*S*D, D, S*D, 1)
+    out, _ = kp.rope(x, theta=10000.0, pairing="half")
+    exp = oracle_lib.rope(to_u16(base.transpose(1, 2).contiguous()), None, pairing="half", theta=10000.0)
+    assert_bf16_close(to_u16(out), exp, what="transposed", max_ulp=1, min_exact=0.99, ulp_abs_slack=4e-6)
+
+
+def test_rope_table_vs_torch_complex(gpu):
+    """The reference op chain on this GPU: view_as_complex(x.float()) * freqs -> bf16."""
+    g = gen(33)
+    S, H, D = 128, 8, 128
+    x = randn_bf16((1, S, H, D), g).to(gpu)
+    freqs = torch.polar(torch.ones(S, D // 2), torch.rand(S, D // 2, generator=g) * 6.28).to(gpu)
+    xc = torch.view_as_complex(x.float().view(1, S, H, D // 2, 2))
+    ref = torch.view_as_real(xc * freqs.view(1, S, 1, D // 2)).reshape(1, S, H, D).to(torch.bfloat16)
+    out, _ = kp.rope(x, freqs_cis=freqs, pairing="interleaved")
+    assert_bf16_close(to_u16(out), to_u16(ref), what="vs torch complex", max_ulp=1, ulp_abs_slack=4e-6)
+
+
+def test_rope_out_of_table_position_flagged(gpu):
+    x = torch.ones((1, 4, 1, 8), dtype=torch.bfloat16, device=gpu)
+    freqs = torch.ones((3, 4), dtype=torch.complex64, device=gpu)
+    with pytest.raises(IndexError):
+        kp.rope(x, positions=torch.tensor([0, 1, 2, 3], device=gpu), freqs_cis=freqs, pairing="interleaved")
