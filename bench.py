@@ -397,6 +397,9 @@ def main():
     ap.add_argument("--all", action="store_true", help="also measure every other workload (GPU only)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--copy-calibration-mib", type=int, default=0,
+                    help="after the workload, run 5 plain device copies of this many MiB (a known-size "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
@@ -427,6 +430,14 @@ def main():
         return wl, r, cpu
 
     wl, r, cpu = run(args.workload, not args.no_cpu)
+    if args.copy_calibration_mib > 0:
+        n = args.copy_calibration_mib << 20
+        src = torch.empty(n, dtype=torch.uint8, device=dev)
+        dst = torch.empty(n, dtype=torch.uint8, device=dev)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"[bench] copy calibration: 5 x {args.copy_calibration_mib} MiB device copies", file=sys.stderr, flush=True)
     line = {
         "metric": "achieved HBM GB/s and % of 8 TB/s peak per fragment; us/call vs CPU eager",
         "value": round(r["value"], 2),

@@ -5,25 +5,26 @@
 // Zipf-distributed ids hit the same rows repeatedly; output rows are written
 // with non-temporal stores.
 //
-// Backward pipeline (five launches on one stream, no float atomics):
+// Backward pipeline (four launches on one stream, no float atomics):
 //   K1 emb_sort_chunks : keys (id << tbits | t) of each 2048-token chunk are
-//                        bitonic-sorted in LDS.  Padding / out-of-range ids get
-//                        the sentinel key and sort last.
-//   K2 emb_merge_rank  : rank of a key = its index in its chunk + the number of
-//                        smaller keys in every other chunk (binary search);
-//                        the key is scattered to that rank.  Keys are unique,
-//                        so the global order is fully determined.
-//   K3 emb_plan        : one block walks the sorted keys, finds id segments,
-//                        splits segments into runs of kRun tokens ("parts"),
-//                        builds the work lists, the touched-row bitmap and
-//                        resets the work-queue counter.
-//   K4 emb_dense       : persistent blocks pull work items from the queue:
-//                        a part sums its run of grad rows in ascending t (fp32)
-//                        and writes the output row (single-part segment) or an
-//                        fp32 partial row; a zero item writes the untouched
-//                        rows of a kZeroRows vocab range as zeros.
-//   K5 emb_combine     : segments with several parts add their partial rows in
-//                        part order and write the output row.
+//                        bitonic-sorted (registers, lane shuffles, LDS only for
+//                        the cross-wave stages); padding / out-of-range ids get
+//                        the sentinel key and sort last.  K1 also clears the
+//                        touched-row bitmap.
+//   K2 emb_rank        : one thread per key.  Binary searches in every sorted
+//                        chunk give the key's global rank (keys are unique, so
+//                        the order is fully determined) and the bounds [lo, hi)
+//                        of its id's run in the global order; the key and its
+//                        bounds are scattered to that rank and the first key of
+//                        a run sets the id's bit in the bitmap.
+//   K3 emb_dense       : one-shot grid.  A window block covers kWin
+//                        consecutive sorted positions x 1024 columns: each run
+//                        piece inside it is summed in ascending t (fp32) and
+//                        written as the output row when the run lies inside the
+//                        window, else as an fp32 piece row.  Every other block
+//                        writes 1024 zero columns of one untouched vocab row.
+//   K4 emb_combine     : runs that span windows: the window holding the run's
+//                        start adds the pieces in window order and writes the row.
 // Every output row is written exactly once.
 #include "kp_common.hpp"
 #include "kp_internal.hpp"
@@ -32,10 +33,8 @@ namespace kp {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 2048;  // keys per K1 block (256 threads x 8)
-constexpr int kRun = 32;      // tokens per part
-constexpr int kZeroRows = 16; // vocab rows per zero-fill item
-constexpr int kPlanThreads = 1024;
+constexpr int kChunk = 2048;   // keys per K1 block (256 threads x 8)
+constexpr int kWin = 32;       // sorted positions per K3 window item
 constexpr uint32_t kSentinel = 0xffffffffu;
 
 __device__ __forceinline__ int64_t load_index(const void* idx, int ib, int64_t t) {
@@ -88,11 +87,7 @@ __global__ __launch_bounds__(kThreads) void emb_fwd(EmbFwdArgs a) {
 
 // =============================================================== backward
 struct EmbHeader {
-  int32_t n_valid;  // tokens that contribute (id in range, != padding_idx)
-  int32_t n_seg;    // distinct contributing ids
-  int32_t n_items;  // parts (segment runs)
-  int32_t n_multi;  // segments with more than one part
-  int32_t queue;    // K4 work-queue counter
+  int32_t n_valid;  // contributing tokens (id in range, != padding_idx)
   int32_t pad[3];
 };
 
@@ -102,7 +97,7 @@ struct EmbBwdArgs {
   const void* idx;
   int ib;
   int64_t T, V, D, padding_idx;
-  int scale;       // scale_grad_by_freq
+  int scale;  // scale_grad_by_freq
   void* out;
   int out_bf16;
   int round_bf16;
@@ -111,240 +106,200 @@ struct EmbBwdArgs {
   int32_t* err;
   // workspace views
   EmbHeader* hdr;
-  uint32_t* keys_chunk;  // [nchunks * kChunk]
-  uint32_t* keys;        // [T] globally sorted valid keys
+  uint32_t* keys_chunk;  // [nchunks * kChunk] chunk-sorted keys
   int32_t* chunk_valid;  // [nchunks]
-  int32_t* seg_id;       // [T]
-  int32_t* seg_start;    // [T + 1]
-  int32_t* part_base;    // [T] first partial slot of a multi-part segment (-1 otherwise)
-  int32_t* item_seg;     // [max_items]
-  int32_t* item_part;    // [max_items]
-  int32_t* multi;        // [max_multi]
-  uint32_t* bitmap;      // [ceil(V / 32)]
-  float* partials;       // [max_partials, D]
+  uint32_t* keys;        // [T] globally sorted valid keys
+  int32_t* run_lo;       // [T] start of the key's id run in the sorted order
+  int32_t* run_hi;       // [T] end of the run
+  uint32_t* bitmap;      // [ceil(V / 32)] touched rows
+  float* pieces;         // [2 * nwin, D] piece rows of runs that span windows
 };
 
 // ---- K1: sort each chunk of keys (bitonic, ascending) --------------------
+// Thread t holds positions 8t..8t+7.  Stages with partner distance j < 8 are
+// register min/max, 8 <= j < 512 exchange within the wave (lane t ^ j/8),
+// j >= 512 go through LDS with block barriers.
 __global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a) {
   __shared__ uint32_t s[kChunk];
   const int tid = threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * kChunk;
-  for (int i = tid; i < kChunk; i += kThreads) {
-    const int64_t t = base + i;
+
+  // clear this block's share of the bitmap (K2 sets bits after this kernel)
+  const int64_t nwords = (a.V + 31) / 32;
+  const int64_t per = (nwords + gridDim.x - 1) / gridDim.x;
+  for (int64_t w = blockIdx.x * per + tid; w < min(nwords, (int64_t)(blockIdx.x + 1) * per); w += kThreads)
+    a.bitmap[w] = 0u;
+
+  // The keys are unique, so their initial placement does not change the
+  // sorted result: load them coalesced (element e of thread tid is token
+  // base + e * 256 + tid) and sort positions 8 * tid + e.
+  uint32_t k8[8];
+  int nvalid = 0;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int64_t t = base + e * kThreads + tid;
     uint32_t key = kSentinel;
     if (t < a.T) {
       const int64_t id = load_index(a.idx, a.ib, t);
       const bool in_range = id >= 0 && id < a.V;
       if (!in_range && a.err) *a.err = 1;
-      if (in_range && id != a.padding_idx) key = ((uint32_t)id << a.tbits) | (uint32_t)t;
+      if (in_range && id != a.padding_idx) {
+        key = ((uint32_t)id << a.tbits) | (uint32_t)t;
+        ++nvalid;
+      }
     }
-    s[i] = key;
+    k8[e] = key;
   }
-  for (int k = 2; k <= kChunk; k <<= 1) {
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      __syncthreads();
-      const int lj = __builtin_ctz(j);
+
 #pragma unroll
-      for (int r = 0; r < kChunk / 2 / kThreads; ++r) {
-        const int p = r * kThreads + tid;  // pair index
-        const int i = ((p >> lj) << (lj + 1)) | (p & (j - 1));
-        const int l = i | j;
-        const uint32_t x = s[i], y = s[l];
-        const bool up = (i & k) == 0;
-        if ((x > y) == up) {
-          s[i] = y;
-          s[l] = x;
+  for (int k = 2; k <= kChunk; k <<= 1) {
+#pragma unroll
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j >= 512) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) s[tid * 8 + e] = k8[e];
+        __syncthreads();
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = tid * 8 + e, l = i ^ j;
+          const uint32_t o = s[l];
+          const bool take_min = ((i < l) == ((i & k) == 0));
+          k8[e] = take_min ? min(k8[e], o) : max(k8[e], o);
+        }
+        __syncthreads();
+      } else if (j >= 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int i = tid * 8 + e, l = i ^ j;
+          const uint32_t o = (uint32_t)__shfl_xor((int)k8[e], j >> 3, 64);
+          const bool take_min = ((i < l) == ((i & k) == 0));
+          k8[e] = take_min ? min(k8[e], o) : max(k8[e], o);
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (e & j) continue;
+          const int i = tid * 8 + e;
+          const bool up = (i & k) == 0;
+          const uint32_t x = k8[e], y = k8[e | j];
+          k8[e] = up ? min(x, y) : max(x, y);
+          k8[e | j] = up ? max(x, y) : min(x, y);
         }
       }
     }
   }
+  uint32_t* dst = a.keys_chunk + base + tid * 8;
+  *reinterpret_cast<u32x4*>(dst) = u32x4{k8[0], k8[1], k8[2], k8[3]};
+  *reinterpret_cast<u32x4*>(dst + 4) = u32x4{k8[4], k8[5], k8[6], k8[7]};
+  // valid keys of the chunk (integer sum: order-independent)
+  __shared__ int s_cnt;
+  if (tid == 0) s_cnt = 0;
   __syncthreads();
-  for (int i = tid; i < kChunk; i += kThreads) a.keys_chunk[base + i] = s[i];
+  if (nvalid) atomicAdd(&s_cnt, nvalid);
+  __syncthreads();
+  if (tid == 0) a.chunk_valid[blockIdx.x] = s_cnt;
 }
 
-// number of entries < key in the ascending array v[0..n)
-__device__ __forceinline__ int lower_bound_u32(const uint32_t* v, int n, uint32_t key) {
-  int lo = 0, hi = n;
-  while (lo < hi) {
-    const int mid = (lo + hi) >> 1;
-    if (v[mid] < key) lo = mid + 1;
-    else hi = mid;
-  }
-  return lo;
-}
+// ---- K2: global rank and run bounds of every valid key -------------------
+// For each key, three counts over every sorted chunk: keys < key (rank),
+// keys < (id << tbits) (run start) and keys < ((id + 1) << tbits) (run end).
+// The 3 * nchunks binary searches advance in lockstep so their LDS reads
+// overlap.  The sorted chunks are staged in LDS when they fit (<= 64 KiB,
+// i.e. up to kMaxLdsChunks chunks), else read from global memory.
+constexpr int kMaxLdsChunks = 8;
 
-// ---- K2: global rank of every valid key ---------------------------------
-// All sorted chunks are staged in LDS when they fit (dynamic LDS), else read
-// from global memory.
 template <bool IN_LDS>
-__global__ __launch_bounds__(kThreads) void emb_merge_rank(EmbBwdArgs a) {
+__global__ __launch_bounds__(kThreads) void emb_rank(EmbBwdArgs a) {
   extern __shared__ uint32_t lds_keys[];
-  const int c = blockIdx.x;
   const int total = a.nchunks * kChunk;
-  const uint32_t* keys = a.keys_chunk;
   if constexpr (IN_LDS) {
-    for (int i = threadIdx.x; i < total; i += kThreads) lds_keys[i] = a.keys_chunk[i];
+    for (int i = threadIdx.x * 4; i < total; i += kThreads * 4)
+      *reinterpret_cast<u32x4*>(lds_keys + i) = *reinterpret_cast<const u32x4*>(a.keys_chunk + i);
     __syncthreads();
-    keys = lds_keys;
   }
-  const uint32_t* mine = keys + (int64_t)c * kChunk;
-  if (threadIdx.x == 0) a.chunk_valid[c] = lower_bound_u32(mine, kChunk, kSentinel);
-  for (int i = threadIdx.x; i < kChunk; i += kThreads) {
-    const uint32_t key = mine[i];
-    if (key == kSentinel) continue;
-    int rank = i;
-    for (int o = 0; o < a.nchunks; ++o)
-      if (o != c) rank += lower_bound_u32(keys + (int64_t)o * kChunk, kChunk, key);
-    if (rank < a.T) a.keys[rank] = key;  // always true for unique keys; bounds the store regardless
+  if (blockIdx.x == 0 && threadIdx.x == 0) {
+    int n = 0;
+    for (int c = 0; c < a.nchunks; ++c) n += a.chunk_valid[c];
+    a.hdr->n_valid = n;
   }
-}
-
-// Exclusive scan of one int per thread over the 1024-thread block; returns the
-// block total through *total.  `buf` holds 1024 + 16 ints of LDS.
-__device__ __forceinline__ int block_exclusive_scan(int v, int* buf, int* total) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  // inclusive scan within the wave (Hillis-Steele over lanes)
-  int x = v;
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t key = IN_LDS ? lds_keys[i] : a.keys_chunk[i];
+  if (key == kSentinel) return;
+  const int c = i / kChunk;
+  const uint32_t id = key >> a.tbits;
+  const uint32_t q[3] = {key, id << a.tbits, (id + 1) << a.tbits};  // (id + 1) << tbits <= 2^31
+  int rank = i - c * kChunk, lo = 0, hi = 0;
+  if constexpr (IN_LDS) {
+    int pos[kMaxLdsChunks][3];
 #pragma unroll
-  for (int d = 1; d < 64; d <<= 1) {
-    const int y = __shfl_up(x, d, 64);
-    if (lane >= d) x += y;
-  }
-  int* wsum = buf + kPlanThreads;
-  if (lane == 63) wsum[wave] = x;
-  __syncthreads();
-  if (tid == 0) {
-    int run = 0;
-    for (int w = 0; w < kPlanThreads / 64; ++w) {
-      const int t = wsum[w];
-      wsum[w] = run;
-      run += t;
-    }
-    buf[0] = run;
-  }
-  __syncthreads();
-  const int res = x - v + wsum[wave];
-  *total = buf[0];
-  __syncthreads();
-  return res;
-}
-
-// ---- K3: segments, parts, work lists, bitmap (one block) -----------------
-__global__ __launch_bounds__(kPlanThreads) void emb_plan(EmbBwdArgs a) {
-  __shared__ int buf[kPlanThreads + 16];
-  __shared__ int carry[4];
-  const int tid = threadIdx.x;
-
-  // bitmap := 0 (rows set below, after a barrier)
-  const int64_t nwords = (a.V + 31) / 32;
-  for (int64_t w = tid; w < nwords; w += kPlanThreads) a.bitmap[w] = 0u;
-
-  int n_valid = 0;
-  for (int c = 0; c < a.nchunks; ++c) n_valid += a.chunk_valid[c];
-
-  // Pass 1: segment heads -> seg_id / seg_start.
-  if (tid == 0) carry[0] = 0;
-  __syncthreads();
-  for (int base = 0; base < n_valid; base += kPlanThreads) {
-    const int i = base + tid;
-    int head = 0;
-    uint32_t id = 0;
-    if (i < n_valid) {
-      id = a.keys[i] >> a.tbits;
-      head = (i == 0) || ((a.keys[i - 1] >> a.tbits) != id);
-    }
-    int tot;
-    const int off = block_exclusive_scan(head, buf, &tot);
-    const int c0 = carry[0];
-    if (head) {
-      a.seg_id[c0 + off] = (int32_t)id;
-      a.seg_start[c0 + off] = i;
-    }
-    __syncthreads();
-    if (tid == 0) carry[0] = c0 + tot;
-    __syncthreads();
-  }
-  const int n_seg = carry[0];
-  if (tid == 0) a.seg_start[n_seg] = n_valid;
-  __threadfence_block();
-  __syncthreads();
-
-  // Bitmap words of touched rows: the first segment falling in a 32-row word
-  // gathers the bits of all segments in that word and stores the word (plain
-  // stores only; ordered after the zeroing above by the block barriers).
-  for (int s = tid; s < n_seg; s += kPlanThreads) {
-    const uint32_t w = (uint32_t)a.seg_id[s] >> 5;
-    if (s > 0 && ((uint32_t)a.seg_id[s - 1] >> 5) == w) continue;
-    uint32_t bits = 0u;
-    for (int q = s; q < n_seg; ++q) {
-      const uint32_t iq = (uint32_t)a.seg_id[q];
-      if ((iq >> 5) != w) break;
-      bits |= 1u << (iq & 31);
-    }
-    a.bitmap[w] = bits;
-  }
-
-  // Pass 2: parts per segment -> items, multi list, partial slots.
-  if (tid == 0) {
-    carry[0] = 0;  // items
-    carry[1] = 0;  // multi segments
-    carry[2] = 0;  // partial slots
-  }
-  __syncthreads();
-  for (int base = 0; base < n_seg; base += kPlanThreads) {
-    const int s = base + tid;
-    int nparts = 0;
-    if (s < n_seg) {
-      const int len = a.seg_start[s + 1] - a.seg_start[s];
-      nparts = (len + kRun - 1) / kRun;
-    }
-    const int is_multi = nparts > 1;
-    int t_items, t_multi, t_slots;
-    const int o_items = block_exclusive_scan(nparts, buf, &t_items);
-    const int o_multi = block_exclusive_scan(is_multi, buf, &t_multi);
-    const int o_slots = block_exclusive_scan(is_multi ? nparts : 0, buf, &t_slots);
-    const int c_items = carry[0], c_multi = carry[1], c_slots = carry[2];
-    if (s < n_seg) {
-      for (int p = 0; p < nparts; ++p) {
-        a.item_seg[c_items + o_items + p] = s;
-        a.item_part[c_items + o_items + p] = p;
+    for (int o = 0; o < kMaxLdsChunks; ++o)
+#pragma unroll
+      for (int k = 0; k < 3; ++k) pos[o][k] = 0;
+#pragma unroll
+    for (int step = kChunk >> 1; step > 0; step >>= 1) {
+#pragma unroll
+      for (int o = 0; o < kMaxLdsChunks; ++o) {
+        if (o >= a.nchunks) break;
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          if (lds_keys[o * kChunk + pos[o][k] + step - 1] < q[k]) pos[o][k] += step;
       }
-      a.part_base[s] = is_multi ? c_slots + o_slots : -1;
-      if (is_multi) a.multi[c_multi + o_multi] = s;
     }
-    __syncthreads();
-    if (tid == 0) {
-      carry[0] = c_items + t_items;
-      carry[1] = c_multi + t_multi;
-      carry[2] = c_slots + t_slots;
+#pragma unroll
+    for (int o = 0; o < kMaxLdsChunks; ++o) {
+      if (o >= a.nchunks) break;
+      int cnt[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) cnt[k] = pos[o][k] + (lds_keys[o * kChunk + pos[o][k]] < q[k] ? 1 : 0);
+      if (o != c) rank += cnt[0];
+      lo += cnt[1];
+      hi += cnt[2];
     }
-    __syncthreads();
+  } else {
+    for (int o = 0; o < a.nchunks; ++o) {
+      const uint32_t* v = a.keys_chunk + (int64_t)o * kChunk;
+      int pos[3] = {0, 0, 0};
+#pragma unroll
+      for (int step = kChunk >> 1; step > 0; step >>= 1)
+#pragma unroll
+        for (int k = 0; k < 3; ++k)
+          if (v[pos[k] + step - 1] < q[k]) pos[k] += step;
+      int cnt[3];
+#pragma unroll
+      for (int k = 0; k < 3; ++k) cnt[k] = pos[k] + (v[pos[k]] < q[k] ? 1 : 0);
+      if (o != c) rank += cnt[0];
+      lo += cnt[1];
+      hi += cnt[2];
+    }
   }
-  if (tid == 0) {
-    a.hdr->n_valid = n_valid;
-    a.hdr->n_seg = n_seg;
-    a.hdr->n_items = carry[0];
-    a.hdr->n_multi = carry[1];
-    a.hdr->queue = 0;
-  }
+  if (rank >= a.T) return;  // impossible for unique keys; bounds the stores regardless
+  a.keys[rank] = key;
+  a.run_lo[rank] = lo;
+  a.run_hi[rank] = hi;
+  if (rank == lo) atomicOr(a.bitmap + (id >> 5), 1u << (id & 31));
 }
 
-// Stores 8 consecutive output values (fp32 or bf16) at column c of row r.
-__device__ __forceinline__ void store_out8(const EmbBwdArgs& a, int64_t r, int64_t c, const float* v) {
+// Column ownership in K3/K4: a block handles one 1024-column chunk q of a
+// row and thread t the 4 columns [q*1024 + 4t, q*1024 + 4t + 4); every wave
+// load of grad (8 B per lane) and every fp32 store (16 B per lane) then covers
+// one contiguous span of the row.
+constexpr int kColStep = kThreads * 4;
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u32x2 ld8_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+}
+
+// Stores 4 consecutive output values (fp32 or bf16) at column c of row r.
+__device__ __forceinline__ void store_out4(const EmbBwdArgs& a, int64_t r, int64_t c, f32x4 v) {
   if (a.out_bf16) {
-    st16_stream(static_cast<uint16_t*>(a.out) + r * a.D + c, pack8(v));
+    const u32x2 pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+    __builtin_nontemporal_store(pk, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + r * a.D + c));
   } else {
-    float* o = static_cast<float*>(a.out) + r * a.D + c;
-    if (a.round_bf16) {
-      float q[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q[e] = round_bf(v[e]);
-      st16f_stream(o, f32x4{q[0], q[1], q[2], q[3]});
-      st16f_stream(o + 4, f32x4{q[4], q[5], q[6], q[7]});
-    } else {
-      st16f_stream(o, f32x4{v[0], v[1], v[2], v[3]});
-      st16f_stream(o + 4, f32x4{v[4], v[5], v[6], v[7]});
-    }
+    if (a.round_bf16) v = f32x4{round_bf(v[0]), round_bf(v[1]), round_bf(v[2]), round_bf(v[3])};
+    st16f_stream(static_cast<float*>(a.out) + r * a.D + c, v);
   }
 }
 __device__ __forceinline__ void store_out1(const EmbBwdArgs& a, int64_t r, int64_t c, float v) {
@@ -355,137 +310,160 @@ __device__ __forceinline__ void store_out1(const EmbBwdArgs& a, int64_t r, int64
   }
 }
 
-// ---- K4: parts and zero-fill, pulled from a work queue --------------------
+// Workspace reads in K3/K4 are clamped to their valid ranges, so even a
+// corrupted workspace cannot steer a load or store out of bounds.
+__device__ __forceinline__ int64_t token_of(const EmbBwdArgs& a, int64_t r) {
+  const int64_t t = (int64_t)(a.keys[r] & ((1u << a.tbits) - 1u));
+  return t < a.T ? t : 0;
+}
+__device__ __forceinline__ int clamp_pos(int v, int n_valid) { return v < 0 ? 0 : (v > n_valid ? n_valid : v); }
+
+// Where a finished piece [p0, p1) of the run [lo, hi) inside window [w0, w1) goes.
+__device__ __forceinline__ void emit_piece(const EmbBwdArgs& a, int64_t w, int64_t w0, int64_t w1, int lo, int hi,
+                                           int64_t c, const f32x4& acc) {
+  if (lo >= w0 && hi <= w1) {
+    const int64_t row = (int64_t)(a.keys[lo] >> a.tbits);
+    if (row < a.V) store_out4(a, row, c, acc);
+  } else {
+    const int slot = lo < w0 ? 0 : 1;  // 0: continues from an earlier window; 1: run starts here
+    *reinterpret_cast<f32x4*>(a.pieces + (2 * w + slot) * a.D + c) = acc;
+  }
+}
+__device__ __forceinline__ void emit_piece1(const EmbBwdArgs& a, int64_t w, int64_t w0, int64_t w1, int lo, int hi,
+                                            int64_t c, float acc) {
+  if (lo >= w0 && hi <= w1) {
+    const int64_t row = (int64_t)(a.keys[lo] >> a.tbits);
+    if (row < a.V) store_out1(a, row, c, acc);
+  } else {
+    const int slot = lo < w0 ? 0 : 1;
+    a.pieces[(2 * w + slot) * a.D + c] = acc;
+  }
+}
+
+// ---- K3: windows and zero-fill -------------------------------------------
+// A window block sums its sorted positions in order for its 1024 columns:
+// U grad rows are loaded before any of them is added (U independent 8-byte
+// loads per thread), and each column's additions run in ascending position
+// order.  Run boundaries are block-uniform (run_lo / run_hi of the position).
 template <bool VEC>
-__device__ void emb_do_part(const EmbBwdArgs& a, int item) {
-  const int s = a.item_seg[item];
-  const int p = a.item_part[item];
-  const int s0 = a.seg_start[s], s1 = a.seg_start[s + 1];
-  const int j0 = s0 + p * kRun;
-  const int j1 = min(s1, j0 + kRun);
-  const int64_t row = a.seg_id[s];
-  const int pb = a.part_base[s];
-  const float cnt = (float)(s1 - s0);
-  const uint32_t tmask = (1u << a.tbits) - 1u;
+__device__ void emb_do_window(const EmbBwdArgs& a, int64_t w, int64_t q, int n_valid) {
+  const int64_t w0 = w * kWin;
+  const int64_t w1 = min((int64_t)n_valid, w0 + kWin);
   if constexpr (VEC) {
-    for (int64_t c = (int64_t)threadIdx.x * 8; c < a.D; c += kThreads * 8) {
-      float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      int j = j0;
-      for (; j + 4 <= j1; j += 4) {
-        u32x4 v[4];
+    constexpr int U = 16;
+    const int64_t col = q * kColStep + threadIdx.x * 4;
+    const bool on = col < a.D;
+    int lo = min(clamp_pos(a.run_lo[w0], n_valid), (int)w0);
+    int hi = max(clamp_pos(a.run_hi[w0], n_valid), (int)w0 + 1);
+    float cnt = (float)(hi - lo);
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    for (int64_t r0 = w0; r0 < w1; r0 += U) {
+      u32x2 v[U];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const int64_t t = a.keys[j + u] & tmask;
-          v[u] = ld16_stream(a.grad + t * a.grs + c);
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          float f[8];
-          unpack8(v[u], f);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[e] += a.scale ? f[e] / cnt : f[e];
-        }
+      for (int u = 0; u < U; ++u) {
+        const bool have = r0 + u < w1;
+        const int64_t t = have ? token_of(a, r0 + u) : 0;
+        v[u] = (have && on) ? ld8_stream(a.grad + t * a.grs + col) : u32x2{0u, 0u};
       }
-      for (; j < j1; ++j) {
-        const int64_t t = a.keys[j] & tmask;
-        float f[8];
-        unpack8(ld16_stream(a.grad + t * a.grs + c), f);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[e] += a.scale ? f[e] / cnt : f[e];
-      }
-      if (pb < 0) {
-        store_out8(a, row, c, acc);
-      } else {
-        float* o = a.partials + (int64_t)(pb + p) * a.D + c;
-        *reinterpret_cast<f32x4*>(o) = f32x4{acc[0], acc[1], acc[2], acc[3]};
-        *reinterpret_cast<f32x4*>(o + 4) = f32x4{acc[4], acc[5], acc[6], acc[7]};
+      for (int u = 0; u < U; ++u) {
+        const int64_t r = r0 + u;
+        if (r < w1) {
+          if (r == hi) {  // a new run starts at r
+            lo = min(clamp_pos(a.run_lo[r], n_valid), (int)r);
+            hi = max(clamp_pos(a.run_hi[r], n_valid), (int)r + 1);
+            cnt = (float)(hi - lo);
+            acc = f32x4{0.f, 0.f, 0.f, 0.f};
+          }
+          f32x4 f = {bf_lo(v[u][0]), bf_hi(v[u][0]), bf_lo(v[u][1]), bf_hi(v[u][1])};
+          if (a.scale) f = f32x4{f[0] / cnt, f[1] / cnt, f[2] / cnt, f[3] / cnt};
+          acc += f;
+          if ((r + 1 == hi || r + 1 == w1) && on) emit_piece(a, w, w0, w0 + kWin, lo, hi, col, acc);
+        }
       }
     }
   } else {
-    for (int64_t c = threadIdx.x; c < a.D; c += kThreads) {
-      float acc = 0.f;
-      for (int j = j0; j < j1; ++j) {
-        const int64_t t = a.keys[j] & tmask;
-        const float f = bf_to_f(a.grad[t * a.grs + c]);
-        acc += a.scale ? f / cnt : f;
+    for (int64_t c = q * kColStep + threadIdx.x; c < min(a.D, (q + 1) * kColStep); c += kThreads) {
+      int64_t r = w0;
+      while (r < w1) {
+        const int lo = min(clamp_pos(a.run_lo[r], n_valid), (int)r);
+        const int hi = max(clamp_pos(a.run_hi[r], n_valid), (int)r + 1);
+        const float cnt = (float)(hi - lo);
+        const int64_t pe = min((int64_t)hi, w1);
+        float acc = 0.f;
+        for (; r < pe; ++r) {
+          const float f = bf_to_f(a.grad[token_of(a, r) * a.grs + c]);
+          acc += a.scale ? f / cnt : f;
+        }
+        emit_piece1(a, w, w0, w0 + kWin, lo, hi, c, acc);
       }
-      if (pb < 0) store_out1(a, row, c, acc);
-      else a.partials[(int64_t)(pb + p) * a.D + c] = acc;
     }
   }
 }
 
+// One-shot dense writer.  Blocks [0, n_win_blocks) are window blocks, one per
+// (window, 1024-column chunk); they come first in the grid so the heavy runs
+// start early.  Every later block writes one 1024-column chunk of one vocab
+// row as zeros, unless the row is touched (its window block writes it): one
+// 16-byte store per thread, the launch shape that streams fastest on gfx950.
 template <bool VEC>
-__device__ void emb_do_zero(const EmbBwdArgs& a, int64_t z) {
-  const int64_t r0 = z * kZeroRows;
-  const int64_t r1 = min(a.V, r0 + kZeroRows);
-  for (int64_t r = r0; r < r1; ++r) {
-    const uint32_t word = a.bitmap[r >> 5];
-    if ((word >> (r & 31)) & 1u) continue;
-    if constexpr (VEC) {
-      const float zeros[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-      for (int64_t c = (int64_t)threadIdx.x * 8; c < a.D; c += kThreads * 8) store_out8(a, r, c, zeros);
-    } else {
-      for (int64_t c = threadIdx.x; c < a.D; c += kThreads) store_out1(a, r, c, 0.f);
-    }
+__global__ __launch_bounds__(kThreads) void emb_dense(EmbBwdArgs a, int64_t n_win_blocks) {
+  const int64_t nq = (a.D + kColStep - 1) / kColStep;
+  const int64_t b = blockIdx.x;
+  if (b < n_win_blocks) {
+    const int n_valid = (int)min((int64_t)max(a.hdr->n_valid, 0), a.T);
+    const int64_t w = b / nq, q = b % nq;
+    if (w * kWin >= n_valid) return;
+    emb_do_window<VEC>(a, w, q, n_valid);
+    return;
+  }
+  const int64_t zb = b - n_win_blocks;
+  const int64_t r = zb / nq, q = zb % nq;
+  if (r >= a.V) return;
+  if ((a.bitmap[r >> 5] >> (r & 31)) & 1u) return;
+  if constexpr (VEC) {
+    const int64_t c = q * kColStep + (int64_t)threadIdx.x * 4;
+    if (c < a.D) store_out4(a, r, c, f32x4{0.f, 0.f, 0.f, 0.f});
+  } else {
+    for (int64_t c = q * kColStep + threadIdx.x; c < min(a.D, (q + 1) * kColStep); c += kThreads) store_out1(a, r, c, 0.f);
   }
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kThreads) void emb_dense(EmbBwdArgs a) {
-  __shared__ int s_item;
-  const int n_items = a.hdr->n_items;
-  const int64_t n_zero = (a.V + kZeroRows - 1) / kZeroRows;
-  const int64_t total = (int64_t)n_items + n_zero;
-  for (;;) {
-    if (threadIdx.x == 0) s_item = atomicAdd(&a.hdr->queue, 1);
-    __syncthreads();
-    const int64_t item = s_item;
-    __syncthreads();
-    if (item >= total) break;
-    if (item < n_items) emb_do_part<VEC>(a, (int)item);
-    else emb_do_zero<VEC>(a, item - n_items);
-  }
-}
-
-// ---- K5: multi-part segments: partial rows added in part order -----------
+// ---- K4: runs spanning windows, pieces added in window order ---------------
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void emb_combine(EmbBwdArgs a) {
-  const int n_multi = a.hdr->n_multi;
-  constexpr int kCols = kThreads * 8;
-  const int64_t nq = (a.D + kCols - 1) / kCols;
-  for (int64_t it = blockIdx.x; it < (int64_t)n_multi * nq; it += gridDim.x) {
-    const int s = a.multi[it / nq];
-    const int64_t q = it % nq;
-    const int len = a.seg_start[s + 1] - a.seg_start[s];
-    const int nparts = (len + kRun - 1) / kRun;
-    const int pb = a.part_base[s];
-    const int64_t row = a.seg_id[s];
+  const int n_valid = (int)min((int64_t)max(a.hdr->n_valid, 0), a.T);
+  const int64_t n_win = (n_valid + kWin - 1) / kWin;
+  const int64_t nq = (a.D + kColStep - 1) / kColStep;
+  for (int64_t it = blockIdx.x; it < n_win * nq; it += gridDim.x) {
+    const int64_t w = it / nq, q = it % nq;
+    const int64_t w0 = w * kWin, w1 = w0 + kWin;
+    if (w1 >= n_valid) continue;  // the last window cannot hold a run that spans past it
+    const int lo = clamp_pos(a.run_lo[w1 - 1], n_valid), hi = clamp_pos(a.run_hi[w1 - 1], n_valid);
+    if (!(lo >= w0 && hi > w1)) continue;  // only the window where a spanning run starts combines it
+    const int64_t wl = (hi - 1) / kWin;   // window holding the run's last position
+    const int64_t row = a.keys[lo] >> a.tbits;
+    if (row >= a.V) continue;
     if constexpr (VEC) {
-      const int64_t c = q * kCols + (int64_t)threadIdx.x * 8;
-      if (c < a.D) {
-        float acc[8];
-        const float* p0 = a.partials + (int64_t)pb * a.D + c;
-        f32x4 u = *reinterpret_cast<const f32x4*>(p0), v = *reinterpret_cast<const f32x4*>(p0 + 4);
-        for (int e = 0; e < 4; ++e) {
-          acc[e] = u[e];
-          acc[4 + e] = v[e];
-        }
-        for (int p = 1; p < nparts; ++p) {
-          const float* pp = a.partials + (int64_t)(pb + p) * a.D + c;
-          u = *reinterpret_cast<const f32x4*>(pp);
-          v = *reinterpret_cast<const f32x4*>(pp + 4);
-          for (int e = 0; e < 4; ++e) {
-            acc[e] += u[e];
-            acc[4 + e] += v[e];
-          }
-        }
-        store_out8(a, row, c, acc);
+      const int64_t c = q * kColStep + (int64_t)threadIdx.x * 4;
+      if (c >= a.D) continue;
+      f32x4 acc = *reinterpret_cast<const f32x4*>(a.pieces + (2 * w + 1) * a.D + c);
+      constexpr int U = 16;
+      for (int64_t w2 = w + 1; w2 <= wl; w2 += U) {
+        f32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          v[u] = (w2 + u <= wl) ? *reinterpret_cast<const f32x4*>(a.pieces + (2 * (w2 + u)) * a.D + c)
+                                : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (w2 + u <= wl) acc += v[u];
       }
+      store_out4(a, row, c, acc);
     } else {
-      for (int64_t c = q * kCols + threadIdx.x; c < min(a.D, (q + 1) * kCols); c += kThreads) {
-        float acc = a.partials[(int64_t)pb * a.D + c];
-        for (int p = 1; p < nparts; ++p) acc += a.partials[(int64_t)(pb + p) * a.D + c];
+      for (int64_t c = q * kColStep + threadIdx.x; c < min(a.D, (q + 1) * kColStep); c += kThreads) {
+        float acc = a.pieces[(2 * w + 1) * a.D + c];
+        for (int64_t w2 = w + 1; w2 <= wl; ++w2) acc += a.pieces[(2 * w2) * a.D + c];
         store_out1(a, row, c, acc);
       }
     }
@@ -500,10 +478,9 @@ int bits_for(int64_t n) {  // bits needed to represent values 0..n-1
 }
 
 struct Layout {
-  size_t hdr, keys_chunk, keys, chunk_valid, seg_id, seg_start, part_base, item_seg, item_part, multi, bitmap,
-      partials, total;
+  size_t hdr, keys_chunk, chunk_valid, keys, run_lo, run_hi, bitmap, pieces, total;
   int nchunks;
-  int64_t max_items, max_multi, max_partials;
+  int64_t nwin;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
@@ -511,34 +488,24 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 Layout make_layout(int64_t T, int64_t V, int64_t D) {
   Layout L{};
   L.nchunks = (int)ceil_div(T > 0 ? T : 1, kChunk);
-  L.max_items = ceil_div(T, kRun) + T;
-  L.max_multi = ceil_div(T, kRun) + 1;
-  L.max_partials = 2 * ceil_div(T, kRun) + 1;
+  L.nwin = ceil_div(T, kWin);
   size_t o = 0;
   L.hdr = o;
   o = align256(o + sizeof(EmbHeader));
   L.keys_chunk = o;
   o = align256(o + (size_t)L.nchunks * kChunk * 4);
-  L.keys = o;
-  o = align256(o + (size_t)T * 4);
   L.chunk_valid = o;
   o = align256(o + (size_t)L.nchunks * 4);
-  L.seg_id = o;
+  L.keys = o;
   o = align256(o + (size_t)T * 4);
-  L.seg_start = o;
-  o = align256(o + (size_t)(T + 1) * 4);
-  L.part_base = o;
+  L.run_lo = o;
   o = align256(o + (size_t)T * 4);
-  L.item_seg = o;
-  o = align256(o + (size_t)L.max_items * 4);
-  L.item_part = o;
-  o = align256(o + (size_t)L.max_items * 4);
-  L.multi = o;
-  o = align256(o + (size_t)L.max_multi * 4);
+  L.run_hi = o;
+  o = align256(o + (size_t)T * 4);
   L.bitmap = o;
   o = align256(o + (size_t)ceil_div(V, 32) * 4);
-  L.partials = o;
-  o = align256(o + (size_t)L.max_partials * (size_t)D * 4);
+  L.pieces = o;
+  o = align256(o + (size_t)(2 * L.nwin + 1) * (size_t)D * 4);
   L.total = o;
   return L;
 }
@@ -554,7 +521,7 @@ int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table
                           int index_bytes, int64_t T, void* out, int64_t out_row_stride, int32_t* error_flag,
                           void* stream) {
   static const char* who = "kp_embedding_fwd_bf16";
-  if (table == nullptr || out == nullptr || (T > 0 && indices == nullptr))
+  if ((T > 0 && (table == nullptr || out == nullptr || indices == nullptr)))
     return fail(KP_EINVAL, "%s: NULL table, indices or out", who);
   if (V <= 0 || D <= 0 || T < 0) return fail(KP_EINVAL, "%s: need V > 0, D > 0, T >= 0", who);
   if (index_bytes != 4 && index_bytes != 8) return fail(KP_EINVAL, "%s: index_bytes must be 4 or 8", who);
@@ -620,36 +587,34 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   a.err = error_flag;
   a.hdr = reinterpret_cast<EmbHeader*>(ws + L.hdr);
   a.keys_chunk = reinterpret_cast<uint32_t*>(ws + L.keys_chunk);
-  a.keys = reinterpret_cast<uint32_t*>(ws + L.keys);
   a.chunk_valid = reinterpret_cast<int32_t*>(ws + L.chunk_valid);
-  a.seg_id = reinterpret_cast<int32_t*>(ws + L.seg_id);
-  a.seg_start = reinterpret_cast<int32_t*>(ws + L.seg_start);
-  a.part_base = reinterpret_cast<int32_t*>(ws + L.part_base);
-  a.item_seg = reinterpret_cast<int32_t*>(ws + L.item_seg);
-  a.item_part = reinterpret_cast<int32_t*>(ws + L.item_part);
-  a.multi = reinterpret_cast<int32_t*>(ws + L.multi);
+  a.keys = reinterpret_cast<uint32_t*>(ws + L.keys);
+  a.run_lo = reinterpret_cast<int32_t*>(ws + L.run_lo);
+  a.run_hi = reinterpret_cast<int32_t*>(ws + L.run_hi);
   a.bitmap = reinterpret_cast<uint32_t*>(ws + L.bitmap);
-  a.partials = reinterpret_cast<float*>(ws + L.partials);
+  a.pieces = reinterpret_cast<float*>(ws + L.pieces);
 
-  const bool vec = (D % 8) == 0 && aligned16(grad_table) && (T == 0 || (aligned16(grad) && grad_row_stride % 8 == 0));
+  const bool vec = (D % 4) == 0 && aligned16(grad_table) &&
+                   (T == 0 || ((reinterpret_cast<uintptr_t>(grad) & 7u) == 0 && grad_row_stride % 4 == 0));
   hipStream_t s = as_stream(stream);
   int st;
   hipLaunchKernelGGL(emb_sort_chunks, dim3(L.nchunks), dim3(kThreads), 0, s, a);
   if ((st = check_launch(who)) != KP_OK) return st;
-  const size_t keys_bytes = (size_t)L.nchunks * kChunk * 4;
-  if (keys_bytes <= 64 * 1024) {
-    hipLaunchKernelGGL(emb_merge_rank<true>, dim3(L.nchunks), dim3(kThreads), keys_bytes, s, a);
-  } else {
-    hipLaunchKernelGGL(emb_merge_rank<false>, dim3(L.nchunks), dim3(kThreads), 0, s, a);
-  }
+  const int total_keys = L.nchunks * kChunk;
+  const size_t keys_bytes = (size_t)total_keys * 4;
+  const dim3 rgrid((unsigned)ceil_div(total_keys, kThreads));
+  if (keys_bytes <= 64 * 1024) hipLaunchKernelGGL(emb_rank<true>, rgrid, dim3(kThreads), keys_bytes, s, a);
+  else hipLaunchKernelGGL(emb_rank<false>, rgrid, dim3(kThreads), 0, s, a);
   if ((st = check_launch(who)) != KP_OK) return st;
-  hipLaunchKernelGGL(emb_plan, dim3(1), dim3(kPlanThreads), 0, s, a);
-  if ((st = check_launch(who)) != KP_OK) return st;
-  const int grid = cu_count() * 4;
+  const int64_t nq = ceil_div(D, kColStep);
+  const int64_t n_win_blocks = L.nwin * nq;
+  const int64_t dense_blocks = n_win_blocks + V * nq;
+  if (dense_blocks > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: V * D too large for one launch", who);
   prof_begin(s);
-  if (vec) hipLaunchKernelGGL(emb_dense<true>, dim3(grid), dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL(emb_dense<false>, dim3(grid), dim3(kThreads), 0, s, a);
+  if (vec) hipLaunchKernelGGL(emb_dense<true>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
+  else hipLaunchKernelGGL(emb_dense<false>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
   prof_end(s);
+  const int grid = cu_count() * 4;
   if ((st = check_launch(who)) != KP_OK) return st;
   if (vec) hipLaunchKernelGGL(emb_combine<true>, dim3(grid), dim3(kThreads), 0, s, a);
   else hipLaunchKernelGGL(emb_combine<false>, dim3(grid), dim3(kThreads), 0, s, a);

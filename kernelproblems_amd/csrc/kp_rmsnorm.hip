@@ -60,27 +60,35 @@ __device__ __forceinline__ int64_t w_index(int64_t c, int64_t seg_len, int64_t s
   return (c / seg_len) * seg_stride + (c % seg_len);
 }
 
-// Loads VPL chunks of the bf16 running sum of up to three row terms.
-template <int VPL>
-__device__ __forceinline__ void load_terms(u32x4 (&v)[VPL], const uint16_t* const* base, const int64_t* strides,
-                                           int n, int64_t row, int64_t col) {
-  const uint16_t* p0 = base[0] + row * strides[0] + col;
+// Raw (not yet summed) 16-byte chunks of up to NT row terms.  Rows are
+// software-pipelined: the next row's raw terms are requested before the
+// current row's stores, because vmcnt counts loads and stores in issue order
+// and a wait on a load issued after a store would also wait for that store.
+template <int VPL, int NT>
+struct RawRow {
+  u32x4 v[NT][VPL];
+};
+
+template <int VPL, int NT>
+__device__ __forceinline__ void load_raw(RawRow<VPL, NT>& r, const uint16_t* const (&base)[3],
+                                         const int64_t (&strides)[3], int64_t row, int64_t col, bool valid) {
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) v[i] = ld16(p0 + i * 512);
-  if (n > 1) {
-    const uint16_t* p1 = base[1] + row * strides[1] + col;
-    u32x4 t[VPL];
+  for (int t = 0; t < NT; ++t) {
+    const uint16_t* p = base[t] + row * strides[t] + col;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) t[i] = ld16(p1 + i * 512);
+    for (int i = 0; i < VPL; ++i) r.v[t][i] = valid ? ld16_stream(p + i * 512) : u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// bf16 running sum of the terms, each add rounded as an eager bf16 add.Tensor.
+template <int VPL, int NT>
+__device__ __forceinline__ void sum_raw(u32x4 (&out)[VPL], const RawRow<VPL, NT>& r) {
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) v[i] = add_bf8(v[i], t[i]);
-    if (n > 2) {
-      const uint16_t* p2 = base[2] + row * strides[2] + col;
+  for (int i = 0; i < VPL; ++i) {
+    u32x4 acc = r.v[0][i];
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) t[i] = ld16(p2 + i * 512);
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) v[i] = add_bf8(v[i], t[i]);
-    }
+    for (int t = 1; t < NT; ++t) acc = add_bf8(acc, r.v[t][i]);
+    out[i] = acc;
   }
 }
 
@@ -98,7 +106,7 @@ __device__ __forceinline__ void load_weight(u32x4 (&wv)[VPL], const uint16_t* w,
 }
 
 // ------------------------------------------------------------------ forward
-template <int VPL, int WPR>
+template <int VPL, int WPR, int NX>
 __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   constexpr int RB = 4 / WPR;
   constexpr int SEG = 512 * VPL;
@@ -110,18 +118,23 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   u32x4 wv[VPL];
   load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
 
+  // Blocks walk the row groups grid-stride (measured faster on gfx950 than
+  // contiguous per-block ranges for these row loops).
   const int64_t ngroups = ceil_div_dev(a.M, RB);
-  int it = 0;
-  for (int64_t g = blockIdx.x; g < ngroups; g += gridDim.x, ++it) {
+  int64_t g = blockIdx.x;
+  RawRow<VPL, NX> cur;
+  load_raw<VPL, NX>(cur, a.x, a.xs, g * RB + rloc, col, g < ngroups && g * RB + rloc < a.M);
+  for (int it = 0; g < ngroups; g += gridDim.x, ++it) {
     const int64_t row = g * RB + rloc;
     const bool valid = row < a.M;
+    const int64_t gn = g + gridDim.x, rown = gn * RB + rloc;
+    RawRow<VPL, NX> nxt;
+    load_raw<VPL, NX>(nxt, a.x, a.xs, rown, col, gn < ngroups && rown < a.M);
+
     u32x4 hv[VPL];
-    if (valid) {
-      load_terms<VPL>(hv, a.x, a.xs, a.n_x, row, col);
-    } else {
+    sum_raw<VPL, NX>(hv, cur);
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) hv[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -140,6 +153,8 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
       ss = t;
     }
     const float r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) reg_barrier(hv[i]);
     if (valid) {
       uint16_t* yrow = a.y + row * a.ys + col;
 #pragma unroll
@@ -151,13 +166,14 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
         for (int e = 0; e < 8; ++e) o[e] = (f[e] * r) * wf[e];
         st16(yrow + i * 512, pack8(o));
       }
-      if (a.h != nullptr && a.n_x > 1) {
+      if (NX > 1 && a.h != nullptr) {
         uint16_t* hrow = a.h + row * a.hs + col;
 #pragma unroll
         for (int i = 0; i < VPL; ++i) st16(hrow + i * 512, hv[i]);
       }
       if (a.rstd != nullptr && part == 0 && lane == 0) a.rstd[row] = r;
     }
+    cur = nxt;
   }
 }
 
@@ -224,7 +240,7 @@ __device__ __forceinline__ void add_acc(const float* buf, int lane, float (&acc)
   }
 }
 
-template <int VPL, int WPR>
+template <int VPL, int WPR, int NX, int NDY, bool RES>
 __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
   constexpr int RB = 4 / WPR;
   constexpr int SEG = 512 * VPL;
@@ -242,19 +258,40 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
   for (int i = 0; i < VPL * 8; ++i) acc[i] = 0.f;
 
   const float inv_n = 1.0f / (float)a.N;
+  // Blocks walk the row groups grid-stride.
   const int64_t ngroups = ceil_div_dev(a.M, RB);
-  int it = 0;
-  for (int64_t g = blockIdx.x; g < ngroups; g += gridDim.x, ++it) {
+  int64_t g = blockIdx.x;
+  RawRow<VPL, NX> xc;
+  RawRow<VPL, NDY> dc;
+  {
+    const int64_t row = g * RB + rloc;
+    const bool ok = g < ngroups && row < a.M;
+    load_raw<VPL, NX>(xc, a.x, a.xs, row, col, ok);
+    load_raw<VPL, NDY>(dc, a.dy, a.dys, row, col, ok);
+  }
+  for (int it = 0; g < ngroups; g += gridDim.x, ++it) {
     const int64_t row = g * RB + rloc;
     const bool valid = row < a.M;
-    u32x4 xv[VPL], dv[VPL];
-    if (valid) {
-      load_terms<VPL>(xv, a.x, a.xs, a.n_x, row, col);
-      load_terms<VPL>(dv, a.dy, a.dys, a.n_dy, row, col);
-    } else {
+    // This row's scalar and residual loads go out before the next row's prefetch.
+    const float r_given = (a.rstd != nullptr && valid) ? a.rstd[row] : 0.f;
+    u32x4 rv[RES ? VPL : 1];
+    if (RES && valid) {
+      const uint16_t* rrow = a.dxr + row * a.dxrs + col;
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) xv[i] = dv[i] = u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < VPL; ++i) rv[i] = ld16_stream(rrow + i * 512);
     }
+    const int64_t gn = g + gridDim.x, rown = gn * RB + rloc;
+    const bool okn = gn < ngroups && rown < a.M;
+    RawRow<VPL, NX> xn;
+    RawRow<VPL, NDY> dn;
+    load_raw<VPL, NX>(xn, a.x, a.xs, rown, col, okn);
+    load_raw<VPL, NDY>(dn, a.dy, a.dys, rown, col, okn);
+
+    u32x4 xv[VPL], dv[VPL];
+    sum_raw<VPL, NX>(xv, xc);
+    sum_raw<VPL, NDY>(dv, dc);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
     // sum(x * g) and, when rstd is not supplied, sum(x^2), in one sweep.
     float sxg = 0.f, ss = 0.f;
 #pragma unroll
@@ -286,22 +323,17 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
       sxg = t0;
       ss = t1;
     }
-    float r;
-    if (a.rstd != nullptr) {
-      r = valid ? a.rstd[row] : 0.f;
-    } else {
-      r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
-    }
+    const float r = (a.rstd != nullptr) ? r_given : 1.0f / sqrtf(ss / (float)a.N + a.eps);
     // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
     const float cN = (r * sxg) * inv_n;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      reg_barrier(xv[i]);
+      reg_barrier(dv[i]);
+      reg_barrier(wv[i]);
+    }
     if (valid) {
       uint16_t* dxrow = a.dx + row * a.dxs + col;
-      const uint16_t* rrow = a.dxr ? a.dxr + row * a.dxrs + col : nullptr;
-      u32x4 rv[VPL];
-      if (rrow) {
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) rv[i] = ld16(rrow + i * 512);
-      }
 #pragma unroll
       for (int i = 0; i < VPL; ++i) {
         float xf[8], df[8], wf[8], o[8];
@@ -316,10 +348,12 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
           acc[i * 8 + e] = fmaf(df[e], xh, acc[i * 8 + e]);
         }
         u32x4 ov = pack8(o);
-        if (rrow) ov = add_bf8(rv[i], ov);
+        if constexpr (RES) ov = add_bf8(rv[i], ov);
         st16(dxrow + i * 512, ov);
       }
     }
+    xc = xn;
+    dc = dn;
   }
 
   if (a.partial == nullptr) return;
@@ -387,19 +421,35 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_generic(RmsBwdArgs a) {
   }
 }
 
-// dw[c] = sum_{p < P} partial[p, c].  Block = 64 columns x 16 row groups; row
-// group q sums rows [q*P/16, (q+1)*P/16) in order, then the 16 group sums are
-// added in group order.
+// dw[c] = sum_{p < P} partial[p, c].  A block owns 16 columns and splits the
+// P partial rows into 64 contiguous groups (thread = 4 columns x 1 group);
+// each group is summed in row order, then the 64 group sums are added in
+// group order.  Every thread's loads are independent, so the whole [P, 16]
+// slab is in flight at once.
+constexpr int kFinCols = 16;
+constexpr int kFinGroups = kThreads / (kFinCols / 4);
+
 __global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restrict__ partial, int P, int64_t N,
                                                             float* dw_f32, uint16_t* dw_bf16, int round_f32) {
-  __shared__ float s[16][64];
-  const int cq = threadIdx.x & 15, q = threadIdx.x >> 4;
-  const int64_t c0 = (int64_t)blockIdx.x * 64 + cq * 4;
-  const int p0 = (int)(((int64_t)P * q) / 16), p1 = (int)(((int64_t)P * (q + 1)) / 16);
+  __shared__ float s[kFinGroups][kFinCols + 1];
+  const int q = threadIdx.x & 3, g = threadIdx.x >> 2;
+  const int64_t c0 = (int64_t)blockIdx.x * kFinCols + q * 4;
+  const int p0 = (int)(((int64_t)P * g) / kFinGroups), p1 = (int)(((int64_t)P * (g + 1)) / kFinGroups);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if ((N & 3) == 0) {
     if (c0 < N) {
-      for (int p = p0; p < p1; ++p) acc += *reinterpret_cast<const f32x4*>(partial + (int64_t)p * N + c0);
+      int p = p0;
+      for (; p + 4 <= p1; p += 4) {
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(partial + (int64_t)p * N + c0);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + 1) * N + c0);
+        const f32x4 v2 = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + 2) * N + c0);
+        const f32x4 v3 = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + 3) * N + c0);
+        acc += v0;
+        acc += v1;
+        acc += v2;
+        acc += v3;
+      }
+      for (; p < p1; ++p) acc += *reinterpret_cast<const f32x4*>(partial + (int64_t)p * N + c0);
     }
   } else {
     for (int k = 0; k < 4; ++k) {
@@ -411,14 +461,13 @@ __global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restr
     }
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) s[q][cq * 4 + k] = acc[k];
+  for (int k = 0; k < 4; ++k) s[g][q * 4 + k] = acc[k];
   __syncthreads();
-  if (threadIdx.x < 64) {
-    const int64_t c = (int64_t)blockIdx.x * 64 + threadIdx.x;
+  if (threadIdx.x < kFinCols) {
+    const int64_t c = (int64_t)blockIdx.x * kFinCols + threadIdx.x;
     if (c < N) {
       float t = s[0][threadIdx.x];
-#pragma unroll
-      for (int g = 1; g < 16; ++g) t += s[g][threadIdx.x];
+      for (int gg = 1; gg < kFinGroups; ++gg) t += s[gg][threadIdx.x];
       if (dw_bf16) dw_bf16[c] = f_to_bf(t);
       if (dw_f32) dw_f32[c] = round_f32 ? round_bf(t) : t;
     }
@@ -429,20 +478,50 @@ __global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restr
 // Fast path shape: N = 512 * VPL * WPR with WPR in {1, 2, 4}.  Fewer chunks
 // per lane (VPL <= 4, at most ~120 VGPRs) keep 4 waves per SIMD resident; a
 // wider row is split over more waves instead.  VPL up to 8 is the fallback.
-int vpl_limit() {
-  static const int lim = [] {
-    const char* e = getenv("KP_RMS_VPL_MAX");
-    const int v = e ? atoi(e) : 4;
-    return (v >= 1 && v <= 8) ? v : 4;
-  }();
-  return lim;
+int env_int(const char* name, int dflt, int lo, int hi) {
+  const char* e = getenv(name);
+  const int v = e ? atoi(e) : dflt;
+  return (v >= lo && v <= hi) ? v : dflt;
+}
+// Launch-shape tuning knobs (read once): KP_RMS_FWD_BPC / KP_RMS_BWD_BPC, row
+// blocks per CU for the forward / backward grids.
+int fwd_bpc() {
+  static const int v = env_int("KP_RMS_FWD_BPC", 8, 1, 64);
+  return v;
+}
+int bwd_bpc() {
+  static const int v = env_int("KP_RMS_BWD_BPC", 2, 1, 4);
+  return v;
+}
+
+// Fast-path row shapes: N = 512 * VPL * WPR, at most 5 16-byte chunks per
+// lane (pipelined kernels stay well under 256 VGPRs); wider rows are split
+// over 2 or 4 waves.  KP_RMS_WPR_MIN (tuning knob) asks for at least that
+// many waves per row where a shape exists.
+int wpr_min() {
+  static const int v = env_int("KP_RMS_WPR_MIN", 1, 1, 4);
+  return v;
+}
+int vpl_max() {
+  static const int v = env_int("KP_RMS_VPL_MAX", 5, 1, 8);
+  return v;
+}
+bool shape_ok(int vpl, int wpr) {
+  switch (vpl * 10 + wpr) {
+    case 11: case 21: case 31: case 41: case 51:
+    case 12: case 22: case 32: case 42: case 52:
+    case 14: case 24: case 34: case 44:
+    case 81: case 82: return true;
+  }
+  return false;
 }
 bool pick_vec(int64_t N, int* vpl, int* wpr) {
   if (N <= 0 || N % 512 != 0) return false;
   const int64_t k = N / 512;
-  for (int vmax : {vpl_limit(), 8}) {
+  for (int pass = 0; pass < 2; ++pass) {
     for (int w : {1, 2, 4}) {
-      if (k % w == 0 && k / w <= vmax) {
+      if (pass == 0 && w < wpr_min()) continue;
+      if (k % w == 0 && k / w <= vpl_max() && shape_ok((int)(k / w), w)) {
         *vpl = (int)(k / w);
         *wpr = w;
         return true;
@@ -455,40 +534,57 @@ bool pick_vec(int64_t N, int* vpl, int* wpr) {
 typedef void (*FwdKernel)(RmsFwdArgs);
 typedef void (*BwdKernel)(RmsBwdArgs);
 
-template <int WPR>
-FwdKernel fwd_kernel_for(int vpl) {
-  switch (vpl) {
-    case 1: return rms_fwd_vec<1, WPR>;
-    case 2: return rms_fwd_vec<2, WPR>;
-    case 3: return rms_fwd_vec<3, WPR>;
-    case 4: return rms_fwd_vec<4, WPR>;
-    case 5: return rms_fwd_vec<5, WPR>;
-    case 6: return rms_fwd_vec<6, WPR>;
-    case 7: return rms_fwd_vec<7, WPR>;
-    case 8: return rms_fwd_vec<8, WPR>;
+template <int VPL, int WPR>
+FwdKernel fwd_for_terms(int nx) {
+  switch (nx) {
+    case 1: return rms_fwd_vec<VPL, WPR, 1>;
+    case 2: return rms_fwd_vec<VPL, WPR, 2>;
+    case 3: return rms_fwd_vec<VPL, WPR, 3>;
   }
   return nullptr;
 }
-template <int WPR>
-BwdKernel bwd_kernel_for(int vpl) {
-  switch (vpl) {
-    case 1: return rms_bwd_vec<1, WPR>;
-    case 2: return rms_bwd_vec<2, WPR>;
-    case 3: return rms_bwd_vec<3, WPR>;
-    case 4: return rms_bwd_vec<4, WPR>;
-    case 5: return rms_bwd_vec<5, WPR>;
-    case 6: return rms_bwd_vec<6, WPR>;
-    case 7: return rms_bwd_vec<7, WPR>;
-    case 8: return rms_bwd_vec<8, WPR>;
+// Term combinations of the backward fast path (x terms, dy terms, residual
+// epilogue) -- the ones the configurations and reference fragments use;
+// others run the generic kernel.
+template <int VPL, int WPR>
+BwdKernel bwd_for_terms(int nx, int ndy, bool res) {
+  if (!res) {
+    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, false>;
+    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, false>;
+    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, false>;
+    if (nx == 2 && ndy == 1) return rms_bwd_vec<VPL, WPR, 2, 1, false>;
+    if (nx == 3 && ndy == 1) return rms_bwd_vec<VPL, WPR, 3, 1, false>;
+    if (nx == 2 && ndy == 2) return rms_bwd_vec<VPL, WPR, 2, 2, false>;
+  } else {
+    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, true>;
+    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, true>;
+    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, true>;
   }
   return nullptr;
 }
-FwdKernel fwd_kernel(int vpl, int wpr) {
-  return wpr == 1 ? fwd_kernel_for<1>(vpl) : wpr == 2 ? fwd_kernel_for<2>(vpl) : fwd_kernel_for<4>(vpl);
-}
-BwdKernel bwd_kernel(int vpl, int wpr) {
-  return wpr == 1 ? bwd_kernel_for<1>(vpl) : wpr == 2 ? bwd_kernel_for<2>(vpl) : bwd_kernel_for<4>(vpl);
-}
+#define KP_SHAPE_SWITCH(FN, ...)                      \
+  switch (vpl * 10 + wpr) {                           \
+    case 11: return FN<1, 1>(__VA_ARGS__);            \
+    case 21: return FN<2, 1>(__VA_ARGS__);            \
+    case 31: return FN<3, 1>(__VA_ARGS__);            \
+    case 41: return FN<4, 1>(__VA_ARGS__);            \
+    case 51: return FN<5, 1>(__VA_ARGS__);            \
+    case 12: return FN<1, 2>(__VA_ARGS__);            \
+    case 22: return FN<2, 2>(__VA_ARGS__);            \
+    case 32: return FN<3, 2>(__VA_ARGS__);            \
+    case 42: return FN<4, 2>(__VA_ARGS__);            \
+    case 52: return FN<5, 2>(__VA_ARGS__);            \
+    case 14: return FN<1, 4>(__VA_ARGS__);            \
+    case 24: return FN<2, 4>(__VA_ARGS__);            \
+    case 34: return FN<3, 4>(__VA_ARGS__);            \
+    case 44: return FN<4, 4>(__VA_ARGS__);            \
+    case 81: return FN<8, 1>(__VA_ARGS__);            \
+    case 82: return FN<8, 2>(__VA_ARGS__);            \
+  }                                                   \
+  return nullptr;
+FwdKernel fwd_kernel(int vpl, int wpr, int nx) { KP_SHAPE_SWITCH(fwd_for_terms, nx) }
+BwdKernel bwd_kernel(int vpl, int wpr, int nx, int ndy, bool res) { KP_SHAPE_SWITCH(bwd_for_terms, nx, ndy, res) }
+#undef KP_SHAPE_SWITCH
 
 bool rows_vec_ok(const void* const* p, const int64_t* s, int n) {
   for (int i = 0; i < n; ++i)
@@ -510,7 +606,7 @@ int check_terms(const char* who, const char* name, const void* const* p, const i
 // count (and hence the summation order) depends only on device and shape.
 int bwd_blocks(int64_t M, int rows_per_block_step) {
   const int64_t groups = ceil_div(M, rows_per_block_step);
-  const int64_t want = (int64_t)cu_count() * 2;
+  const int64_t want = (int64_t)cu_count() * bwd_bpc();
   return (int)(groups < want ? (groups > 0 ? groups : 1) : want);
 }
 
@@ -555,15 +651,17 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
   bool vec = pick_vec(N, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) && aligned16(y) && (y_stride & 7) == 0;
   if (vec && h_out) vec = aligned16(h_out) && (h_stride & 7) == 0;
   if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
+  const FwdKernel fk = vec ? fwd_kernel(vpl, wpr, n_x) : nullptr;
+  vec = vec && fk != nullptr;
   hipStream_t s = as_stream(stream);
   if (vec) {
     const int rb = 4 / wpr;
     const int64_t groups = ceil_div(M, rb);
-    const int64_t cap = (int64_t)cu_count() * 8;
+    const int64_t cap = (int64_t)cu_count() * fwd_bpc();
     const int grid = (int)(groups < cap ? groups : cap);
     void* args[] = {&a};
     prof_begin(s);
-    (void)hipLaunchKernel(reinterpret_cast<const void*>(fwd_kernel(vpl, wpr)), dim3(grid), dim3(kThreads), args, 0, s);
+    (void)hipLaunchKernel(reinterpret_cast<const void*>(fk), dim3(grid), dim3(kThreads), args, 0, s);
     prof_end(s);
   } else {
     const int64_t cap = (int64_t)cu_count() * 8;
@@ -577,8 +675,8 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
 
 size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N) {
   if (M <= 0 || N <= 0) return 16;
-  // Partial rows: at most one per row block; the block count never exceeds 2 per CU.
-  const int64_t blocks = (int64_t)cu_count() * 2;
+  // Partial rows: at most one per row block; the block count never exceeds 4 per CU.
+  const int64_t blocks = (int64_t)cu_count() * 4;
   const int64_t rows = M < blocks ? M : blocks;
   return (size_t)(rows * N * (int64_t)sizeof(float));
 }
@@ -636,13 +734,14 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
                rows_vec_ok(dy_terms, dy_strides, n_dy) && aligned16(dx) && (dx_stride & 7) == 0;
     if (vec && dx_residual) vec = aligned16(dx_residual) && (dxr_stride & 7) == 0;
     if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
+    const BwdKernel bk = vec ? bwd_kernel(vpl, wpr, n_x, n_dy, dx_residual != nullptr) : nullptr;
+    vec = vec && bk != nullptr;
     if (vec) {
       blocks = bwd_blocks(M, 4 / wpr);
       const size_t lds = (want_dw && wpr < 4) ? (size_t)2 * 512 * vpl * sizeof(float) : 0;
       void* args[] = {&a};
       prof_begin(s);
-      (void)hipLaunchKernel(reinterpret_cast<const void*>(bwd_kernel(vpl, wpr)), dim3(blocks), dim3(kThreads), args,
-                            lds, s);
+      (void)hipLaunchKernel(reinterpret_cast<const void*>(bk), dim3(blocks), dim3(kThreads), args, lds, s);
       prof_end(s);
     } else {
       blocks = bwd_blocks(M, 1);
@@ -654,7 +753,7 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
     if (st != KP_OK) return st;
   }
   if (want_dw) {
-    hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, 64)), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, kFinCols)), dim3(kThreads), 0, s,
                        static_cast<const float*>(workspace), blocks, N, dw_f32, static_cast<uint16_t*>(dw_bf16),
                        dw_f32_round_bf16);
     st = check_launch(who);
