@@ -287,7 +287,7 @@ class Rope(Workload):
             sq = L.i64_array(list(qs.stride()[:3]))
             sk = L.i64_array(list(ks.stride()[:3]))
             args = (qs.data_ptr(), qo.data_ptr(), Hq, sq, sq, ks.data_ptr(), ko.data_ptr(), Hk, sk, sk, B, S, D,
-                    pd.data_ptr(), 8, S, 1, 0, theta, None, 0, 0, 0, None, stream)
+                    pd.data_ptr(), 8, S, 1, 0, theta, None, 0, 0, 0, 0, None, stream)
             self.sets.append((fn, args, (qs, ks, qo, ko, sq, sk, pd)))
         self.cpu_sample = f"full [{B},{S}] q and k"
 

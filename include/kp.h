@@ -184,8 +184,12 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride,
  *   stride freq_row_stride (complex elements) and pair i of position p uses
  *   freqs_cis[p, i] (p must lie in [0, freq_rows)).
  * pairing KP_ROPE_HALF pairs (i, i + D/2); KP_ROPE_INTERLEAVED pairs (2i, 2i+1).
- * out = bf16(x_a * c - x_b * s, x_b * c + x_a * s) computed in fp32; conj != 0
- *   uses (c, -s) (the backward of the forward rotation).
+ * out = (x_a * c - x_b * s, x_b * c + x_a * s) computed in fp32 and stored as
+ *   bf16, or as fp32 for tensor i when bit i of out_f32_mask is set (the
+ *   fragment v7/0f38bc55457c/problem.py returns its q rotation in fp32);
+ *   conj != 0 uses (c, -s) (the backward of the forward rotation).
+ * With a table, a position outside [0, freq_rows) reads nothing: its output is
+ *   zero and *error_flag (if non-NULL) is set to 1.
  */
 int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides, const int64_t* out0_strides,
                  const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,
@@ -193,7 +197,20 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
                  const void* positions, int pos_bytes, int64_t pos_stride_b, int64_t pos_stride_s,
                  int pairing, double theta,
                  const float* freqs_cis, int64_t freq_rows, int64_t freq_row_stride,
-                 int conj, int32_t* error_flag, void* stream);
+                 int conj, int out_f32_mask, int32_t* error_flag, void* stream);
+
+/* ------------------------------------------------------------------------
+ * FSDP parameter unshard: n_seg (<= 16) column ranges of a row-strided bf16
+ * view src[shards, *] (row stride shard_stride) copied to contiguous outputs.
+ * Segment s covers columns [col_off[s], col_off[s] + col_len[s]) of every
+ * shard row and lands in dst[s] as a contiguous [shards, col_len[s]] block.
+ *
+ * Replaces the view -> split_with_sizes -> clone(contiguous_format) chains of
+ * the per-layer parameters in v8/94985bdb7630/problem.py (and
+ * v8/7815074de963, v8/12545c1e9b06, v8/8e33a91b7364), in one launch.
+ */
+int kp_unshard_bf16(const void* src, int64_t shards, int64_t shard_stride,
+                    const int64_t* col_off, const int64_t* col_len, void* const* dst, int n_seg, void* stream);
 
 #ifdef __cplusplus
 }

@@ -21,6 +21,7 @@ from .fused import (
     rms_norm_backward,
     rope,
     set_index_checking,
+    unshard,
 )
 
 __all__ = [
@@ -35,5 +36,6 @@ __all__ = [
     "rms_norm_backward",
     "rope",
     "set_index_checking",
+    "unshard",
     "version",
 ]

@@ -81,8 +81,9 @@ SIGNATURES = {
     "kp_rope_bf16": (
         i32,
         [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64,
-         i32, f64, vp, i64, i64, i32, vp, vp],
+         i32, f64, vp, i64, i64, i32, i32, vp, vp],
     ),
+    "kp_unshard_bf16": (i32, [vp, i64, i64, pi64, pi64, pvp, i32, vp]),
 }
 
 _lib = None

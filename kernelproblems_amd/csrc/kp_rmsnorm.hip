@@ -486,7 +486,7 @@ int env_int(const char* name, int dflt, int lo, int hi) {
 // Launch-shape tuning knobs (read once): KP_RMS_FWD_BPC / KP_RMS_BWD_BPC, row
 // blocks per CU for the forward / backward grids.
 int fwd_bpc() {
-  static const int v = env_int("KP_RMS_FWD_BPC", 8, 1, 64);
+  static const int v = env_int("KP_RMS_FWD_BPC", 2, 1, 64);
   return v;
 }
 int bwd_bpc() {
@@ -502,26 +502,31 @@ int wpr_min() {
   static const int v = env_int("KP_RMS_WPR_MIN", 1, 1, 4);
   return v;
 }
-int vpl_max() {
-  static const int v = env_int("KP_RMS_VPL_MAX", 5, 1, 8);
-  return v;
+// Measured defaults (MI355X): the forward keeps a whole row in one wave up
+// to 8 chunks per lane (N <= 4096; no cross-wave barrier), the backward --
+// which also holds per-column weight-gradient accumulators -- at most 5.
+// KP_RMS_VPL_MAX (tuning knob) overrides both.
+int vpl_max(bool forward, int64_t N) {
+  static const int v = env_int("KP_RMS_VPL_MAX", 0, 1, 8);
+  if (v) return v;
+  return (forward && N <= 4096) ? 8 : 5;
 }
 bool shape_ok(int vpl, int wpr) {
   switch (vpl * 10 + wpr) {
     case 11: case 21: case 31: case 41: case 51:
     case 12: case 22: case 32: case 42: case 52:
     case 14: case 24: case 34: case 44:
-    case 81: case 82: return true;
+    case 61: case 81: case 82: return true;
   }
   return false;
 }
-bool pick_vec(int64_t N, int* vpl, int* wpr) {
+bool pick_vec(int64_t N, bool forward, int* vpl, int* wpr) {
   if (N <= 0 || N % 512 != 0) return false;
   const int64_t k = N / 512;
   for (int pass = 0; pass < 2; ++pass) {
     for (int w : {1, 2, 4}) {
       if (pass == 0 && w < wpr_min()) continue;
-      if (k % w == 0 && k / w <= vpl_max() && shape_ok((int)(k / w), w)) {
+      if (k % w == 0 && k / w <= vpl_max(forward, N) && shape_ok((int)(k / w), w)) {
         *vpl = (int)(k / w);
         *wpr = w;
         return true;
@@ -578,6 +583,7 @@ BwdKernel bwd_for_terms(int nx, int ndy, bool res) {
     case 24: return FN<2, 4>(__VA_ARGS__);            \
     case 34: return FN<3, 4>(__VA_ARGS__);            \
     case 44: return FN<4, 4>(__VA_ARGS__);            \
+    case 61: return FN<6, 1>(__VA_ARGS__);            \
     case 81: return FN<8, 1>(__VA_ARGS__);            \
     case 82: return FN<8, 2>(__VA_ARGS__);            \
   }                                                   \
@@ -648,7 +654,7 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
   a.eps = eps;
 
   int vpl = 0, wpr = 0;
-  bool vec = pick_vec(N, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) && aligned16(y) && (y_stride & 7) == 0;
+  bool vec = pick_vec(N, true, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) && aligned16(y) && (y_stride & 7) == 0;
   if (vec && h_out) vec = aligned16(h_out) && (h_stride & 7) == 0;
   if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
   const FwdKernel fk = vec ? fwd_kernel(vpl, wpr, n_x) : nullptr;
@@ -730,7 +736,7 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
   int blocks = 0;
   if (M > 0) {
     int vpl = 0, wpr = 0;
-    bool vec = pick_vec(N, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) &&
+    bool vec = pick_vec(N, false, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) &&
                rows_vec_ok(dy_terms, dy_strides, n_dy) && aligned16(dx) && (dx_stride & 7) == 0;
     if (vec && dx_residual) vec = aligned16(dx_residual) && (dxr_stride & 7) == 0;
     if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;

@@ -27,7 +27,8 @@ constexpr int kMaxHalf = 256;  // D <= 512
 
 struct RopeTensor {
   const uint16_t* x;
-  uint16_t* out;
+  void* out;  // bf16, or fp32 when out_f32
+  int out_f32;
   int64_t H;
   int64_t xs[3];  // b, s, h strides (elements)
   int64_t os[3];
@@ -47,6 +48,21 @@ struct RopeArgs {
   int conj;
   int32_t* err;
 };
+
+// Output element offset o of tensor T gets 8 (16-byte bf16 / 32-byte fp32) or 1 value.
+__device__ __forceinline__ void store8(const RopeTensor& T, int64_t o, const float* v) {
+  if (T.out_f32) {
+    float* p = static_cast<float*>(T.out) + o;
+    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+  } else {
+    st16(static_cast<uint16_t*>(T.out) + o, pack8(v));
+  }
+}
+__device__ __forceinline__ void store1(const RopeTensor& T, int64_t o, float v) {
+  if (T.out_f32) static_cast<float*>(T.out)[o] = v;
+  else static_cast<uint16_t*>(T.out)[o] = f_to_bf(v);
+}
 
 __device__ __forceinline__ void rot(float a, float b, float c, float s, float& oa, float& ob) {
   oa = a * c - b * s;
@@ -113,14 +129,14 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeArgs a) {
     for (int ti = 0; ti < a.nt; ++ti) {
       const RopeTensor& T = a.t[ti];
       const uint16_t* xb = T.x + b * T.xs[0] + s * T.xs[1];
-      uint16_t* ob = T.out + b * T.os[0] + s * T.os[1];
+      const int64_t ob = b * T.os[0] + s * T.os[1];  // output element offset of this position
       if constexpr (VEC) {
         if (a.pairing == KP_ROPE_HALF) {
           const int64_t nch = half / 8;  // chunks per half
           for (int64_t u = lane; u < T.H * nch; u += 64) {
             const int64_t h = u / nch, c = u % nch;
             const uint16_t* xp = xb + h * T.xs[2] + c * 8;
-            uint16_t* op = ob + h * T.os[2] + c * 8;
+            const int64_t oo = ob + h * T.os[2] + c * 8;
             float x1[8], x2[8], o1[8], o2[8];
             unpack8(ld16_stream(xp), x1);
             unpack8(ld16_stream(xp + half), x2);
@@ -138,15 +154,15 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeArgs a) {
               rot(x1[e], x2[e], cv, sgn * sv, o1[e], o2[e]);
               if (!ok) o1[e] = o2[e] = 0.f;
             }
-            st16(op, pack8(o1));
-            st16(op + half, pack8(o2));
+            store8(T, oo, o1);
+            store8(T, oo + half, o2);
           }
         } else {
           const int64_t nch = a.D / 8;  // chunks per head, 4 pairs each
           for (int64_t u = lane; u < T.H * nch; u += 64) {
             const int64_t h = u / nch, c = u % nch;
             const uint16_t* xp = xb + h * T.xs[2] + c * 8;
-            uint16_t* op = ob + h * T.os[2] + c * 8;
+            const int64_t oo = ob + h * T.os[2] + c * 8;
             float xv[8], o[8];
             unpack8(ld16_stream(xp), xv);
 #pragma unroll
@@ -163,7 +179,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeArgs a) {
               rot(xv[2 * q], xv[2 * q + 1], cv, sgn * sv, o[2 * q], o[2 * q + 1]);
               if (!ok) o[2 * q] = o[2 * q + 1] = 0.f;
             }
-            st16(op, pack8(o));
+            store8(T, oo, o);
           }
         }
       } else {
@@ -173,7 +189,7 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeArgs a) {
           const int64_t ia = a.pairing == KP_ROPE_HALF ? f : 2 * f;
           const int64_t ib = a.pairing == KP_ROPE_HALF ? f + half : 2 * f + 1;
           const uint16_t* xp = xb + h * T.xs[2];
-          uint16_t* op = ob + h * T.os[2];
+          const int64_t oo = ob + h * T.os[2];
           float cv, sv;
           if constexpr (TABLE) {
             cv = frow[2 * f];
@@ -185,8 +201,8 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeArgs a) {
           float oa, obv;
           rot(bf_to_f(xp[ia]), bf_to_f(xp[ib]), cv, sgn * sv, oa, obv);
           if (!ok) oa = obv = 0.f;
-          op[ia] = f_to_bf(oa);
-          op[ib] = f_to_bf(obv);
+          store1(T, oo + ia, oa);
+          store1(T, oo + ib, obv);
         }
       }
     }
@@ -220,7 +236,7 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
                  const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,
                  int64_t B, int64_t S, int64_t D, const void* positions, int pos_bytes, int64_t pos_stride_b,
                  int64_t pos_stride_s, int pairing, double theta, const float* freqs_cis, int64_t freq_rows,
-                 int64_t freq_row_stride, int conj, int32_t* error_flag, void* stream) {
+                 int64_t freq_row_stride, int conj, int out_f32_mask, int32_t* error_flag, void* stream) {
   static const char* who = "kp_rope_bf16";
   if (x0 == nullptr || out0 == nullptr || x0_strides == nullptr || out0_strides == nullptr)
     return fail(KP_EINVAL, "%s: tensor 0 needs x, out and strides", who);
@@ -236,12 +252,12 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
     return fail(KP_EINVAL, "%s: freqs_cis needs rows > 0 and row stride >= D/2", who);
 
   RopeArgs a{};
-  a.t[0] = RopeTensor{static_cast<const uint16_t*>(x0), static_cast<uint16_t*>(out0), H0,
+  a.t[0] = RopeTensor{static_cast<const uint16_t*>(x0), out0, out_f32_mask & 1, H0,
                       {x0_strides[0], x0_strides[1], x0_strides[2]},
                       {out0_strides[0], out0_strides[1], out0_strides[2]}};
   a.nt = 1;
   if (x1 != nullptr) {
-    a.t[1] = RopeTensor{static_cast<const uint16_t*>(x1), static_cast<uint16_t*>(out1), H1,
+    a.t[1] = RopeTensor{static_cast<const uint16_t*>(x1), out1, (out_f32_mask >> 1) & 1, H1,
                         {x1_strides[0], x1_strides[1], x1_strides[2]},
                         {out1_strides[0], out1_strides[1], out1_strides[2]}};
     a.nt = 2;

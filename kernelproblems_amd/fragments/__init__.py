@@ -1,0 +1,35 @@
+"""Per-fragment drop-ins for the reference's hot-path fragments.
+
+Each module ``<round>_<id>`` mirrors ``<round>/<id>/problem.py``: it exports
+``kernel_function(*inputs)`` with the inputs of that fragment's
+``Model.forward`` in the same order, returning the same outputs (dtype, shape,
+aliasing between views), and ``get_inputs()`` drawing inputs of the same
+shapes and strides.  ``load("v8/d8f596b3df34")`` returns the module.
+"""
+from __future__ import annotations
+
+import importlib
+
+FRAGMENTS = (
+    # RMSNorm forward
+    "v7/59f786beb25f", "v8/4b90e2d83144", "v8/f4e9e58fef73", "v7/215dd2e6a519", "v6/ac3fb0b7281f",
+    # residual add + RMSNorm forward (+ FSDP parameter unshard)
+    "v8/7884328a5557", "v8/8e33a91b7364", "v8/94985bdb7630", "v8/7815074de963",
+    # RMSNorm backward (+ gradient adds, + residual add recompute)
+    "v7/45990c83cfd6", "v8/d8f596b3df34", "v7/7f544ceb2120", "v7/ed20955ec34b", "v8/3c6c589cdf81",
+    # embedding forward / backward
+    "v7/1e49beb8a123", "v8/12545c1e9b06", "v7/a12a160cb11b",
+    # RoPE (interleaved complex, table) forward / backward
+    "v7/e29b92927600", "v8/493cad38cac9", "v8/c8c60d8f7015", "v8/97032595d968", "v7/0f38bc55457c",
+    "v7/5c65f62b0422", "v7/bfe872e373e4",
+)
+
+
+def module_name(fragment_id: str) -> str:
+    return fragment_id.replace("/", "_")
+
+
+def load(fragment_id: str):
+    if fragment_id not in FRAGMENTS:
+        raise KeyError(f"unknown fragment {fragment_id!r}")
+    return importlib.import_module(f"{__name__}.{module_name(fragment_id)}")

@@ -319,6 +319,8 @@ def rope(
     freqs_cis: Optional[torch.Tensor] = None,
     pairing: str = "half",
     conj: bool = False,
+    q_dtype: torch.dtype = torch.bfloat16,
+    k_dtype: torch.dtype = torch.bfloat16,
 ):
     """Rotary embedding of q (and k) laid out [B, S, H, D] (unit stride on D).
 
@@ -327,13 +329,18 @@ def rope(
     complex64 table ``freqs_cis`` whose last dim is D/2 (row p used for
     position p).  positions: [B, S] or [S] integer tensor, default s.
     pairing "half" = (i, i + D/2), "interleaved" = (2i, 2i+1).  conj=True
-    rotates by the conjugate (backward).  Returns contiguous (q_out, k_out).
+    rotates by the conjugate (backward).  q_dtype / k_dtype pick each
+    output's type, bf16 or fp32 (the fp32 rotation result without the final
+    rounding).  Returns contiguous (q_out, k_out).
     """
+    for dt in (q_dtype, k_dtype):
+        if dt not in (torch.bfloat16, torch.float32):
+            raise RuntimeError(f"rope: output dtype must be bfloat16 or float32, got {dt}")
     _need_gpu("rope q", q)
     dev = q.device
     q, qs = _rope_strides(q)
     B, S, Hq, D = q.shape
-    q_out = torch.empty((B, S, Hq, D), dtype=torch.bfloat16, device=dev)
+    q_out = torch.empty((B, S, Hq, D), dtype=q_dtype, device=dev)
     k_out = None
     k_args = [None, None, 0, None, None]
     if k is not None:
@@ -341,7 +348,7 @@ def rope(
         k, ks = _rope_strides(k)
         if k.shape[0] != B or k.shape[1] != S or k.shape[3] != D:
             raise RuntimeError("rope: q and k must agree on B, S and D")
-        k_out = torch.empty(k.shape, dtype=torch.bfloat16, device=dev)
+        k_out = torch.empty(k.shape, dtype=k_dtype, device=dev)
         k_args = [k.data_ptr(), k_out.data_ptr(), k.shape[2], L.i64_array(ks),
                   L.i64_array(list(k_out.stride()[:3]))]
     pos_ptr, pos_bytes, psb, pss = None, 0, 0, 0
@@ -382,7 +389,47 @@ def rope(
         q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(qs), L.i64_array(list(q_out.stride()[:3])),
         *k_args,
         B, S, D, pos_ptr, pos_bytes, psb, pss, mode, th, f_ptr, frows, frs, 1 if conj else 0,
+        (1 if q_dtype == torch.float32 else 0) | (2 if k is not None and k_dtype == torch.float32 else 0),
         _ptr(flag), _stream(dev),
     )
     _raise_if_flagged(flag, "rope")
     return q_out, k_out
+
+
+# ---------------------------------------------------------------- FSDP unshard
+def unshard(flat: torch.Tensor, shards: int, split_sizes: Sequence[int], keep: Sequence[int]):
+    """Contiguous copies of column segments of a sharded flat parameter buffer.
+
+    ``flat`` holds ``shards`` rows of equal length (a 1-D all-gather output or
+    a [shards, L] row-strided view); the row is split into ``split_sizes``.
+    Returns, for each index in ``keep``, a fresh contiguous [shards, size]
+    tensor -- the view -> split_with_sizes -> clone chain of an FSDP unshard,
+    done for all kept segments in one launch.
+    """
+    _need_gpu("unshard buffer", flat)
+    if flat.dim() == 1:
+        if flat.numel() % shards != 0:
+            raise RuntimeError(f"unshard: {flat.numel()} elements do not split into {shards} shards")
+        row_len = flat.numel() // shards
+        if flat.stride(0) != 1 and flat.numel() > 1:
+            flat = flat.contiguous()
+        stride = row_len
+    elif flat.dim() == 2 and flat.shape[0] == shards and (flat.stride(1) == 1 or flat.shape[1] == 1):
+        row_len, stride = flat.shape[1], flat.stride(0)
+    else:
+        raise RuntimeError(f"unshard: expected a 1-D buffer or a [{shards}, L] view, got {tuple(flat.shape)}")
+    if sum(split_sizes) != row_len:
+        raise RuntimeError(f"unshard: split sizes sum to {sum(split_sizes)}, shard row has {row_len}")
+    offs = [0]
+    for s in split_sizes:
+        offs.append(offs[-1] + s)
+    outs = [torch.empty((shards, split_sizes[i]), dtype=torch.bfloat16, device=flat.device) for i in keep]
+    for start in range(0, len(outs), 16):
+        sel = list(range(start, min(start + 16, len(outs))))
+        L.call(
+            "kp_unshard_bf16",
+            flat.data_ptr(), shards, stride,
+            L.i64_array([offs[keep[i]] for i in sel]), L.i64_array([split_sizes[keep[i]] for i in sel]),
+            L.ptr_array([outs[i].data_ptr() for i in sel]), len(sel), _stream(flat.device),
+        )
+    return outs

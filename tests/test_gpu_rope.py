@@ -73,3 +73,31 @@ def test_rope_out_of_table_position_flagged(gpu):
     freqs = torch.ones((3, 4), dtype=torch.complex64, device=gpu)
     with pytest.raises(IndexError):
         kp.rope(x, positions=torch.tensor([0, 1, 2, 3], device=gpu), freqs_cis=freqs, pairing="interleaved")
+
+
+@pytest.mark.parametrize("vec", [True, False])
+def test_rope_fp32_output(gpu, vec):
+    """fp32 outputs (v7/0f38bc55457c returns its q rotation unrounded): within
+    fp32 evaluation error of the fp64 rotation, and rounding them to bf16
+    gives exactly the bf16-output kernel's result."""
+    g = gen(77)
+    S, Hq, Hk, D, P = 48, 4, 2, 128 if vec else 6, 64
+    q = randn_bf16((1, S, Hq, D), g)
+    k = randn_bf16((1, S, Hk, D), g)
+    freqs = torch.complex(torch.randn(P, D // 2, generator=g), torch.randn(P, D // 2, generator=g))
+    pos = torch.randint(0, P, (1, S), generator=g)
+    qd, kd, fd, pd = q.to(gpu), k.to(gpu), freqs.to(gpu), pos.to(gpu)
+    q32, kb = kp.rope(qd, kd, positions=pd, freqs_cis=fd, pairing="interleaved", q_dtype=torch.float32)
+    qb, k32 = kp.rope(qd, kd, positions=pd, freqs_cis=fd, pairing="interleaved", k_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert q32.dtype == torch.float32 and kb.dtype == torch.bfloat16
+    assert torch.equal(q32.to(torch.bfloat16), qb) and torch.equal(k32.to(torch.bfloat16), kb)
+    for x, out in ((q, q32), (k, k32)):
+        xc = torch.view_as_complex(x.double().reshape(*x.shape[:-1], D // 2, 2))
+        f = freqs.to(torch.complex128)[pos[0]][None, :, None, :]
+        exact = torch.view_as_real(xc * f).reshape(x.shape)
+        # fp32 a*c - b*d: two rounded products and a rounded difference, each
+        # within 2^-24 relative, bounded by 2^-23 (|ac| + |bd|) <= 2^-23 |x||f|
+        pair = (2.0**-22 * xc.abs() * f.abs()).unsqueeze(-1).expand(*xc.shape, 2)
+        bound = pair.reshape(x.shape)
+        assert ((out.cpu().double() - exact).abs() <= bound).all()
