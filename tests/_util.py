@@ -78,3 +78,40 @@ def zipf_ids(n: int, vocab: int, s: float, g: torch.Generator) -> torch.Tensor:
     p = r.pow(-s)
     p /= p.sum()
     return torch.multinomial(p, n, replacement=True, generator=g).to(torch.int64)
+
+
+_BF16_TABLE = None
+
+
+def bf16_round_exact(v: np.ndarray) -> np.ndarray:
+    """Correctly rounded (nearest, ties to even) float64 -> bf16 bit patterns,
+    by search over the sorted table of all finite bf16 values; saturates to
+    +-inf beyond the largest finite value's rounding boundary.  Independent
+    of any float32 intermediate (no double rounding)."""
+    global _BF16_TABLE
+    if _BF16_TABLE is None:
+        pats = np.arange(0x10000, dtype=np.uint32).astype(np.uint16)
+        with np.errstate(invalid="ignore"):
+            vals = bf(pats)
+        keep = np.isfinite(vals) & ~((pats == 0x8000))  # one zero
+        order = np.argsort(vals[keep], kind="stable")
+        _BF16_TABLE = (vals[keep][order], pats[keep][order])
+    tv, tp = _BF16_TABLE
+    v = np.asarray(v, dtype=np.float64).ravel()
+    out = np.empty(v.shape, dtype=np.uint16)
+    hi_i = np.clip(np.searchsorted(tv, v, side="left"), 1, len(tv) - 1)
+    lo_i = hi_i - 1
+    lo, hi = tv[lo_i], tv[hi_i]
+    d_lo, d_hi = v - lo, hi - v
+    pick_hi = (d_hi < d_lo) | ((d_hi == d_lo) & ((tp[hi_i] & 1) == 0))
+    res = np.where(pick_hi, tp[hi_i], tp[lo_i])
+    exact = np.isin(v, tv)
+    res = np.where(exact, tp[np.clip(np.searchsorted(tv, v), 0, len(tv) - 1)], res)
+    # beyond the largest finite value: overflow boundary is max + half an ulp
+    big = 3.3895313892515355e38  # 0x7F7F
+    ulp = 2.0 ** (127 - 7)
+    res = np.where(v >= big + ulp / 2, 0x7F80, res)
+    res = np.where(v <= -(big + ulp / 2), 0xFF80, res)
+    res = np.where(v == 0, np.where(np.signbit(v), 0x8000, 0x0000), res)
+    out[:] = res
+    return out.reshape(np.shape(v))

@@ -1,0 +1,107 @@
+"""The C ABI without a GPU: include/kp.h, the ctypes table in
+kernelproblems_amd/_lib.py and the exports of libkp_hip.so agree one for
+one, and argument validation returns its error codes (with a message)
+before anything touches a device."""
+import ctypes as C
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from kernelproblems_amd import _lib as L
+
+ROOT = Path(__file__).resolve().parent.parent
+HEADER = ROOT / "include" / "kp.h"
+_DECL = re.compile(r"^(?:int|size_t|const char\*|void)\s+(kp_\w+)\(([^;]*?)\);", re.M | re.S)
+
+
+def _declarations():
+    text = HEADER.read_text()
+    out = {}
+    for name, params in _DECL.findall(text):
+        params = " ".join(params.split())
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not L.LIB_PATH.exists():
+        from kernelproblems_amd import build
+        build.build()
+    return L.lib()
+
+
+def test_header_matches_ctypes_table():
+    decl = _declarations()
+    assert decl, "no declarations parsed"
+    assert set(decl) == set(L.SIGNATURES), set(decl) ^ set(L.SIGNATURES)
+    for name, n in decl.items():
+        assert len(L.SIGNATURES[name][1]) == n, f"{name}: header has {n} parameters"
+
+
+def test_library_exports_every_declared_symbol(lib):
+    out = subprocess.run(["nm", "-D", "--defined-only", str(L.LIB_PATH)], capture_output=True, text=True, check=True)
+    exported = {line.split()[-1] for line in out.stdout.splitlines() if " T " in line}
+    missing = set(_declarations()) - exported
+    assert not missing, missing
+    for name in _declarations():
+        assert getattr(lib, name) is not None
+
+
+def test_version(lib):
+    assert "gfx950" in L.version()
+
+
+def _expect(lib, status, fn, *args):
+    st = getattr(lib, fn)(*args)
+    assert st == status, (fn, st, lib.kp_last_error_message())
+    assert fn.encode() in lib.kp_last_error_message()
+
+
+def test_rmsnorm_validation(lib):
+    one = L.i64_array([8])
+    _expect(lib, L.KP_EINVAL, "kp_rmsnorm_fwd_bf16", None, one, 0, None, 8, 8, None, 8, None, 8, None, 4, 8,
+            1e-5, None)  # no input terms
+    _expect(lib, L.KP_EINVAL, "kp_rmsnorm_fwd_bf16", L.ptr_array([None]), one, 1, None, 8, 8, None, 8, None, 8,
+            None, 4, 8, 1e-5, None)  # NULL term with rows to do
+    ptr = L.ptr_array([16])
+    _expect(lib, L.KP_EWORKSPACE, "kp_rmsnorm_bwd_bf16", ptr, one, 1, ptr, one, 1, None, 16, 8, 8, None, 8, 16, 8,
+            32, None, 0, 4, 8, 1e-5, 32, 1, None)  # dw requested, 1-byte workspace
+    assert lib.kp_rmsnorm_bwd_workspace_size(8192, 4096) >= 4096 * 4
+
+
+def test_embedding_validation(lib):
+    _expect(lib, L.KP_EINVAL, "kp_embedding_fwd_bf16", 16, 10, 8, 8, 32, 3, 4, 48, 8, None, None)  # 3-byte ids
+    ws = lib.kp_embedding_bwd_workspace_size(40000, 1000, 64)
+    _expect(lib, L.KP_EUNSUPPORTED, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 40000, 1000, 64, -1, 0, 48,
+            L.KP_DTYPE_F32, 0, 64, max(ws, 1), None, None)  # more tokens than one sort handles
+    _expect(lib, L.KP_EINVAL, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 100, 1000, 64, -1, 0, 48, 7, 0, 64,
+            1 << 20, None, None)  # unknown output dtype
+
+
+def test_rope_validation(lib):
+    st = L.i64_array([0, 0, 0])
+    common = (1, 1)  # B, S
+    _expect(lib, L.KP_EINVAL, "kp_rope_bf16", 16, 32, 1, st, st, None, None, 0, None, None, *common, 7, None, 0, 0,
+            0, 0, 1e4, None, 0, 0, 0, 0, None, None)  # odd head dim
+    _expect(lib, L.KP_EINVAL, "kp_rope_bf16", 16, 32, 1, st, st, None, None, 0, None, None, *common, 8, None, 0, 0,
+            0, 0, -1.0, None, 0, 0, 0, 0, None, None)  # theta <= 0 without a table
+    _expect(lib, L.KP_EINVAL, "kp_rope_bf16", 16, 32, 1, st, st, None, None, 0, None, None, *common, 8, None, 0, 0,
+            0, 5, 1e4, None, 0, 0, 0, 0, None, None)  # unknown pairing
+
+
+def test_unshard_validation(lib):
+    off, ln = L.i64_array([0] * 17), L.i64_array([8] * 17)
+    _expect(lib, L.KP_EINVAL, "kp_unshard_bf16", 16, 8, 64, off, ln, L.ptr_array([32] * 17), 17, None)
+    off2, ln2 = L.i64_array([60]), L.i64_array([8])
+    _expect(lib, L.KP_EINVAL, "kp_unshard_bf16", 16, 8, 64, off2, ln2, L.ptr_array([32]), 1, None)  # past the row
+
+
+def test_empty_work_is_ok_without_device(lib):
+    """Zero rows / positions / segments return KP_OK without a launch."""
+    one = L.i64_array([8])
+    assert lib.kp_rmsnorm_fwd_bf16(L.ptr_array([None]), one, 1, None, 8, 8, None, 8, None, 8, None, 0, 8, 1e-5,
+                                   None) == L.KP_OK
+    assert lib.kp_unshard_bf16(None, 8, 64, None, None, None, 0, None) == L.KP_OK

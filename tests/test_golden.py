@@ -1,0 +1,124 @@
+"""The oracle (CPU) and the HIP kernels (GPU) against the committed golden
+vectors of tests/golden/golden.npz (made by tests/golden/make_golden.py with
+torch library ops in float64)."""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from tests._util import bf, from_u16, ulp_bf16
+
+G = np.load(Path(__file__).resolve().parent / "golden" / "golden.npz")
+
+
+def _check_rms_fwd(y, rstd, tag, exact_ulps=1):
+    u = ulp_bf16(y, G[f"{tag}_y"])
+    assert u.max() <= exact_ulps, u.max()
+    np.testing.assert_allclose(rstd, G[f"{tag}_rstd"], rtol=4 * 2.0**-24)
+
+
+def _check_dx(dx, exact):
+    assert np.all(np.abs(bf(dx) - exact) <= 2.0**-8 * np.abs(exact) + 1e-5 * np.abs(exact).max())
+
+
+def _dw_bound(rstd):
+    x = bf(G["rms_x"])
+    return 2.0**-22 * (np.abs(bf(G["rms_dy"]) * x) * np.abs(rstd)[:, None]).sum(0) + 1e-9
+
+
+def _check_emb_bwd(dense):
+    exact, absd = G["emb_bwd"], G["emb_bwd_abs"]
+    counts = np.bincount(G["emb_ids"][G["emb_ids"] != G["emb_pad"]], minlength=exact.shape[0])[:, None]
+    # fp32 accumulation: within (count + 1) * 2^-24 * sum|g| of the fp64 sum
+    assert np.all(np.abs(dense.astype(np.float64) - exact) <= (counts + 1) * 2.0**-24 * absd)
+    assert not dense[int(G["emb_pad"])].any()
+
+
+def _check_rope(out_u16, exact):
+    ov = bf(out_u16)
+    # one bf16 rounding; the angle reduction and fp32 evaluation add < 1e-5 absolute
+    assert np.all(np.abs(ov - exact) <= 2.0**-8 * np.abs(exact) + 1e-5)
+
+
+# ---------------------------------------------------------------- CPU: oracle
+def test_oracle_rms_fwd_golden():
+    eps = float(G["rms_eps"])
+    _, y, r = oracle.rmsnorm_fwd([G["rms_x"]], G["rms_w"], eps, G["rms_x"].shape[1])
+    _check_rms_fwd(y, r, "rms", exact_ulps=0)
+    h, y, r = oracle.rmsnorm_fwd([G["rms_res"], G["rms_x"]], G["rms_w"], eps, G["rms_x"].shape[1])
+    assert np.array_equal(h, G["rms_h"])
+    _check_rms_fwd(y, r, "addrms", exact_ulps=0)
+
+
+def test_oracle_rms_bwd_golden():
+    eps, N = float(G["rms_eps"]), G["rms_x"].shape[1]
+    dx, dw, r = oracle.rmsnorm_bwd([G["rms_dy"]], [G["rms_x"]], None, G["rms_w"], eps, N)
+    _check_dx(dx, G["rmsbwd_dx"])
+    assert np.all(np.abs(dw - G["rmsbwd_dw"]) <= _dw_bound(r))
+    dx, dw, _ = oracle.rmsnorm_bwd([G["rms_dy"]], [G["rms_x"]], G["rmsbwd_given_rstd"], G["rms_w"], eps, N)
+    _check_dx(dx, G["rmsbwd_given_dx"])
+    np.testing.assert_allclose(dw, G["rmsbwd_given_dw"], rtol=1e-12, atol=1e-12)
+
+
+def test_oracle_embedding_golden():
+    out, bad = oracle.embedding_fwd(G["emb_table"], G["emb_ids"])
+    assert bad == 0 and np.array_equal(out, G["emb_fwd"])
+    dense = oracle.embedding_bwd_dense(G["emb_grad"], G["emb_ids"], G["emb_table"].shape[0], int(G["emb_pad"]))
+    _check_emb_bwd(dense)
+
+
+def test_oracle_rope_golden():
+    out = oracle.rope(G["rope_x"], G["rope_pos"], pairing="half", theta=float(G["rope_theta"]))
+    _check_rope(out, G["rope_half"])
+    out = oracle.rope(G["rope_x"], G["rope_tpos"], pairing="interleaved", freqs=G["rope_table"])
+    _check_rope(out, G["rope_inter"])
+
+
+# ---------------------------------------------------------------- GPU: kernels
+@pytest.mark.gpu
+def test_kernels_rms_golden(gpu):
+    import kernelproblems_amd as kp
+
+    eps, N = float(G["rms_eps"]), G["rms_x"].shape[1]
+    x, res, dy, w = (from_u16(G[k], gpu) for k in ("rms_x", "rms_res", "rms_dy", "rms_w"))
+    _, y, r = kp.rms_norm([x], w, eps, N)
+    _check_rms_fwd(y.cpu().view(torch.int16).numpy().view(np.uint16), r.cpu().numpy(), "rms")
+    h, y, r = kp.rms_norm([res, x], w, eps, N, return_h=True)
+    assert np.array_equal(h.cpu().view(torch.int16).numpy().view(np.uint16), G["rms_h"])
+    _check_rms_fwd(y.cpu().view(torch.int16).numpy().view(np.uint16), r.cpu().numpy(), "addrms")
+    dx, dw = kp.rms_norm_backward([dy], [x], None, w, eps, N)
+    _check_dx(dx.cpu().view(torch.int16).numpy().view(np.uint16), G["rmsbwd_dx"])
+    _, _, r = kp.rms_norm([x], w, eps, N)
+    assert np.all(np.abs(dw.cpu().double().numpy() - G["rmsbwd_dw"]) <= _dw_bound(r.cpu().numpy()))
+    rs = torch.from_numpy(G["rmsbwd_given_rstd"]).to(gpu)
+    dx, dw = kp.rms_norm_backward([dy], [x], rs, w, eps, N)
+    _check_dx(dx.cpu().view(torch.int16).numpy().view(np.uint16), G["rmsbwd_given_dx"])
+    ex = G["rmsbwd_given_dw"]
+    mag = (np.abs(bf(G["rms_dy"]) * bf(G["rms_x"])) * np.abs(G["rmsbwd_given_rstd"])[:, None]).sum(0)
+    assert np.all(np.abs(dw.cpu().double().numpy() - ex) <= 2.0**-20 * mag)
+
+
+@pytest.mark.gpu
+def test_kernels_embedding_golden(gpu):
+    import kernelproblems_amd as kp
+
+    table, grad = from_u16(G["emb_table"], gpu), from_u16(G["emb_grad"], gpu)
+    ids = torch.from_numpy(G["emb_ids"]).to(gpu)
+    out = kp.embedding(table, ids)
+    assert np.array_equal(out.cpu().view(torch.int16).numpy().view(np.uint16), G["emb_fwd"])
+    dense = kp.embedding_dense_backward(grad, ids, table.shape[0], int(G["emb_pad"]))
+    _check_emb_bwd(dense.cpu().numpy())
+
+
+@pytest.mark.gpu
+def test_kernels_rope_golden(gpu):
+    import kernelproblems_amd as kp
+
+    x = from_u16(G["rope_x"], gpu)
+    out, _ = kp.rope(x, positions=torch.from_numpy(G["rope_pos"]).to(gpu), theta=float(G["rope_theta"]))
+    _check_rope(out.cpu().view(torch.int16).numpy().view(np.uint16), G["rope_half"])
+    tab = torch.from_numpy(G["rope_table"]).to(gpu)
+    out, _ = kp.rope(x, positions=torch.from_numpy(G["rope_tpos"]).to(gpu), freqs_cis=tab, pairing="interleaved")
+    _check_rope(out.cpu().view(torch.int16).numpy().view(np.uint16), G["rope_inter"])
