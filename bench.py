@@ -20,9 +20,10 @@ Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 find its operands in cache from the previous call.  The timed loop calls the
 C ABI directly through pre-bound ctypes arguments.  value = algorithmic
 bytes per call * steps / wall time.  roofline.achieved = the dominant
-kernel's algorithmic bytes / its mean duration, timed with HIP events that
-the library records around that kernel (kp_profile_dominant_kernel) in the
-same timed loop.  The cpu_baseline is the torch CPU eager restatement of the
+kernel's algorithmic bytes / its mean duration, timed in the same loop with
+HIP events that the library has the runtime stamp at that kernel's own start
+and completion (kp_profile_dominant_kernel -> hipExtLaunchKernel), on the
+stream the kernel runs on.  The cpu_baseline is the torch CPU eager restatement of the
 fragment (oracle/torch_ref.py) on the same seeded inputs.
 """
 from __future__ import annotations

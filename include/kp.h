@@ -51,11 +51,12 @@ int kp_last_hip_error(void);
 const char* kp_last_error_message(void);
 
 /* Benchmark timing hook (no counterpart in the reference, whose timing lives
- * in an external harness).  While set, every entry point records start_event
- * (a hipEvent_t) immediately before and stop_event immediately after the
- * launch of its dominant kernel, on the call's stream: the row kernel of the
- * RMSNorm entry points, the gather kernel of kp_embedding_fwd_bf16, the
- * dense-write kernel of kp_embedding_bwd_bf16 and the kernel of kp_rope_bf16.
+ * in an external harness).  While set, every entry point launches its
+ * dominant kernel with hipExtLaunchKernel, which stamps start_event and
+ * stop_event (hipEvent_t, timing enabled) at that kernel's own start and
+ * completion: the row kernel of the RMSNorm entry points, the gather kernel
+ * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
+ * the kernel of kp_rope_bf16 and the copy kernel of kp_unshard_bf16.
  * Pass NULL, NULL to clear.  Per calling thread. */
 void kp_profile_dominant_kernel(void* start_event, void* stop_event);
 
@@ -143,15 +144,16 @@ int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table
  * at v7/a12a160cb11b/problem.py:16-20, following the decomposition
  * torch/_decomp/decompositions.py:1245-1275.
  *
- * Deterministic sort-and-segment: (id, t) keys are sorted, each id's
- * contributions are summed in ascending t, in fixed-size runs whose fp32
- * partial sums are then added in run order.  No float atomics; the result is
- * bitwise reproducible run to run.
+ * Deterministic sort-and-segment: (id, t) keys are sorted; the sorted order
+ * is cut into windows of 32 keys, each id's contributions inside a window are
+ * summed in fp32 in ascending t, and an id whose keys span several windows
+ * adds its window partial sums in window order.  No float atomics; the result
+ * is bitwise reproducible run to run.
  * grad: bf16 [T, D] with row stride grad_row_stride.  indices as above.
  * grad_table: [V, D] contiguous, out_dtype KP_DTYPE_F32 or KP_DTYPE_BF16; with
  *   KP_DTYPE_F32 and out_round_bf16 != 0 every value is first rounded to bf16.
  * padding_idx < 0 means none.  Out-of-range ids are skipped and flagged.
- * Limits of this build: T <= 32768 and ceil(log2 V) + ceil(log2 T) <= 32
+ * Limits of this build: T <= 32768 and ceil(log2 V) + ceil(log2 T) <= 31
  *   (KP_EUNSUPPORTED otherwise).
  */
 size_t kp_embedding_bwd_workspace_size(int64_t T, int64_t V, int64_t D);

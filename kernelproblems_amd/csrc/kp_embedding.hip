@@ -535,10 +535,8 @@ int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table
   const int64_t cap = (int64_t)cu_count() * 16;
   const int grid = (int)(blocks_needed < cap ? blocks_needed : cap);
   hipStream_t s = as_stream(stream);
-  prof_begin(s);
-  if (vec) hipLaunchKernelGGL(emb_fwd<true>, dim3(grid), dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL(emb_fwd<false>, dim3(grid), dim3(kThreads), 0, s, a);
-  prof_end(s);
+  if (vec) KP_LAUNCH_DOMINANT(emb_fwd<true>, dim3(grid), dim3(kThreads), 0, s, a);
+  else KP_LAUNCH_DOMINANT(emb_fwd<false>, dim3(grid), dim3(kThreads), 0, s, a);
   return check_launch(who);
 }
 
@@ -610,10 +608,8 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   const int64_t n_win_blocks = L.nwin * nq;
   const int64_t dense_blocks = n_win_blocks + V * nq;
   if (dense_blocks > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: V * D too large for one launch", who);
-  prof_begin(s);
-  if (vec) hipLaunchKernelGGL(emb_dense<true>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
-  else hipLaunchKernelGGL(emb_dense<false>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
-  prof_end(s);
+  if (vec) KP_LAUNCH_DOMINANT(emb_dense<true>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
+  else KP_LAUNCH_DOMINANT(emb_dense<false>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
   const int grid = cu_count() * 4;
   if ((st = check_launch(who)) != KP_OK) return st;
   if (vec) hipLaunchKernelGGL(emb_combine<true>, dim3(grid), dim3(kThreads), 0, s, a);

@@ -1,6 +1,7 @@
 // Host-side helpers shared by the C-ABI entry points (not part of the ABI).
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stddef.h>
 #include <stdint.h>
@@ -16,13 +17,26 @@ int check_launch(const char* what);
 // Number of compute units of the current device (cached per device ordinal).
 int cu_count();
 
-// Timing hook (kp_profile_dominant_kernel): record the caller's events right
-// before / after the dominant kernel launch of an entry point.
-void prof_begin(hipStream_t s);
-void prof_end(hipStream_t s);
+// Timing hook (kp_profile_dominant_kernel): the caller's events, or nullptr.
+hipEvent_t prof_start_event();
+hipEvent_t prof_stop_event();
+
+// Launches an entry point's dominant kernel.  With timing events set, the
+// launch goes through hipExtLaunchKernel, which stamps the events at the
+// kernel's own start and completion, so they time that kernel alone.
+void launch_dominant_raw(const void* fn, dim3 grid, dim3 block, void** args, size_t shmem, hipStream_t s);
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 }  // namespace kp
+
+#define KP_LAUNCH_DOMINANT(kernel, grid, block, shmem, stream, ...)                                       \
+  do {                                                                                                  \
+    hipEvent_t kp_ev_a_ = ::kp::prof_start_event(), kp_ev_b_ = ::kp::prof_stop_event();               \
+    if (kp_ev_a_ && kp_ev_b_)                                                                           \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, kp_ev_a_, kp_ev_b_, 0, __VA_ARGS__);    \
+    else                                                                                                \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                              \
+  } while (0)

@@ -666,15 +666,11 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
     const int64_t cap = (int64_t)cu_count() * fwd_bpc();
     const int grid = (int)(groups < cap ? groups : cap);
     void* args[] = {&a};
-    prof_begin(s);
-    (void)hipLaunchKernel(reinterpret_cast<const void*>(fk), dim3(grid), dim3(kThreads), args, 0, s);
-    prof_end(s);
+    launch_dominant_raw(reinterpret_cast<const void*>(fk), dim3(grid), dim3(kThreads), args, 0, s);
   } else {
     const int64_t cap = (int64_t)cu_count() * 8;
     const int grid = (int)(M < cap ? M : cap);
-    prof_begin(s);
-    hipLaunchKernelGGL(rms_fwd_generic, dim3(grid), dim3(kThreads), 0, s, a);
-    prof_end(s);
+    KP_LAUNCH_DOMINANT(rms_fwd_generic, dim3(grid), dim3(kThreads), 0, s, a);
   }
   return check_launch(who);
 }
@@ -746,14 +742,10 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
       blocks = bwd_blocks(M, 4 / wpr);
       const size_t lds = (want_dw && wpr < 4) ? (size_t)2 * 512 * vpl * sizeof(float) : 0;
       void* args[] = {&a};
-      prof_begin(s);
-      (void)hipLaunchKernel(reinterpret_cast<const void*>(bk), dim3(blocks), dim3(kThreads), args, lds, s);
-      prof_end(s);
+      launch_dominant_raw(reinterpret_cast<const void*>(bk), dim3(blocks), dim3(kThreads), args, lds, s);
     } else {
       blocks = bwd_blocks(M, 1);
-      prof_begin(s);
-      hipLaunchKernelGGL(rms_bwd_generic, dim3(blocks), dim3(kThreads), 0, s, a);
-      prof_end(s);
+      KP_LAUNCH_DOMINANT(rms_bwd_generic, dim3(blocks), dim3(kThreads), 0, s, a);
     }
     st = check_launch(who);
     if (st != KP_OK) return st;

@@ -285,12 +285,10 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
   const int grid = (int)(blocks_needed < cap ? blocks_needed : cap);
   hipStream_t s = as_stream(stream);
   const bool tab = freqs_cis != nullptr;
-  prof_begin(s);
-  if (vec && tab) hipLaunchKernelGGL((rope_kernel<true, true>), dim3(grid), dim3(kThreads), 0, s, a);
-  else if (vec) hipLaunchKernelGGL((rope_kernel<true, false>), dim3(grid), dim3(kThreads), 0, s, a);
-  else if (tab) hipLaunchKernelGGL((rope_kernel<false, true>), dim3(grid), dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL((rope_kernel<false, false>), dim3(grid), dim3(kThreads), 0, s, a);
-  prof_end(s);
+  if (vec && tab) KP_LAUNCH_DOMINANT((rope_kernel<true, true>), dim3(grid), dim3(kThreads), 0, s, a);
+  else if (vec) KP_LAUNCH_DOMINANT((rope_kernel<true, false>), dim3(grid), dim3(kThreads), 0, s, a);
+  else if (tab) KP_LAUNCH_DOMINANT((rope_kernel<false, true>), dim3(grid), dim3(kThreads), 0, s, a);
+  else KP_LAUNCH_DOMINANT((rope_kernel<false, false>), dim3(grid), dim3(kThreads), 0, s, a);
   return check_launch(who);
 }
 

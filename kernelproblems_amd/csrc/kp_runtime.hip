@@ -33,11 +33,14 @@ int check_launch(const char* what) {
   return fail(KP_EHIP, "%s: %s", what, hipGetErrorString(e));
 }
 
-void prof_begin(hipStream_t s) {
-  if (t_prof_start) (void)hipEventRecord(t_prof_start, s);
-}
-void prof_end(hipStream_t s) {
-  if (t_prof_stop) (void)hipEventRecord(t_prof_stop, s);
+hipEvent_t prof_start_event() { return t_prof_start; }
+hipEvent_t prof_stop_event() { return t_prof_stop; }
+
+void launch_dominant_raw(const void* fn, dim3 grid, dim3 block, void** args, size_t shmem, hipStream_t s) {
+  if (t_prof_start && t_prof_stop)
+    (void)hipExtLaunchKernel(fn, grid, block, args, shmem, s, t_prof_start, t_prof_stop, 0);
+  else
+    (void)hipLaunchKernel(fn, grid, block, args, shmem, s);
 }
 
 int cu_count() {

@@ -77,9 +77,7 @@ extern "C" int kp_unshard_bf16(const void* src, int64_t shards, int64_t shard_st
   if (blocks == 0) return KP_OK;
   if (blocks > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: too many blocks", who);
   hipStream_t s = as_stream(stream);
-  prof_begin(s);
-  if (vec) hipLaunchKernelGGL(unshard_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL(unshard_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
-  prof_end(s);
+  if (vec) KP_LAUNCH_DOMINANT(unshard_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
+  else KP_LAUNCH_DOMINANT(unshard_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
   return check_launch(who);
 }
