@@ -19,11 +19,12 @@ Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 ~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
 find its operands in cache from the previous call.  The timed loop calls the
 C ABI directly through pre-bound ctypes arguments.  value = algorithmic
-bytes per call * steps / wall time.  roofline.achieved = the dominant
-kernel's algorithmic bytes / its mean duration, timed in the same loop with
-HIP events that the library has the runtime stamp at that kernel's own start
-and completion (kp_profile_dominant_kernel -> hipExtLaunchKernel), on the
-stream the kernel runs on.  The cpu_baseline is the torch CPU eager restatement of the
+bytes per call * steps / wall time of the timed loop (synchronised on both
+sides, no per-kernel instrumentation inside).  roofline.achieved = the
+dominant kernel's algorithmic bytes / its mean duration, from a second pass
+over K steps with HIP events that the library has the runtime stamp at that
+kernel's own start and completion (kp_profile_dominant_kernel ->
+hipExtLaunchKernel), on the stream the kernel runs on.  The cpu_baseline is the torch CPU eager restatement of the
 fragment (oracle/torch_ref.py) on the same seeded inputs.
 """
 from __future__ import annotations
@@ -320,28 +321,37 @@ ALL = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
 
 # ------------------------------------------------------------------ measure
 def measure_gpu(wl, steps, warmup):
+    """Two passes over the same K steps: the timed pass (wall clock and HIP
+    events around the whole loop, no per-kernel hooks) gives value and
+    ms_per_step; a second pass with the timing hook set gives the dominant
+    kernel's per-launch durations (events stamped at its own start / end)."""
     import torch
     from kernelproblems_amd import _lib as L
     lib = L.lib()
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for e in starts + stops:  # materialise the hipEvent_t handles
-        e.record()
     t0e, t1e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
     t0e.record()
     for i in range(steps):
-        lib.kp_profile_dominant_kernel(starts[i].cuda_event, stops[i].cuda_event)
         wl.step(warmup + i)
-    lib.kp_profile_dominant_kernel(None, None)
     t1e.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     gpu_ms = t0e.elapsed_time(t1e)
+
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in starts + stops:  # materialise the hipEvent_t handles
+        e.record()
+    torch.cuda.synchronize()
+    for i in range(steps):
+        lib.kp_profile_dominant_kernel(starts[i].cuda_event, stops[i].cuda_event)
+        wl.step(warmup + steps + i)
+    lib.kp_profile_dominant_kernel(None, None)
+    torch.cuda.synchronize()
     dom = [starts[i].elapsed_time(stops[i]) for i in range(steps)]
     dom_ms = sum(dom) / len(dom)
     ms_per_step = wall * 1e3 / steps

@@ -106,6 +106,62 @@ __device__ __forceinline__ void load_weight(u32x4 (&wv)[VPL], const uint16_t* w,
 }
 
 // ------------------------------------------------------------------ forward
+// One row (this wave's column segment of it): bf16 term sum, sum of squares,
+// cross-wave combine, y = bf16(h * rstd * w), optional h and rstd stores.
+template <int VPL, int WPR, int NX>
+__device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, NX>& cur, u32x4 (&wv)[VPL],
+                                        float (&red)[2][4], int64_t row, int64_t col, int lane, int wave, int part,
+                                        int rloc, int it) {
+  const bool valid = row < a.M;
+  u32x4 hv[VPL];
+  sum_raw<VPL, NX>(hv, cur);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    float f[8];
+    unpack8(hv[i], f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
+  }
+  ss = wave_sum(ss);
+  if constexpr (WPR > 1) {
+    if (lane == 0) red[it & 1][wave] = ss;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int p = 0; p < WPR; ++p) t += red[it & 1][rloc * WPR + p];
+    ss = t;
+  }
+  const float r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) reg_barrier(hv[i]);
+  if (valid) {
+    uint16_t* yrow = a.y + row * a.ys + col;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float f[8], wf[8], o[8];
+      unpack8(hv[i], f);
+      unpack8(wv[i], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = (f[e] * r) * wf[e];
+      st16(yrow + i * 512, pack8(o));
+    }
+    if (NX > 1 && a.h != nullptr) {
+      uint16_t* hrow = a.h + row * a.hs + col;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) st16(hrow + i * 512, hv[i]);
+    }
+    if (a.rstd != nullptr && part == 0 && lane == 0) a.rstd[row] = r;
+  }
+}
+
+// Blocks walk the row groups grid-stride (measured faster on gfx950 than
+// contiguous per-block ranges for these row loops) with one row group of loads
+// in flight ahead of the one being reduced.  The two register slots are
+// separate named variables (an array of slots indexed by the step ends up in
+// scratch memory); for WPR < 4 the loop is unrolled two steps per pass.
 template <int VPL, int WPR, int NX>
 __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   constexpr int RB = 4 / WPR;
@@ -118,63 +174,38 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   u32x4 wv[VPL];
   load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
 
-  // Blocks walk the row groups grid-stride (measured faster on gfx950 than
-  // contiguous per-block ranges for these row loops).
   const int64_t ngroups = ceil_div_dev(a.M, RB);
-  int64_t g = blockIdx.x;
-  RawRow<VPL, NX> cur;
-  load_raw<VPL, NX>(cur, a.x, a.xs, g * RB + rloc, col, g < ngroups && g * RB + rloc < a.M);
-  for (int it = 0; g < ngroups; g += gridDim.x, ++it) {
-    const int64_t row = g * RB + rloc;
-    const bool valid = row < a.M;
-    const int64_t gn = g + gridDim.x, rown = gn * RB + rloc;
-    RawRow<VPL, NX> nxt;
-    load_raw<VPL, NX>(nxt, a.x, a.xs, rown, col, gn < ngroups && rown < a.M);
-
-    u32x4 hv[VPL];
-    sum_raw<VPL, NX>(hv, cur);
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      float f[8];
-      unpack8(hv[i], f);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
-    }
-    ss = wave_sum(ss);
-    if constexpr (WPR > 1) {
-      if (lane == 0) red[it & 1][wave] = ss;
-      __syncthreads();
-      float t = 0.f;
-#pragma unroll
-      for (int p = 0; p < WPR; ++p) t += red[it & 1][rloc * WPR + p];
-      ss = t;
-    }
-    const float r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) reg_barrier(hv[i]);
-    if (valid) {
-      uint16_t* yrow = a.y + row * a.ys + col;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        float f[8], wf[8], o[8];
-        unpack8(hv[i], f);
-        unpack8(wv[i], wf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (f[e] * r) * wf[e];
-        st16(yrow + i * 512, pack8(o));
-      }
-      if (NX > 1 && a.h != nullptr) {
-        uint16_t* hrow = a.h + row * a.hs + col;
-#pragma unroll
-        for (int i = 0; i < VPL; ++i) st16(hrow + i * 512, hv[i]);
-      }
-      if (a.rstd != nullptr && part == 0 && lane == 0) a.rstd[row] = r;
-    }
-    cur = nxt;
+  const int64_t G = gridDim.x;
+  RawRow<VPL, NX> s0, s1;
+  int it = 0;
+#define KP_ROW(g) ((g) * RB + rloc)
+#define KP_LOAD(S, g) load_raw<VPL, NX>(S, a.x, a.xs, KP_ROW(g), col, (g) < ngroups && KP_ROW(g) < a.M)
+#define KP_PROC(S, g)                                                                 \
+  if ((g) < ngroups) {                                                                \
+    fwd_row<VPL, WPR, NX>(a, S, wv, red, KP_ROW(g), col, lane, wave, part, rloc, it); \
+    ++it;                                                                             \
   }
+  int64_t g = blockIdx.x;
+  KP_LOAD(s0, g);
+  if constexpr (WPR < 4) {
+    for (; g < ngroups; g += 2 * G) {
+      KP_LOAD(s1, g + G);
+      KP_PROC(s0, g);
+      KP_LOAD(s0, g + 2 * G);
+      KP_PROC(s1, g + G);
+    }
+  } else {
+    // Rows split over 4 waves (one row per block step) measure faster with
+    // the single-step loop that moves the prefetched slot into place.
+    for (; g < ngroups; g += G) {
+      KP_LOAD(s1, g + G);
+      KP_PROC(s0, g);
+      s0 = s1;
+    }
+  }
+#undef KP_ROW
+#undef KP_LOAD
+#undef KP_PROC
 }
 
 // Any N, any alignment: one block per row, scalar accesses, two passes.
@@ -240,6 +271,99 @@ __device__ __forceinline__ void add_acc(const float* buf, int lane, float (&acc)
   }
 }
 
+// Loads of one row group of the backward: x and dy terms, the residual
+// gradient (RES) and the given rstd (when a.rstd).
+template <int VPL, int NX, int NDY, bool RES>
+__device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& dr, RawRow<VPL, 1>& rr, float& rq,
+                                         const RmsBwdArgs& a, int64_t row, int64_t col, bool ok) {
+  load_raw<VPL, NX>(xr, a.x, a.xs, row, col, ok);
+  load_raw<VPL, NDY>(dr, a.dy, a.dys, row, col, ok);
+  if constexpr (RES) {
+    const uint16_t* rrow = a.dxr + row * a.dxrs + col;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) rr.v[0][i] = ok ? ld16_stream(rrow + i * 512) : u32x4{0u, 0u, 0u, 0u};
+  }
+  rq = (a.rstd != nullptr && ok) ? a.rstd[row] : 0.f;
+}
+
+// One row of the backward: dx (with the residual epilogue) and this row's
+// contribution dy * xhat to the per-column weight-gradient accumulators.
+template <int VPL, int WPR, int NX, int NDY, bool RES>
+__device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, NX>& xr, const RawRow<VPL, NDY>& dr,
+                                        const RawRow<VPL, 1>& rr, float rq, u32x4 (&wv)[VPL], float (&acc)[VPL * 8],
+                                        float (&red)[2][4][2], int64_t row, int64_t col, int lane, int wave, int rloc,
+                                        int it) {
+  const bool valid = row < a.M;
+  const float inv_n = 1.0f / (float)a.N;
+  u32x4 xv[VPL], dv[VPL];
+  sum_raw<VPL, NX>(xv, xr);
+  sum_raw<VPL, NDY>(dv, dr);
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
+  // sum(x * g) and, when rstd is not supplied, sum(x^2), in one sweep.
+  float sxg = 0.f, ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    float xf[8], df[8], wf[8];
+    unpack8(xv[i], xf);
+    unpack8(dv[i], df);
+    unpack8(wv[i], wf);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      sxg = fmaf(xf[e], df[e] * wf[e], sxg);
+      ss = fmaf(xf[e], xf[e], ss);
+    }
+  }
+  sxg = wave_sum(sxg);
+  if (a.rstd == nullptr) ss = wave_sum(ss);
+  if constexpr (WPR > 1) {
+    if (lane == 0) {
+      red[it & 1][wave][0] = sxg;
+      red[it & 1][wave][1] = ss;
+    }
+    __syncthreads();
+    float t0 = 0.f, t1 = 0.f;
+#pragma unroll
+    for (int p = 0; p < WPR; ++p) {
+      t0 += red[it & 1][rloc * WPR + p][0];
+      t1 += red[it & 1][rloc * WPR + p][1];
+    }
+    sxg = t0;
+    ss = t1;
+  }
+  const float r = (a.rstd != nullptr) ? rq : 1.0f / sqrtf(ss / (float)a.N + a.eps);
+  // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
+  const float cN = (r * sxg) * inv_n;
+#pragma unroll
+  for (int i = 0; i < VPL; ++i) {
+    reg_barrier(xv[i]);
+    reg_barrier(dv[i]);
+    reg_barrier(wv[i]);
+  }
+  if (valid) {
+    uint16_t* dxrow = a.dx + row * a.dxs + col;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float xf[8], df[8], wf[8], o[8];
+      unpack8(xv[i], xf);
+      unpack8(dv[i], df);
+      unpack8(wv[i], wf);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float xh = xf[e] * r;
+        const float gg = df[e] * wf[e];
+        o[e] = (gg - xh * cN) * r;
+        acc[i * 8 + e] = fmaf(df[e], xh, acc[i * 8 + e]);
+      }
+      u32x4 ov = pack8(o);
+      if constexpr (RES) ov = add_bf8(rr.v[0][i], ov);
+      st16(dxrow + i * 512, ov);
+    }
+  }
+}
+
+// Grid-stride over row groups with one group of loads in flight, in two named
+// register slots (see rms_fwd_vec).
 template <int VPL, int WPR, int NX, int NDY, bool RES>
 __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
   constexpr int RB = 4 / WPR;
@@ -257,104 +381,45 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
 #pragma unroll
   for (int i = 0; i < VPL * 8; ++i) acc[i] = 0.f;
 
-  const float inv_n = 1.0f / (float)a.N;
-  // Blocks walk the row groups grid-stride.
   const int64_t ngroups = ceil_div_dev(a.M, RB);
+  const int64_t G = gridDim.x;
+  RawRow<VPL, NX> x0, x1;
+  RawRow<VPL, NDY> d0, d1;
+  RawRow<VPL, 1> r0, r1;
+  float q0, q1;
+  int it = 0;
+#define KP_ROW(g) ((g) * RB + rloc)
+#define KP_LOAD(S, g) \
+  bwd_load<VPL, NX, NDY, RES>(x##S, d##S, r##S, q##S, a, KP_ROW(g), col, (g) < ngroups && KP_ROW(g) < a.M)
+#define KP_PROC(S, g)                                                                                         \
+  if ((g) < ngroups) {                                                                                        \
+    bwd_row<VPL, WPR, NX, NDY, RES>(a, x##S, d##S, r##S, q##S, wv, acc, red, KP_ROW(g), col, lane, wave, rloc, \
+                                    it);                                                                      \
+    ++it;                                                                                                     \
+  }
   int64_t g = blockIdx.x;
-  RawRow<VPL, NX> xc;
-  RawRow<VPL, NDY> dc;
-  {
-    const int64_t row = g * RB + rloc;
-    const bool ok = g < ngroups && row < a.M;
-    load_raw<VPL, NX>(xc, a.x, a.xs, row, col, ok);
-    load_raw<VPL, NDY>(dc, a.dy, a.dys, row, col, ok);
+  KP_LOAD(0, g);
+  if constexpr (WPR < 4) {
+    for (; g < ngroups; g += 2 * G) {
+      KP_LOAD(1, g + G);
+      KP_PROC(0, g);
+      KP_LOAD(0, g + 2 * G);
+      KP_PROC(1, g + G);
+    }
+  } else {
+    // Single-step loop for rows split over 4 waves (measured faster there).
+    for (; g < ngroups; g += G) {
+      KP_LOAD(1, g + G);
+      KP_PROC(0, g);
+      x0 = x1;
+      d0 = d1;
+      r0 = r1;
+      q0 = q1;
+    }
   }
-  for (int it = 0; g < ngroups; g += gridDim.x, ++it) {
-    const int64_t row = g * RB + rloc;
-    const bool valid = row < a.M;
-    // This row's scalar and residual loads go out before the next row's prefetch.
-    const float r_given = (a.rstd != nullptr && valid) ? a.rstd[row] : 0.f;
-    u32x4 rv[RES ? VPL : 1];
-    if (RES && valid) {
-      const uint16_t* rrow = a.dxr + row * a.dxrs + col;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) rv[i] = ld16_stream(rrow + i * 512);
-    }
-    const int64_t gn = g + gridDim.x, rown = gn * RB + rloc;
-    const bool okn = gn < ngroups && rown < a.M;
-    RawRow<VPL, NX> xn;
-    RawRow<VPL, NDY> dn;
-    load_raw<VPL, NX>(xn, a.x, a.xs, rown, col, okn);
-    load_raw<VPL, NDY>(dn, a.dy, a.dys, rown, col, okn);
-
-    u32x4 xv[VPL], dv[VPL];
-    sum_raw<VPL, NX>(xv, xc);
-    sum_raw<VPL, NDY>(dv, dc);
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
-    // sum(x * g) and, when rstd is not supplied, sum(x^2), in one sweep.
-    float sxg = 0.f, ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      float xf[8], df[8], wf[8];
-      unpack8(xv[i], xf);
-      unpack8(dv[i], df);
-      unpack8(wv[i], wf);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        sxg = fmaf(xf[e], df[e] * wf[e], sxg);
-        ss = fmaf(xf[e], xf[e], ss);
-      }
-    }
-    sxg = wave_sum(sxg);
-    if (a.rstd == nullptr) ss = wave_sum(ss);
-    if constexpr (WPR > 1) {
-      if (lane == 0) {
-        red[it & 1][wave][0] = sxg;
-        red[it & 1][wave][1] = ss;
-      }
-      __syncthreads();
-      float t0 = 0.f, t1 = 0.f;
-#pragma unroll
-      for (int p = 0; p < WPR; ++p) {
-        t0 += red[it & 1][rloc * WPR + p][0];
-        t1 += red[it & 1][rloc * WPR + p][1];
-      }
-      sxg = t0;
-      ss = t1;
-    }
-    const float r = (a.rstd != nullptr) ? r_given : 1.0f / sqrtf(ss / (float)a.N + a.eps);
-    // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
-    const float cN = (r * sxg) * inv_n;
-#pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      reg_barrier(xv[i]);
-      reg_barrier(dv[i]);
-      reg_barrier(wv[i]);
-    }
-    if (valid) {
-      uint16_t* dxrow = a.dx + row * a.dxs + col;
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        float xf[8], df[8], wf[8], o[8];
-        unpack8(xv[i], xf);
-        unpack8(dv[i], df);
-        unpack8(wv[i], wf);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const float xh = xf[e] * r;
-          const float gg = df[e] * wf[e];
-          o[e] = (gg - xh * cN) * r;
-          acc[i * 8 + e] = fmaf(df[e], xh, acc[i * 8 + e]);
-        }
-        u32x4 ov = pack8(o);
-        if constexpr (RES) ov = add_bf8(rv[i], ov);
-        st16(dxrow + i * 512, ov);
-      }
-    }
-    xc = xn;
-    dc = dn;
-  }
+#undef KP_ROW
+#undef KP_LOAD
+#undef KP_PROC
 
   if (a.partial == nullptr) return;
   // Combine the column partials of the waves that share a column segment
@@ -438,16 +503,14 @@ __global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restr
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if ((N & 3) == 0) {
     if (c0 < N) {
+      // All of a batch's loads are issued before the (in-order) adds.
       int p = p0;
-      for (; p + 4 <= p1; p += 4) {
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(partial + (int64_t)p * N + c0);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + 1) * N + c0);
-        const f32x4 v2 = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + 2) * N + c0);
-        const f32x4 v3 = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + 3) * N + c0);
-        acc += v0;
-        acc += v1;
-        acc += v2;
-        acc += v3;
+      for (; p + 8 <= p1; p += 8) {
+        f32x4 v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + k) * N + c0);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) acc += v[k];
       }
       for (; p < p1; ++p) acc += *reinterpret_cast<const f32x4*>(partial + (int64_t)p * N + c0);
     }
