@@ -56,6 +56,14 @@ struct RmsBwdArgs {
   float eps;
 };
 
+// Weight-gradient partials are stored column-chunk-major, [ceil(N/32)][P][32]
+// fp32 (P = row blocks): a block's partial row lands as full 128-byte lines
+// and the finalize reads each 32-column chunk of all P rows contiguously.
+constexpr int kPartChunk = 32;
+__host__ __device__ __forceinline__ int64_t part_index(int64_t c, int64_t p, int64_t P) {
+  return ((c / kPartChunk) * P + p) * kPartChunk + (c % kPartChunk);
+}
+
 __device__ __forceinline__ int64_t w_index(int64_t c, int64_t seg_len, int64_t seg_stride) {
   return (c / seg_len) * seg_stride + (c % seg_len);
 }
@@ -288,10 +296,10 @@ __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& 
 
 // One row of the backward: dx (with the residual epilogue) and this row's
 // contribution dy * xhat to the per-column weight-gradient accumulators.
-template <int VPL, int WPR, int NX, int NDY, bool RES>
+template <int VPL, int WPR, int NX, int NDY, bool RES, int NW>
 __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, NX>& xr, const RawRow<VPL, NDY>& dr,
                                         const RawRow<VPL, 1>& rr, float rq, u32x4 (&wv)[VPL], float (&acc)[VPL * 8],
-                                        float (&red)[2][4][2], int64_t row, int64_t col, int lane, int wave, int rloc,
+                                        float (&red)[2][NW][2], int64_t row, int64_t col, int lane, int wave, int rloc,
                                         int it) {
   const bool valid = row < a.M;
   const float inv_n = 1.0f / (float)a.N;
@@ -363,13 +371,14 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
 }
 
 // Grid-stride over row groups with one group of loads in flight, in two named
-// register slots (see rms_fwd_vec).
-template <int VPL, int WPR, int NX, int NDY, bool RES>
-__global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
-  constexpr int RB = 4 / WPR;
+// register slots (see rms_fwd_vec).  NW waves per block (4 or 8): RB = NW / WPR
+// rows per block step; every block owns one weight-gradient partial row.
+template <int VPL, int WPR, int NX, int NDY, bool RES, int NW>
+__global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
+  constexpr int RB = NW / WPR;
   constexpr int SEG = 512 * VPL;
-  extern __shared__ float smem[];  // [2][SEG] weight-gradient combine (only when a.partial)
-  __shared__ float red[2][4][2];
+  extern __shared__ float smem[];  // [RB / 2][WPR][SEG] weight-gradient combine (only when a.partial)
+  __shared__ float red[2][NW][2];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int part = wave % WPR, rloc = wave / WPR;
   const int64_t col = (int64_t)part * SEG + lane * 8;
@@ -393,8 +402,8 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
   bwd_load<VPL, NX, NDY, RES>(x##S, d##S, r##S, q##S, a, KP_ROW(g), col, (g) < ngroups && KP_ROW(g) < a.M)
 #define KP_PROC(S, g)                                                                                         \
   if ((g) < ngroups) {                                                                                        \
-    bwd_row<VPL, WPR, NX, NDY, RES>(a, x##S, d##S, r##S, q##S, wv, acc, red, KP_ROW(g), col, lane, wave, rloc, \
-                                    it);                                                                      \
+    bwd_row<VPL, WPR, NX, NDY, RES, NW>(a, x##S, d##S, r##S, q##S, wv, acc, red, KP_ROW(g), col, lane, wave,  \
+                                        rloc, it);                                                            \
     ++it;                                                                                                     \
   }
   int64_t g = blockIdx.x;
@@ -422,38 +431,36 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_vec(RmsBwdArgs a) {
 #undef KP_PROC
 
   if (a.partial == nullptr) return;
-  // Combine the column partials of the waves that share a column segment
-  // (fixed order: ((w0 + w2) + (w1 + w3)) for WPR 1, (w0 + w2) / (w1 + w3) for
-  // WPR 2) through at most 2*SEG floats of LDS, then write one partial row.
-  if constexpr (RB >= 2) {
-    if (wave >= 2) stash_acc<VPL>(smem + (wave - 2) * SEG, lane, acc);
+  // Combine the column partials of the RB waves that share a column segment
+  // with a fixed pairwise tree (level `step`: rloc r += rloc r + step), through
+  // [RB / 2][WPR][SEG] floats of LDS, then write one partial row per block.
+#pragma unroll
+  for (int step = RB / 2; step >= 1; step /= 2) {
+    if (rloc >= step && rloc < 2 * step) stash_acc<VPL>(smem + ((rloc - step) * WPR + part) * SEG, lane, acc);
     __syncthreads();
-    if (wave < 2) add_acc<VPL>(smem + wave * SEG, lane, acc);
+    if (rloc < step) add_acc<VPL>(smem + (rloc * WPR + part) * SEG, lane, acc);
+    __syncthreads();
   }
-  if constexpr (RB == 4) {
-    __syncthreads();
-    if (wave == 1) stash_acc<VPL>(smem, lane, acc);
-    __syncthreads();
-    if (wave == 0) add_acc<VPL>(smem, lane, acc);
-  }
-  if (wave < WPR) {
-    float* prow = a.partial + (int64_t)blockIdx.x * a.N + col;
+  if (rloc == 0) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      *reinterpret_cast<f32x4*>(prow + i * 512) = f32x4{acc[i * 8], acc[i * 8 + 1], acc[i * 8 + 2], acc[i * 8 + 3]};
-      *reinterpret_cast<f32x4*>(prow + i * 512 + 4) = f32x4{acc[i * 8 + 4], acc[i * 8 + 5], acc[i * 8 + 6], acc[i * 8 + 7]};
+      // 8 consecutive columns, 8-aligned: inside one 32-column chunk
+      float* pp = a.partial + part_index(col + i * 512, blockIdx.x, gridDim.x);
+      *reinterpret_cast<f32x4*>(pp) = f32x4{acc[i * 8], acc[i * 8 + 1], acc[i * 8 + 2], acc[i * 8 + 3]};
+      *reinterpret_cast<f32x4*>(pp + 4) = f32x4{acc[i * 8 + 4], acc[i * 8 + 5], acc[i * 8 + 6], acc[i * 8 + 7]};
     }
   }
 }
 
 // Any N, any alignment: one block per row, scalar accesses.  The block's
 // weight-gradient partial row lives directly in `partial` (read-modify-write,
-// owned by this block only).
+// owned by this block only; same chunked layout as the vector kernel).
 __global__ __launch_bounds__(kThreads) void rms_bwd_generic(RmsBwdArgs a) {
   __shared__ float red[4];
-  float* prow = a.partial ? a.partial + (int64_t)blockIdx.x * a.N : nullptr;
-  if (prow)
-    for (int64_t c = threadIdx.x; c < a.N; c += kThreads) prow[c] = 0.f;
+  float* part = a.partial;
+  const int64_t P = gridDim.x;
+  if (part)
+    for (int64_t c = threadIdx.x; c < a.N; c += kThreads) part[part_index(c, blockIdx.x, P)] = 0.f;
   const float inv_n = 1.0f / (float)a.N;
   for (int64_t row = blockIdx.x; row < a.M; row += gridDim.x) {
     float sxg = 0.f, ss = 0.f;
@@ -481,59 +488,57 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_generic(RmsBwdArgs a) {
       float o = round_bf((df * wf - xh * cN) * r);
       if (a.dxr) o = bf_to_f(a.dxr[row * a.dxrs + c]) + o;
       a.dx[row * a.dxs + c] = f_to_bf(o);
-      if (prow) prow[c] = fmaf(df, xh, prow[c]);
+      if (part) {
+        float& pc = part[part_index(c, blockIdx.x, P)];
+        pc = fmaf(df, xh, pc);
+      }
     }
   }
 }
 
-// dw[c] = sum_{p < P} partial[p, c].  A block owns 16 columns and splits the
-// P partial rows into 64 contiguous groups (thread = 4 columns x 1 group);
-// each group is summed in row order, then the 64 group sums are added in
-// group order.  Every thread's loads are independent, so the whole [P, 16]
-// slab is in flight at once.
-constexpr int kFinCols = 16;
-constexpr int kFinGroups = kThreads / (kFinCols / 4);
+// dw[c] = sum_{p < P} partial[p, c].  A block owns one 32-column chunk, whose
+// P partial rows are contiguous ([P][32] fp32).  Thread (r, q) sums columns
+// 4q..4q+3 over rows r, r + 32, r + 64, ... in row order; the 32 row-group
+// sums are then added in group order.  Loads go out in batches of 8 rows.
+constexpr int kFinGroups = kThreads / (kPartChunk / 4);  // 32
 
 __global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restrict__ partial, int P, int64_t N,
                                                             float* dw_f32, uint16_t* dw_bf16, int round_f32) {
-  __shared__ float s[kFinGroups][kFinCols + 1];
-  const int q = threadIdx.x & 3, g = threadIdx.x >> 2;
-  const int64_t c0 = (int64_t)blockIdx.x * kFinCols + q * 4;
-  const int p0 = (int)(((int64_t)P * g) / kFinGroups), p1 = (int)(((int64_t)P * (g + 1)) / kFinGroups);
+  __shared__ float s[kFinGroups][kPartChunk + 1];
+  const int q = threadIdx.x & 7, r = threadIdx.x >> 3;
+  const int64_t c0 = (int64_t)blockIdx.x * kPartChunk;
+  const float* base = partial + (int64_t)blockIdx.x * P * kPartChunk;
+  const int ncol = (int)(N - c0 < kPartChunk ? N - c0 : kPartChunk);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-  if ((N & 3) == 0) {
-    if (c0 < N) {
-      // All of a batch's loads are issued before the (in-order) adds.
-      int p = p0;
-      for (; p + 8 <= p1; p += 8) {
-        f32x4 v[8];
+  if (ncol == kPartChunk) {
+    int p = r;
+    for (; p + 7 * kFinGroups < P; p += 8 * kFinGroups) {
+      f32x4 v[8];
 #pragma unroll
-        for (int k = 0; k < 8; ++k) v[k] = *reinterpret_cast<const f32x4*>(partial + (int64_t)(p + k) * N + c0);
+      for (int k = 0; k < 8; ++k)
+        v[k] = *reinterpret_cast<const f32x4*>(base + (int64_t)(p + k * kFinGroups) * kPartChunk + q * 4);
 #pragma unroll
-        for (int k = 0; k < 8; ++k) acc += v[k];
-      }
-      for (; p < p1; ++p) acc += *reinterpret_cast<const f32x4*>(partial + (int64_t)p * N + c0);
+      for (int k = 0; k < 8; ++k) acc += v[k];
     }
+    for (; p < P; p += kFinGroups) acc += *reinterpret_cast<const f32x4*>(base + (int64_t)p * kPartChunk + q * 4);
   } else {
     for (int k = 0; k < 4; ++k) {
-      if (c0 + k < N) {
+      if (q * 4 + k < ncol) {
         float t = 0.f;
-        for (int p = p0; p < p1; ++p) t += partial[(int64_t)p * N + c0 + k];
+        for (int p = r; p < P; p += kFinGroups) t += base[(int64_t)p * kPartChunk + q * 4 + k];
         acc[k] = t;
       }
     }
   }
 #pragma unroll
-  for (int k = 0; k < 4; ++k) s[g][q * 4 + k] = acc[k];
+  for (int k = 0; k < 4; ++k) s[r][q * 4 + k] = acc[k];
   __syncthreads();
-  if (threadIdx.x < kFinCols) {
-    const int64_t c = (int64_t)blockIdx.x * kFinCols + threadIdx.x;
-    if (c < N) {
-      float t = s[0][threadIdx.x];
-      for (int gg = 1; gg < kFinGroups; ++gg) t += s[gg][threadIdx.x];
-      if (dw_bf16) dw_bf16[c] = f_to_bf(t);
-      if (dw_f32) dw_f32[c] = round_f32 ? round_bf(t) : t;
-    }
+  if (threadIdx.x < ncol) {
+    float t = s[0][threadIdx.x];
+    for (int g = 1; g < kFinGroups; ++g) t += s[g][threadIdx.x];
+    const int64_t c = c0 + threadIdx.x;
+    if (dw_bf16) dw_bf16[c] = f_to_bf(t);
+    if (dw_f32) dw_f32[c] = round_f32 ? round_bf(t) : t;
   }
 }
 
@@ -552,8 +557,14 @@ int fwd_bpc() {
   static const int v = env_int("KP_RMS_FWD_BPC", 2, 1, 64);
   return v;
 }
+// Backward block shape: KP_RMS_BWD_WAVES waves per block (4 or 8) and
+// KP_RMS_BWD_BPC blocks per CU (default: 8 waves per CU either way).
+int bwd_waves() {
+  static const int v = env_int("KP_RMS_BWD_WAVES", 4, 4, 8) == 8 ? 8 : 4;
+  return v;
+}
 int bwd_bpc() {
-  static const int v = env_int("KP_RMS_BWD_BPC", 2, 1, 4);
+  static const int v = env_int("KP_RMS_BWD_BPC", 8 / bwd_waves(), 1, 4);
   return v;
 }
 
@@ -614,21 +625,25 @@ FwdKernel fwd_for_terms(int nx) {
 // Term combinations of the backward fast path (x terms, dy terms, residual
 // epilogue) -- the ones the configurations and reference fragments use;
 // others run the generic kernel.
-template <int VPL, int WPR>
-BwdKernel bwd_for_terms(int nx, int ndy, bool res) {
+template <int VPL, int WPR, int NW>
+BwdKernel bwd_for_terms_nw(int nx, int ndy, bool res) {
   if (!res) {
-    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, false>;
-    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, false>;
-    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, false>;
-    if (nx == 2 && ndy == 1) return rms_bwd_vec<VPL, WPR, 2, 1, false>;
-    if (nx == 3 && ndy == 1) return rms_bwd_vec<VPL, WPR, 3, 1, false>;
-    if (nx == 2 && ndy == 2) return rms_bwd_vec<VPL, WPR, 2, 2, false>;
+    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, false, NW>;
+    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, false, NW>;
+    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, false, NW>;
+    if (nx == 2 && ndy == 1) return rms_bwd_vec<VPL, WPR, 2, 1, false, NW>;
+    if (nx == 3 && ndy == 1) return rms_bwd_vec<VPL, WPR, 3, 1, false, NW>;
+    if (nx == 2 && ndy == 2) return rms_bwd_vec<VPL, WPR, 2, 2, false, NW>;
   } else {
-    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, true>;
-    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, true>;
-    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, true>;
+    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, true, NW>;
+    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, true, NW>;
+    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, true, NW>;
   }
   return nullptr;
+}
+template <int VPL, int WPR>
+BwdKernel bwd_for_terms(int nx, int ndy, bool res, int nw) {
+  return nw == 8 ? bwd_for_terms_nw<VPL, WPR, 8>(nx, ndy, res) : bwd_for_terms_nw<VPL, WPR, 4>(nx, ndy, res);
 }
 #define KP_SHAPE_SWITCH(FN, ...)                      \
   switch (vpl * 10 + wpr) {                           \
@@ -652,7 +667,9 @@ BwdKernel bwd_for_terms(int nx, int ndy, bool res) {
   }                                                   \
   return nullptr;
 FwdKernel fwd_kernel(int vpl, int wpr, int nx) { KP_SHAPE_SWITCH(fwd_for_terms, nx) }
-BwdKernel bwd_kernel(int vpl, int wpr, int nx, int ndy, bool res) { KP_SHAPE_SWITCH(bwd_for_terms, nx, ndy, res) }
+BwdKernel bwd_kernel(int vpl, int wpr, int nx, int ndy, bool res, int nw) {
+  KP_SHAPE_SWITCH(bwd_for_terms, nx, ndy, res, nw)
+}
 #undef KP_SHAPE_SWITCH
 
 bool rows_vec_ok(const void* const* p, const int64_t* s, int n) {
@@ -740,10 +757,11 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
 
 size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N) {
   if (M <= 0 || N <= 0) return 16;
-  // Partial rows: at most one per row block; the block count never exceeds 4 per CU.
+  // Partial rows: at most one per row block; the block count never exceeds 4 per
+  // CU.  Rows are padded to whole 32-column chunks.
   const int64_t blocks = (int64_t)cu_count() * 4;
   const int64_t rows = M < blocks ? M : blocks;
-  return (size_t)(rows * N * (int64_t)sizeof(float));
+  return (size_t)(rows * ceil_div(N, kPartChunk) * kPartChunk * (int64_t)sizeof(float));
 }
 
 int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy, const void* const* x_terms,
@@ -799,13 +817,17 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
                rows_vec_ok(dy_terms, dy_strides, n_dy) && aligned16(dx) && (dx_stride & 7) == 0;
     if (vec && dx_residual) vec = aligned16(dx_residual) && (dxr_stride & 7) == 0;
     if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
-    const BwdKernel bk = vec ? bwd_kernel(vpl, wpr, n_x, n_dy, dx_residual != nullptr) : nullptr;
+    int nw = bwd_waves();
+    // 8-wave blocks need (8 / wpr / 2) * wpr * SEG floats of combine LDS; stay within 48 KiB.
+    if (vec && nw == 8 && (size_t)(8 / wpr / 2) * wpr * 512 * vpl * sizeof(float) > 48 * 1024) nw = 4;
+    const BwdKernel bk = vec ? bwd_kernel(vpl, wpr, n_x, n_dy, dx_residual != nullptr, nw) : nullptr;
     vec = vec && bk != nullptr;
     if (vec) {
-      blocks = bwd_blocks(M, 4 / wpr);
-      const size_t lds = (want_dw && wpr < 4) ? (size_t)2 * 512 * vpl * sizeof(float) : 0;
+      const int rb = nw / wpr;
+      blocks = bwd_blocks(M, rb);
+      const size_t lds = (want_dw && rb >= 2) ? (size_t)(rb / 2) * wpr * 512 * vpl * sizeof(float) : 0;
       void* args[] = {&a};
-      launch_dominant_raw(reinterpret_cast<const void*>(bk), dim3(blocks), dim3(kThreads), args, lds, s);
+      launch_dominant_raw(reinterpret_cast<const void*>(bk), dim3(blocks), dim3(nw * 64), args, lds, s);
     } else {
       blocks = bwd_blocks(M, 1);
       KP_LAUNCH_DOMINANT(rms_bwd_generic, dim3(blocks), dim3(kThreads), 0, s, a);
@@ -814,7 +836,7 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
     if (st != KP_OK) return st;
   }
   if (want_dw) {
-    hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, kFinCols)), dim3(kThreads), 0, s,
+    hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, kPartChunk)), dim3(kThreads), 0, s,
                        static_cast<const float*>(workspace), blocks, N, dw_f32, static_cast<uint16_t*>(dw_bf16),
                        dw_f32_round_bf16);
     st = check_launch(who);
