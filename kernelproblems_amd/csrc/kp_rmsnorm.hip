@@ -72,19 +72,30 @@ __device__ __forceinline__ int64_t w_index(int64_t c, int64_t seg_len, int64_t s
 // software-pipelined: the next row's raw terms are requested before the
 // current row's stores, because vmcnt counts loads and stores in issue order
 // and a wait on a load issued after a store would also wait for that store.
+//
+// Row loads are never predicated.  The row loops run an exact per-block trip
+// count, so a row past the end occurs only in the last row group when M is
+// not a multiple of the rows per group; it is read as row M - 1 and its
+// results are discarded.  A load under a branch makes the compiler's
+// wait-count merge at the join assume nothing is known about the loads in
+// flight and emit vmcnt(0), which would also wait for the prefetched row.
+// A scheduling barrier follows every prefetch so that the machine scheduler
+// cannot hoist the current row's arithmetic (and its waits) above it.
 template <int VPL, int NT>
 struct RawRow {
   u32x4 v[NT][VPL];
 };
 
+__device__ __forceinline__ int64_t clamp_row(int64_t row, int64_t M) { return row < M ? row : M - 1; }
+
 template <int VPL, int NT>
 __device__ __forceinline__ void load_raw(RawRow<VPL, NT>& r, const uint16_t* const (&base)[3],
-                                         const int64_t (&strides)[3], int64_t row, int64_t col, bool valid) {
+                                         const int64_t (&strides)[3], int64_t row, int64_t col) {
 #pragma unroll
   for (int t = 0; t < NT; ++t) {
     const uint16_t* p = base[t] + row * strides[t] + col;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) r.v[t][i] = valid ? ld16_stream(p + i * 512) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < VPL; ++i) r.v[t][i] = ld16_stream(p + i * 512);
   }
 }
 
@@ -154,12 +165,12 @@ __device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, N
       unpack8(wv[i], wf);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = (f[e] * r) * wf[e];
-      st16(yrow + i * 512, pack8(o));
+      st16_stream(yrow + i * 512, pack8(o));
     }
     if (NX > 1 && a.h != nullptr) {
       uint16_t* hrow = a.h + row * a.hs + col;
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) st16(hrow + i * 512, hv[i]);
+      for (int i = 0; i < VPL; ++i) st16_stream(hrow + i * 512, hv[i]);
     }
     if (a.rstd != nullptr && part == 0 && lane == 0) a.rstd[row] = r;
   }
@@ -168,8 +179,9 @@ __device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, N
 // Blocks walk the row groups grid-stride (measured faster on gfx950 than
 // contiguous per-block ranges for these row loops) with one row group of loads
 // in flight ahead of the one being reduced.  The two register slots are
-// separate named variables (an array of slots indexed by the step ends up in
-// scratch memory); for WPR < 4 the loop is unrolled two steps per pass.
+// separate named variables, and the loop is unrolled two steps per pass so
+// that no slot is ever copied: an array of slots indexed by the step ends up
+// in scratch memory, and a slot copy makes the wave wait for the prefetch.
 template <int VPL, int WPR, int NX>
 __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   constexpr int RB = 4 / WPR;
@@ -187,29 +199,29 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   RawRow<VPL, NX> s0, s1;
   int it = 0;
 #define KP_ROW(g) ((g) * RB + rloc)
-#define KP_LOAD(S, g) load_raw<VPL, NX>(S, a.x, a.xs, KP_ROW(g), col, (g) < ngroups && KP_ROW(g) < a.M)
-#define KP_PROC(S, g)                                                                 \
-  if ((g) < ngroups) {                                                                \
-    fwd_row<VPL, WPR, NX>(a, S, wv, red, KP_ROW(g), col, lane, wave, part, rloc, it); \
-    ++it;                                                                             \
-  }
-  int64_t g = blockIdx.x;
+#define KP_LOAD(S, g)                                              \
+  load_raw<VPL, NX>(S, a.x, a.xs, clamp_row(KP_ROW(g), a.M), col); \
+  __builtin_amdgcn_sched_barrier(0)
+#define KP_PROC(S, g)                                                               \
+  fwd_row<VPL, WPR, NX>(a, S, wv, red, KP_ROW(g), col, lane, wave, part, rloc, it); \
+  ++it
+  // Exact trip count: the grid never exceeds the row-group count, so every
+  // block owns nb >= 1 groups and nothing is prefetched past its last one.
+  const int64_t nb = (ngroups - 1 - blockIdx.x) / G + 1;
+  int64_t g = blockIdx.x, k = 0;
   KP_LOAD(s0, g);
-  if constexpr (WPR < 4) {
-    for (; g < ngroups; g += 2 * G) {
-      KP_LOAD(s1, g + G);
-      KP_PROC(s0, g);
-      KP_LOAD(s0, g + 2 * G);
-      KP_PROC(s1, g + G);
-    }
+  for (; k + 2 < nb; k += 2, g += 2 * G) {
+    KP_LOAD(s1, g + G);
+    KP_PROC(s0, g);
+    KP_LOAD(s0, g + 2 * G);
+    KP_PROC(s1, g + G);
+  }
+  if (k + 1 < nb) {
+    KP_LOAD(s1, g + G);
+    KP_PROC(s0, g);
+    KP_PROC(s1, g + G);
   } else {
-    // Rows split over 4 waves (one row per block step) measure faster with
-    // the single-step loop that moves the prefetched slot into place.
-    for (; g < ngroups; g += G) {
-      KP_LOAD(s1, g + G);
-      KP_PROC(s0, g);
-      s0 = s1;
-    }
+    KP_PROC(s0, g);
   }
 #undef KP_ROW
 #undef KP_LOAD
@@ -280,18 +292,21 @@ __device__ __forceinline__ void add_acc(const float* buf, int lane, float (&acc)
 }
 
 // Loads of one row group of the backward: x and dy terms, the residual
-// gradient (RES) and the given rstd (when a.rstd).
+// gradient (RES) and the given rstd.  `row` is already clamped to M - 1 and
+// nothing is predicated (see load_raw); without a given rstd the 4-byte load
+// reads the row's own first x word instead (an L1 hit, never used).
 template <int VPL, int NX, int NDY, bool RES>
 __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& dr, RawRow<VPL, 1>& rr, float& rq,
-                                         const RmsBwdArgs& a, int64_t row, int64_t col, bool ok) {
-  load_raw<VPL, NX>(xr, a.x, a.xs, row, col, ok);
-  load_raw<VPL, NDY>(dr, a.dy, a.dys, row, col, ok);
+                                         const RmsBwdArgs& a, int64_t row, int64_t col) {
+  load_raw<VPL, NX>(xr, a.x, a.xs, row, col);
+  load_raw<VPL, NDY>(dr, a.dy, a.dys, row, col);
   if constexpr (RES) {
     const uint16_t* rrow = a.dxr + row * a.dxrs + col;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) rr.v[0][i] = ok ? ld16_stream(rrow + i * 512) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < VPL; ++i) rr.v[0][i] = ld16_stream(rrow + i * 512);
   }
-  rq = (a.rstd != nullptr && ok) ? a.rstd[row] : 0.f;
+  const float* rp = a.rstd != nullptr ? a.rstd + row : reinterpret_cast<const float*>(a.x[0] + row * a.xs[0]);
+  rq = *rp;
 }
 
 // One row of the backward: dx (with the residual epilogue) and this row's
@@ -365,7 +380,7 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
       }
       u32x4 ov = pack8(o);
       if constexpr (RES) ov = add_bf8(rr.v[0][i], ov);
-      st16(dxrow + i * 512, ov);
+      st16_stream(dxrow + i * 512, ov);
     }
   }
 }
@@ -398,33 +413,28 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   float q0, q1;
   int it = 0;
 #define KP_ROW(g) ((g) * RB + rloc)
-#define KP_LOAD(S, g) \
-  bwd_load<VPL, NX, NDY, RES>(x##S, d##S, r##S, q##S, a, KP_ROW(g), col, (g) < ngroups && KP_ROW(g) < a.M)
-#define KP_PROC(S, g)                                                                                         \
-  if ((g) < ngroups) {                                                                                        \
-    bwd_row<VPL, WPR, NX, NDY, RES, NW>(a, x##S, d##S, r##S, q##S, wv, acc, red, KP_ROW(g), col, lane, wave,  \
-                                        rloc, it);                                                            \
-    ++it;                                                                                                     \
-  }
-  int64_t g = blockIdx.x;
+#define KP_LOAD(S, g)                                                                       \
+  bwd_load<VPL, NX, NDY, RES>(x##S, d##S, r##S, q##S, a, clamp_row(KP_ROW(g), a.M), col); \
+  __builtin_amdgcn_sched_barrier(0)
+#define KP_PROC(S, g)                                                                                               \
+  bwd_row<VPL, WPR, NX, NDY, RES, NW>(a, x##S, d##S, r##S, q##S, wv, acc, red, KP_ROW(g), col, lane, wave, rloc, it); \
+  ++it
+  // Exact trip count (see rms_fwd_vec): nb >= 1 groups per block.
+  const int64_t nb = (ngroups - 1 - blockIdx.x) / G + 1;
+  int64_t g = blockIdx.x, k = 0;
   KP_LOAD(0, g);
-  if constexpr (WPR < 4) {
-    for (; g < ngroups; g += 2 * G) {
-      KP_LOAD(1, g + G);
-      KP_PROC(0, g);
-      KP_LOAD(0, g + 2 * G);
-      KP_PROC(1, g + G);
-    }
+  for (; k + 2 < nb; k += 2, g += 2 * G) {
+    KP_LOAD(1, g + G);
+    KP_PROC(0, g);
+    KP_LOAD(0, g + 2 * G);
+    KP_PROC(1, g + G);
+  }
+  if (k + 1 < nb) {
+    KP_LOAD(1, g + G);
+    KP_PROC(0, g);
+    KP_PROC(1, g + G);
   } else {
-    // Single-step loop for rows split over 4 waves (measured faster there).
-    for (; g < ngroups; g += G) {
-      KP_LOAD(1, g + G);
-      KP_PROC(0, g);
-      x0 = x1;
-      d0 = d1;
-      r0 = r1;
-      q0 = q1;
-    }
+    KP_PROC(0, g);
   }
 #undef KP_ROW
 #undef KP_LOAD
@@ -551,21 +561,31 @@ int env_int(const char* name, int dflt, int lo, int hi) {
   const int v = e ? atoi(e) : dflt;
   return (v >= lo && v <= hi) ? v : dflt;
 }
-// Launch-shape tuning knobs (read once): KP_RMS_FWD_BPC / KP_RMS_BWD_BPC, row
-// blocks per CU for the forward / backward grids.
-int fwd_bpc() {
-  static const int v = env_int("KP_RMS_FWD_BPC", 2, 1, 64);
-  return v;
+// Row blocks per CU for the pipelined row kernels: enough blocks that the
+// row loads in flight per CU (waves x 2 slots x bytes per wave slot) come to
+// about 128 KiB.  Measured on MI355X: 3-stream backward rows ([16384, 8192])
+// run 5% faster at 1 block per CU than at 2, 2-stream rows of 4096 columns
+// are best at 2, and more blocks never helped.
+int auto_bpc(int waves_per_block, int64_t wave_slot_bytes, int max_bpc) {
+  const int64_t per_block = (int64_t)waves_per_block * 2 * wave_slot_bytes;
+  const int v = (int)((128 * 1024 + per_block / 2) / per_block);
+  return v < 1 ? 1 : (v > max_bpc ? max_bpc : v);
 }
-// Backward block shape: KP_RMS_BWD_WAVES waves per block (4 or 8) and
-// KP_RMS_BWD_BPC blocks per CU (default: 8 waves per CU either way).
+// Launch-shape tuning knobs (read once): KP_RMS_FWD_BPC / KP_RMS_BWD_BPC, row
+// blocks per CU for the forward / backward grids (0 or unset: auto_bpc).
+int fwd_bpc(int64_t wave_slot_bytes) {
+  static const int v = env_int("KP_RMS_FWD_BPC", 0, 0, 64);
+  return v ? v : auto_bpc(4, wave_slot_bytes, 8);
+}
+// Backward block shape: KP_RMS_BWD_WAVES waves per block (4 or 8).
 int bwd_waves() {
   static const int v = env_int("KP_RMS_BWD_WAVES", 4, 4, 8) == 8 ? 8 : 4;
   return v;
 }
-int bwd_bpc() {
-  static const int v = env_int("KP_RMS_BWD_BPC", 8 / bwd_waves(), 1, 4);
-  return v;
+// At most 4 blocks per CU: the workspace holds one partial row per block.
+int bwd_bpc(int64_t wave_slot_bytes) {
+  static const int v = env_int("KP_RMS_BWD_BPC", 0, 0, 4);
+  return v ? v : auto_bpc(bwd_waves(), wave_slot_bytes, 4);
 }
 
 // Fast-path row shapes: N = 512 * VPL * WPR, at most 5 16-byte chunks per
@@ -690,9 +710,9 @@ int check_terms(const char* who, const char* name, const void* const* p, const i
 
 // Row blocks for the backward: a fixed number per CU so that the partial row
 // count (and hence the summation order) depends only on device and shape.
-int bwd_blocks(int64_t M, int rows_per_block_step) {
+int bwd_blocks(int64_t M, int rows_per_block_step, int bpc) {
   const int64_t groups = ceil_div(M, rows_per_block_step);
-  const int64_t want = (int64_t)cu_count() * bwd_bpc();
+  const int64_t want = (int64_t)cu_count() * bpc;
   return (int)(groups < want ? (groups > 0 ? groups : 1) : want);
 }
 
@@ -743,7 +763,7 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
   if (vec) {
     const int rb = 4 / wpr;
     const int64_t groups = ceil_div(M, rb);
-    const int64_t cap = (int64_t)cu_count() * fwd_bpc();
+    const int64_t cap = (int64_t)cu_count() * fwd_bpc((int64_t)n_x * vpl * 1024);
     const int grid = (int)(groups < cap ? groups : cap);
     void* args[] = {&a};
     launch_dominant_raw(reinterpret_cast<const void*>(fk), dim3(grid), dim3(kThreads), args, 0, s);
@@ -824,12 +844,12 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
     vec = vec && bk != nullptr;
     if (vec) {
       const int rb = nw / wpr;
-      blocks = bwd_blocks(M, rb);
+      blocks = bwd_blocks(M, rb, bwd_bpc((int64_t)(n_x + n_dy + (dx_residual ? 1 : 0)) * vpl * 1024));
       const size_t lds = (want_dw && rb >= 2) ? (size_t)(rb / 2) * wpr * 512 * vpl * sizeof(float) : 0;
       void* args[] = {&a};
       launch_dominant_raw(reinterpret_cast<const void*>(bk), dim3(blocks), dim3(nw * 64), args, lds, s);
     } else {
-      blocks = bwd_blocks(M, 1);
+      blocks = bwd_blocks(M, 1, 2);  // generic kernel: one row per block step, 2 blocks per CU
       KP_LAUNCH_DOMINANT(rms_bwd_generic, dim3(blocks), dim3(kThreads), 0, s, a);
     }
     st = check_launch(who);

@@ -49,16 +49,17 @@ struct RopeArgs {
   int32_t* err;
 };
 
-// Output element offset o of tensor T gets 8 (16-byte bf16 / 32-byte fp32) or 1 value.
-__device__ __forceinline__ void store8(const RopeTensor& T, int64_t o, const float* v) {
-  if (T.out_f32) {
-    float* p = static_cast<float*>(T.out) + o;
-    *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
-    *reinterpret_cast<f32x4*>(p + 4) = f32x4{v[4], v[5], v[6], v[7]};
+// Output element offset o gets 8 values (16-byte bf16 / 32-byte fp32) or 1 value.
+__device__ __forceinline__ void store8p(void* out, int out_f32, int64_t o, const float* v) {
+  if (out_f32) {
+    float* p = static_cast<float*>(out) + o;
+    st16f_stream(p, f32x4{v[0], v[1], v[2], v[3]});
+    st16f_stream(p + 4, f32x4{v[4], v[5], v[6], v[7]});
   } else {
-    st16(static_cast<uint16_t*>(T.out) + o, pack8(v));
+    st16_stream(static_cast<uint16_t*>(out) + o, pack8(v));
   }
 }
+__device__ __forceinline__ void store8(const RopeTensor& T, int64_t o, const float* v) { store8p(T.out, T.out_f32, o, v); }
 __device__ __forceinline__ void store1(const RopeTensor& T, int64_t o, float v) {
   if (T.out_f32) static_cast<float*>(T.out)[o] = v;
   else static_cast<uint16_t*>(T.out)[o] = f_to_bf(v);
@@ -218,6 +219,183 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeArgs a) {
 #undef COSV
 #undef SINV
 
+// ------------------------------------------------------------ fast path
+// D = 128 with 16-byte aligned rows (every reference fragment and the
+// rotate-half configuration): one wave per (b, s) position, and every 16-byte
+// chunk of the position's q and k heads is requested before any arithmetic,
+// so a wave has up to 16 loads (16 KiB) in flight.  Work unit u of a position
+// is (tensor, head, chunk c), q units first; lane l holds units l, l + 64, ...
+// Rotate-half: a unit is the chunk pair (c, c + 8) of one head (8 units per
+// head, two loads); interleaved: a unit is one chunk of 4 (2i, 2i+1) pairs (16
+// units per head, one load).  64 is a multiple of the units per head and q has
+// a whole number of heads, so lane l always holds chunk c = l % (units per
+// head) and its 8 (or 4) rotation angles serve every unit it holds.  Units
+// past the end re-read the last unit (same lines, no predicated loads: see
+// the row kernels of kp_rmsnorm.hip) and store nothing.  Arithmetic, rounding
+// and angles are those of rope_kernel, so both paths give identical bits.
+constexpr int kFastD = 128;
+constexpr int kFastMaxLoads = 16;
+
+template <int PAIRING, bool TABLE, int UPL>
+__global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
+  constexpr bool kHalf = PAIRING == KP_ROPE_HALF;
+  constexpr int HD = kFastD / 2;
+  constexpr int CPH = kHalf ? kFastD / 16 : kFastD / 8;  // units per head
+  constexpr int FPU = kHalf ? 8 : 4;                     // angles per unit
+  __shared__ float cs[kWavesPerBlock][2][HD];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t ps = (int64_t)blockIdx.x * kWavesPerBlock + wave;
+  if (ps >= a.B * a.S) return;  // wave-uniform; only wave barriers follow
+  const int64_t b = ps / a.S, s = ps - b * a.S;
+
+  const RopeTensor& T0 = a.t[0];
+  const RopeTensor& T1 = a.t[a.nt > 1 ? 1 : 0];
+  const int U0 = (int)T0.H * CPH;
+  const int U = U0 + (a.nt > 1 ? (int)T1.H * CPH : 0);
+  const uint16_t* xb0 = T0.x + b * T0.xs[0] + s * T0.xs[1];
+  const uint16_t* xb1 = T1.x + b * T1.xs[0] + s * T1.xs[1];
+
+  u32x4 v1[UPL], v2[UPL];
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    int u = lane + 64 * j;
+    u = u < U ? u : U - 1;
+    const bool second = u >= U0;
+    const int ul = second ? u - U0 : u;
+    const int h = ul / CPH, c = ul % CPH;
+    const uint16_t* xp = (second ? xb1 + h * T1.xs[2] : xb0 + h * T0.xs[2]) + c * 8;
+    v1[j] = ld16_stream(xp);
+    if constexpr (kHalf) v2[j] = ld16_stream(xp + HD);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  int64_t p = s;
+  if (a.pos) p = a.pb == 8 ? static_cast<const int64_t*>(a.pos)[b * a.psb + s * a.pss]
+                           : (int64_t) static_cast<const int32_t*>(a.pos)[b * a.psb + s * a.pss];
+  const int cl = lane % CPH;
+  float cv[FPU], sv[FPU];
+  bool ok = true;
+  if constexpr (TABLE) {
+    ok = p >= 0 && p < a.frows;
+    if (!ok && lane == 0 && a.err) *a.err = 1;
+    const float* frow = a.freqs + 2 * ((ok ? p : 0) * a.frs + cl * FPU);
+#pragma unroll
+    for (int q = 0; q < FPU / 2; ++q) {
+      const f32x4 t = *reinterpret_cast<const f32x4*>(frow + 4 * q);
+      cv[2 * q] = t[0];
+      sv[2 * q] = t[1];
+      cv[2 * q + 1] = t[2];
+      sv[2 * q + 1] = t[3];
+    }
+  } else {
+    // lane f < D/2 produces angle f: fp32(fp32(p) * fp32(theta^(-2f/D)))
+    const float inv = (float)pow(a.theta, -(double)(2 * lane) / (double)kFastD);
+    float sn, cn;
+    sincosf((float)p * inv, &sn, &cn);
+    cs[wave][0][lane] = cn;
+    cs[wave][1][lane] = sn;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+    for (int e = 0; e < FPU; ++e) {
+      cv[e] = cs[wave][0][cl * FPU + e];
+      sv[e] = cs[wave][1][cl * FPU + e];
+    }
+  }
+  const float sgn = a.conj ? -1.f : 1.f;
+#pragma unroll
+  for (int e = 0; e < FPU; ++e) sv[e] = sgn * sv[e];
+
+  // Per-tensor output fields as wave-uniform scalars: selected per lane from
+  // kernel-argument memory they become per-unit vector loads, and their waits
+  // (vmcnt counts stores too) would serialize the stores.
+  const int64_t ob0 = uniform64(b * T0.os[0] + s * T0.os[1]);
+  const int64_t ob1 = uniform64(b * T1.os[0] + s * T1.os[1]);
+  const int64_t hs0 = uniform64(T0.os[2]), hs1 = uniform64(T1.os[2]);
+  // tensor 1's output as a byte offset from tensor 0's (a select of pointers
+  // loses the global address space and turns the stores into flat stores)
+  char* const out0 = static_cast<char*>(T0.out);
+  const int64_t dout = uniform64(static_cast<char*>(T1.out) - out0);
+  const int f0 = __builtin_amdgcn_readfirstlane(T0.out_f32), f1 = __builtin_amdgcn_readfirstlane(T1.out_f32);
+#pragma unroll
+  for (int j = 0; j < UPL; ++j) {
+    const int u = lane + 64 * j;
+    if (u < U) {
+      const bool second = u >= U0;
+      const int ul = second ? u - U0 : u;
+      const int h = ul / CPH;
+      void* out = out0 + (second ? dout : 0);
+      const int f32 = second ? f1 : f0;
+      const int64_t oo = (second ? ob1 + h * hs1 : ob0 + h * hs0) + cl * 8;
+      float x1[8], o1[8];
+      unpack8(v1[j], x1);
+      if constexpr (kHalf) {
+        float x2[8], o2[8];
+        unpack8(v2[j], x2);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          rot(x1[e], x2[e], cv[e], sv[e], o1[e], o2[e]);
+          if (!ok) o1[e] = o2[e] = 0.f;
+        }
+        store8p(out, f32, oo, o1);
+        store8p(out, f32, oo + HD, o2);
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          rot(x1[2 * q], x1[2 * q + 1], cv[q], sv[q], o1[2 * q], o1[2 * q + 1]);
+          if (!ok) o1[2 * q] = o1[2 * q + 1] = 0.f;
+        }
+        store8p(out, f32, oo, o1);
+      }
+    }
+  }
+}
+
+typedef void (*RopeKernel)(RopeArgs);
+
+template <int PAIRING, bool TABLE>
+RopeKernel fast_for_upl(int upl) {
+  switch (upl) {
+    case 1: return rope_fast<PAIRING, TABLE, 1>;
+    case 2: return rope_fast<PAIRING, TABLE, 2>;
+    case 3: return rope_fast<PAIRING, TABLE, 3>;
+    case 4: return rope_fast<PAIRING, TABLE, 4>;
+    case 5: return rope_fast<PAIRING, TABLE, 5>;
+    case 6: return rope_fast<PAIRING, TABLE, 6>;
+    case 8: return rope_fast<PAIRING, TABLE, 8>;
+  }
+  if constexpr (PAIRING == KP_ROPE_INTERLEAVED) {
+    switch (upl) {
+      case 10: return rope_fast<PAIRING, TABLE, 10>;
+      case 12: return rope_fast<PAIRING, TABLE, 12>;
+      case 16: return rope_fast<PAIRING, TABLE, 16>;
+    }
+  }
+  return nullptr;
+}
+
+// The fast kernel for this call, or nullptr (then rope_kernel runs).
+RopeKernel pick_fast(const RopeArgs& a, int pairing, bool table) {
+  if (a.D != kFastD) return nullptr;
+  if (table && (!aligned16(a.freqs) || (a.frs & 1) != 0)) return nullptr;
+  const bool half = pairing == KP_ROPE_HALF;
+  const int64_t cph = half ? kFastD / 16 : kFastD / 8;
+  const int64_t units = (a.t[0].H + (a.nt > 1 ? a.t[1].H : 0)) * cph;
+  if (units <= 0) return nullptr;
+  int64_t upl = ceil_div(units, 64);
+  if (upl * (half ? 2 : 1) > kFastMaxLoads) return nullptr;
+  static const int kUpl[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+  for (int c : kUpl)
+    if (c >= upl) {
+      upl = c;
+      break;
+    }
+  if (half) return table ? fast_for_upl<KP_ROPE_HALF, true>((int)upl) : fast_for_upl<KP_ROPE_HALF, false>((int)upl);
+  return table ? fast_for_upl<KP_ROPE_INTERLEAVED, true>((int)upl) : fast_for_upl<KP_ROPE_INTERLEAVED, false>((int)upl);
+}
+
 bool tensor_vec_ok(const RopeTensor& t, int64_t D, int pairing) {
   if (!aligned16(t.x) || !aligned16(t.out)) return false;
   for (int i = 0; i < 3; ++i)
@@ -281,6 +459,15 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
 
   bool vec = tensor_vec_ok(a.t[0], D, pairing) && (a.nt == 1 || tensor_vec_ok(a.t[1], D, pairing));
   const int64_t blocks_needed = ceil_div(npos, kWavesPerBlock);
+  if (vec) {
+    const RopeKernel fk = pick_fast(a, pairing, freqs_cis != nullptr);
+    if (fk != nullptr && blocks_needed <= INT32_MAX) {
+      void* args[] = {&a};
+      launch_dominant_raw(reinterpret_cast<const void*>(fk), dim3((unsigned)blocks_needed), dim3(kThreads), args, 0,
+                          as_stream(stream));
+      return check_launch(who);
+    }
+  }
   const int64_t cap = (int64_t)cu_count() * 16;
   const int grid = (int)(blocks_needed < cap ? blocks_needed : cap);
   hipStream_t s = as_stream(stream);
