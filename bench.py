@@ -276,7 +276,7 @@ class Rope(Workload):
         nq, nk = B * S * Hq * D, B * S * Hk * D
         self.bytes_per_call = 2 * (nq + nk) * 2 + B * S * 8
         self.dominant_bytes = self.bytes_per_call
-        self.dominant_kernel = "rope_kernel"
+        self.dominant_kernel = "rope_fast"
         self.description = (f"C4 RoPE rotate-half: q [{B},{S},{Hq},{D}], k [{B},{S},{Hk},{D}] bf16, positions "
                             f"[{B},{S}] int64 0..{S - 1}, theta={theta:g}, cos/sin in fp32 in-kernel")
         R = self.rotations(self.bytes_per_call)
@@ -497,6 +497,7 @@ def main():
                 "kernel": w2.dominant_kernel,
                 "kernel_us": round(r2["dominant_ms"] * 1e3, 3),
                 "kernel_GBps": round(r2["achieved"], 1),
+                "kernel_bytes": w2.dominant_bytes,
                 "bytes_per_call": w2.bytes_per_call,
             }
         line["fragments"] = frags

@@ -187,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   constexpr int RB = 4 / WPR;
   constexpr int SEG = 512 * VPL;
   __shared__ float red[2][4];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int part = wave % WPR, rloc = wave / WPR;
   const int64_t col = (int64_t)part * SEG + lane * 8;
 
@@ -394,7 +394,7 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   constexpr int SEG = 512 * VPL;
   extern __shared__ float smem[];  // [RB / 2][WPR][SEG] weight-gradient combine (only when a.partial)
   __shared__ float red[2][NW][2];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int part = wave % WPR, rloc = wave / WPR;
   const int64_t col = (int64_t)part * SEG + lane * 8;
 
@@ -563,19 +563,22 @@ int env_int(const char* name, int dflt, int lo, int hi) {
 }
 // Row blocks per CU for the pipelined row kernels: enough blocks that the
 // row loads in flight per CU (waves x 2 slots x bytes per wave slot) come to
-// about 128 KiB.  Measured on MI355X: 3-stream backward rows ([16384, 8192])
-// run 5% faster at 1 block per CU than at 2, 2-stream rows of 4096 columns
-// are best at 2, and more blocks never helped.
-int auto_bpc(int waves_per_block, int64_t wave_slot_bytes, int max_bpc) {
+// about `target` bytes.  Measured on MI355X (kernel time, 4-wave blocks): the
+// forward is best near 128 KiB per CU ([4096, 4096]: 2 blocks 12.8 us, 1 block
+// 15.0 us); the backward near 64-96 KiB ([8192, 4096]: 1 block 36.7 us, 2
+// blocks 37.7 us, 3 blocks 42.2 us; [16384, 8192] with 3 input streams: 1
+// block 177 us, 2 blocks 187 us) -- more loads in flight only add DRAM
+// contention there, and fewer blocks also mean fewer weight-gradient partials.
+int auto_bpc(int waves_per_block, int64_t wave_slot_bytes, int64_t target, int max_bpc) {
   const int64_t per_block = (int64_t)waves_per_block * 2 * wave_slot_bytes;
-  const int v = (int)((128 * 1024 + per_block / 2) / per_block);
+  const int v = (int)((target + per_block / 2) / per_block);
   return v < 1 ? 1 : (v > max_bpc ? max_bpc : v);
 }
 // Launch-shape tuning knobs (read once): KP_RMS_FWD_BPC / KP_RMS_BWD_BPC, row
 // blocks per CU for the forward / backward grids (0 or unset: auto_bpc).
 int fwd_bpc(int64_t wave_slot_bytes) {
   static const int v = env_int("KP_RMS_FWD_BPC", 0, 0, 64);
-  return v ? v : auto_bpc(4, wave_slot_bytes, 8);
+  return v ? v : auto_bpc(4, wave_slot_bytes, 128 * 1024, 8);
 }
 // Backward block shape: KP_RMS_BWD_WAVES waves per block (4 or 8).
 int bwd_waves() {
@@ -585,7 +588,7 @@ int bwd_waves() {
 // At most 4 blocks per CU: the workspace holds one partial row per block.
 int bwd_bpc(int64_t wave_slot_bytes) {
   static const int v = env_int("KP_RMS_BWD_BPC", 0, 0, 4);
-  return v ? v : auto_bpc(bwd_waves(), wave_slot_bytes, 4);
+  return v ? v : auto_bpc(bwd_waves(), wave_slot_bytes, 64 * 1024, 4);
 }
 
 // Fast-path row shapes: N = 512 * VPL * WPR, at most 5 16-byte chunks per
