@@ -133,16 +133,43 @@ __global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a) {
   // The keys are unique, so their initial placement does not change the
   // sorted result: load them coalesced (element e of thread tid is token
   // base + e * 256 + tid) and sort positions 8 * tid + e.
+  // All 8 index loads go out before any of them is used: the error-flag
+  // store below may alias the index buffer as far as the compiler knows, so
+  // loading and checking one index at a time serializes 8 memory round trips.
+  // Slots past the end re-read the last index (never used); with no tokens
+  // at all (the index buffer may be NULL) nothing is read.
+  // The index width is tested once for the whole batch (a per-load branch
+  // makes the compiler wait after every int32 load).
+  int64_t id8[8];
+  if (a.T > 0 && a.ib == 8) {
+    const int64_t* ix = static_cast<const int64_t*>(a.idx);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t t = base + e * kThreads + tid;
+      id8[e] = ix[t < a.T ? t : a.T - 1];
+    }
+  } else if (a.T > 0) {
+    const int32_t* ix = static_cast<const int32_t*>(a.idx);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int64_t t = base + e * kThreads + tid;
+      id8[e] = ix[t < a.T ? t : a.T - 1];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) id8[e] = 0;
+  }
   uint32_t k8[8];
   int nvalid = 0;
+  bool bad = false;
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int64_t t = base + e * kThreads + tid;
+    const int64_t id = id8[e];
     uint32_t key = kSentinel;
     if (t < a.T) {
-      const int64_t id = load_index(a.idx, a.ib, t);
       const bool in_range = id >= 0 && id < a.V;
-      if (!in_range && a.err) *a.err = 1;
+      bad |= !in_range;
       if (in_range && id != a.padding_idx) {
         key = ((uint32_t)id << a.tbits) | (uint32_t)t;
         ++nvalid;
@@ -150,6 +177,7 @@ __global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a) {
     }
     k8[e] = key;
   }
+  if (bad && a.err) *a.err = 1;
 
 #pragma unroll
   for (int k = 2; k <= kChunk; k <<= 1) {
@@ -213,8 +241,20 @@ __global__ __launch_bounds__(kThreads) void emb_rank(EmbBwdArgs a) {
   extern __shared__ uint32_t lds_keys[];
   const int total = a.nchunks * kChunk;
   if constexpr (IN_LDS) {
-    for (int i = threadIdx.x * 4; i < total; i += kThreads * 4)
-      *reinterpret_cast<u32x4*>(lds_keys + i) = *reinterpret_cast<const u32x4*>(a.keys_chunk + i);
+    // up to kMaxLdsChunks * kChunk keys = 16 vectors per thread, all loads
+    // issued before the LDS writes (a load-write loop waits per iteration)
+    constexpr int kPer = kMaxLdsChunks * kChunk / (kThreads * 4);
+    u32x4 v[kPer];
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = (k * kThreads + threadIdx.x) * 4;
+      v[k] = *reinterpret_cast<const u32x4*>(a.keys_chunk + (i < total ? i : 0));
+    }
+#pragma unroll
+    for (int k = 0; k < kPer; ++k) {
+      const int i = (k * kThreads + threadIdx.x) * 4;
+      if (i < total) *reinterpret_cast<u32x4*>(lds_keys + i) = v[k];
+    }
     __syncthreads();
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
