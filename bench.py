@@ -24,7 +24,12 @@ sides, no per-kernel instrumentation inside).  roofline.achieved = the
 dominant kernel's algorithmic bytes / its mean duration, from a second pass
 over K steps with HIP events that the library has the runtime stamp at that
 kernel's own start and completion (kp_profile_dominant_kernel ->
-hipExtLaunchKernel), on the stream the kernel runs on.  The cpu_baseline is the torch CPU eager restatement of the
+hipExtLaunchKernel), on the stream the kernel runs on.  roofline.ceiling is
+the same measurement for kp_stream_probe -- plain one-shot streaming of the
+workload's byte mix (same number and sizes of arrays read and written,
+16-byte non-temporal accesses) -- so kernel_frac_of_ceiling says how close
+the kernel comes to what this GPU streams for those bytes.  The
+cpu_baseline is the torch CPU eager restatement of the
 fragment (oracle/torch_ref.py) on the same seeded inputs.
 """
 from __future__ import annotations
@@ -58,6 +63,9 @@ class Workload:
     dominant_bytes = 0       # algorithmic bytes moved by the dominant kernel
     dominant_kernel = ""
     cpu_sample = ""
+    # streaming-ceiling probe of the same byte mix: (inputs, outputs, bytes per
+    # input array, bytes per output array, description)
+    probe_mix = None
 
     def __init__(self, dev):
         self.dev = dev
@@ -116,6 +124,7 @@ class RmsFwd(Workload):
             self.description = f"C5 residual add + RMSNorm forward: x, res [{M},{N}] bf16 -> h, y bf16 (eps={eps})"
         else:
             self.description = f"C1 RMSNorm forward: x [{M},{N}] bf16 -> y bf16, rstd fp32 (eps={eps})"
+        self.probe_mix = (n_in, n_out, M * N * 2, M * N * 2, f"{n_in} read(s) + {n_out} write(s) of {M * N * 2 / 1e6:.1f} MB")
         per_set = self.bytes_per_call
         R = self.rotations(per_set)
         xd, wd = self.x.to(dev), self.w.to(dev)
@@ -159,6 +168,7 @@ class RmsBwd(Workload):
         self.dominant_bytes = (n_in + 1) * M * N * 2 + N * 2
         self.bytes_per_call = self.dominant_bytes + N * 4
         self.dominant_kernel = "rms_bwd_vec"
+        self.probe_mix = (n_in, 1, M * N * 2, M * N * 2, f"{n_in} reads + 1 write of {M * N * 2 / 1e6:.1f} MB")
         if residual:
             self.description = (f"C5 residual add + RMSNorm backward: x, res, dy [{M},{N}] bf16 -> dx bf16, dw fp32 "
                                 f"(h, rstd recomputed; eps={eps})")
@@ -206,6 +216,7 @@ class EmbFwd(Workload):
         self.bytes_per_call = 2 * T * D * 2 + T * 8
         self.dominant_bytes = self.bytes_per_call
         self.dominant_kernel = "emb_fwd"
+        self.probe_mix = (1, 1, T * D * 2, T * D * 2, f"copy of {T * D * 2 / 1e6:.1f} MB (the gather's bytes)")
         uniq = int(torch.unique(self.ids).numel())
         self.description = (f"C3 embedding forward: table [{V},{D}] bf16, ids [{B},{S}] int64 Zipf(1.1) "
                             f"({uniq} distinct) -> [{B},{S},{D}] bf16, bit-exact gather")
@@ -239,6 +250,8 @@ class EmbBwd(Workload):
         self.bytes_per_call = T * D * 2 + T * 8 + V * D * 4
         self.dominant_bytes = self.bytes_per_call
         self.dominant_kernel = "emb_dense"
+        self.probe_mix = (1, 1, T * D * 2, V * D * 4,
+                          f"read {T * D * 2 / 1e6:.1f} MB + write {V * D * 4 / 1e6:.1f} MB")
         uniq = int(torch.unique(self.ids).numel())
         self.description = (f"C3 embedding backward: grad [{B},{S},{D}] bf16, ids Zipf(1.1) ({uniq} distinct) -> "
                             f"dense fp32 [{V},{D}], sort-and-segment, each row written once")
@@ -277,6 +290,7 @@ class Rope(Workload):
         self.bytes_per_call = 2 * (nq + nk) * 2 + B * S * 8
         self.dominant_bytes = self.bytes_per_call
         self.dominant_kernel = "rope_fast"
+        self.probe_mix = (1, 1, (nq + nk) * 2, (nq + nk) * 2, f"copy of {(nq + nk) * 2 / 1e6:.1f} MB (q and k)")
         self.description = (f"C4 RoPE rotate-half: q [{B},{S},{Hq},{D}], k [{B},{S},{Hk},{D}] bf16, positions "
                             f"[{B},{S}] int64 0..{S - 1}, theta={theta:g}, cos/sin in fp32 in-kernel")
         R = self.rotations(self.bytes_per_call)
@@ -367,6 +381,51 @@ def measure_gpu(wl, steps, warmup):
     }
 
 
+def measure_probe(wl, steps, warmup):
+    """The streaming ceiling of the workload's byte mix: kp_stream_probe over
+    fresh arrays of the same sizes (rotated past the Infinity Cache like the
+    workload's own), timed per launch like the dominant kernel."""
+    import torch
+    from kernelproblems_amd import _lib as L
+    if wl.probe_mix is None:
+        return None
+    n_in, n_out, in_b, out_b, text = wl.probe_mix
+    lib = L.lib()
+    stream = torch.cuda.current_stream(wl.dev).cuda_stream
+    per_set = n_in * in_b + n_out * out_b
+    R = max(2, math.ceil(MIN_ROTATION_BYTES / per_set))
+    sets = []
+    for _ in range(R):
+        ins = [torch.empty(in_b, dtype=torch.uint8, device=wl.dev) for _ in range(n_in)]
+        outs = [torch.empty(out_b, dtype=torch.uint8, device=wl.dev) for _ in range(n_out)]
+        for t in ins:
+            t.fill_(1)
+        sets.append((L.ptr_array([t.data_ptr() for t in ins]), L.ptr_array([t.data_ptr() for t in outs]), ins, outs))
+
+    def launch(i):
+        ip, op, _, _ = sets[i % R]
+        st = lib.kp_stream_probe(ip, n_in, in_b, op, n_out, out_b, stream)
+        if st != 0:
+            raise L.KPError("kp_stream_probe", st, lib.kp_last_error_message().decode())
+
+    for i in range(warmup):
+        launch(i)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    for e in starts + stops:
+        e.record()
+    torch.cuda.synchronize()
+    for i in range(steps):
+        lib.kp_profile_dominant_kernel(starts[i].cuda_event, stops[i].cuda_event)
+        launch(warmup + i)
+    lib.kp_profile_dominant_kernel(None, None)
+    torch.cuda.synchronize()
+    ms = sum(starts[i].elapsed_time(stops[i]) for i in range(steps)) / steps
+    del sets
+    torch.cuda.empty_cache()
+    return {"GBps": per_set / (ms * 1e-3) / 1e9, "us": ms * 1e3, "mix": text, "bytes": per_set}
+
+
 def measure_cpu(wl, seconds):
     import torch
     wl.cpu_run()  # warm-up
@@ -391,6 +450,14 @@ def measure_cpu(wl, seconds):
     }
 
 
+def _ceiling_json(r):
+    c = r.get("ceiling")
+    if not c:
+        return None
+    return {"GBps": round(c["GBps"], 1), "frac_of_peak": round(c["GBps"] / PEAK_GBS, 4), "probe_us": round(c["us"], 3),
+            "mix": c["mix"], "kernel_frac_of_ceiling": round(r["achieved"] / c["GBps"], 4)}
+
+
 def load_traffic(name):
     p = ROOT / "profiles" / "traffic.json"
     try:
@@ -407,6 +474,7 @@ def main():
     ap.add_argument("--workload", default="c2", choices=ALL)
     ap.add_argument("--all", action="store_true", help="also measure every other workload (GPU only)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-probe", action="store_true", help="skip the streaming-ceiling probe")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the workload, run 5 plain device copies of this many MiB (a known-size "
@@ -432,6 +500,11 @@ def main():
         r = measure_gpu(wl, args.steps, args.warmup)
         print(f"[bench] {name}: {r['ms_per_step'] * 1e3:.1f} us/call, {r['value']:.0f} GB/s, dominant kernel "
               f"{r['dominant_ms'] * 1e3:.1f} us -> {r['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+        r["ceiling"] = None if args.no_probe else measure_probe(wl, args.steps, args.warmup)
+        if r["ceiling"]:
+            c = r["ceiling"]
+            print(f"[bench] {name}: streaming ceiling of its mix ({c['mix']}): {c['us']:.1f} us -> {c['GBps']:.0f} GB/s; "
+                  f"dominant kernel at {r['achieved'] / c['GBps']:.1%} of it", file=sys.stderr, flush=True)
         cpu = None
         if with_cpu:
             print(f"[bench] cpu baseline {name}", file=sys.stderr, flush=True)
@@ -480,6 +553,7 @@ def main():
             "kernel": wl.dominant_kernel,
             "kernel_us": round(r["dominant_ms"] * 1e3, 3),
             "kernel_bytes": wl.dominant_bytes,
+            "ceiling": _ceiling_json(r),
         },
         "cpu_baseline": cpu,
     }
@@ -498,6 +572,7 @@ def main():
                 "kernel_us": round(r2["dominant_ms"] * 1e3, 3),
                 "kernel_GBps": round(r2["achieved"], 1),
                 "kernel_bytes": w2.dominant_bytes,
+                "ceiling": _ceiling_json(r2),
                 "bytes_per_call": w2.bytes_per_call,
             }
         line["fragments"] = frags

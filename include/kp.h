@@ -56,7 +56,8 @@ const char* kp_last_error_message(void);
  * stop_event (hipEvent_t, timing enabled) at that kernel's own start and
  * completion: the row kernel of the RMSNorm entry points, the gather kernel
  * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
- * the kernel of kp_rope_bf16 and the copy kernel of kp_unshard_bf16.
+ * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16 and the
+ * kernel of kp_stream_probe.
  * Pass NULL, NULL to clear.  Per calling thread. */
 void kp_profile_dominant_kernel(void* start_event, void* stop_event);
 
@@ -119,6 +120,18 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
                         float* dw_f32, void* dw_bf16, int dw_f32_round_bf16,
                         int64_t M, int64_t N, float eps,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Streaming-ceiling probe (a measurement aid; no counterpart in the
+ * reference).  Reads n_in (0..3) arrays of in_bytes each and writes n_out
+ * (1..2) arrays of out_bytes each (sizes multiples of 16, arrays 16-byte
+ * aligned) with the fragment kernels' access form: 16-byte non-temporal
+ * loads and stores, 1 KiB per wave instruction, one-shot grid.  bench.py
+ * times it on each workload's byte mix to report the bandwidth plain
+ * streaming of those bytes reaches on this GPU.
+ */
+int kp_stream_probe(const void* const* in, int n_in, int64_t in_bytes, void* const* out, int n_out,
+                    int64_t out_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
  * Embedding forward: out[t, :] = table[indices[t], :] (bit copy).

@@ -105,3 +105,11 @@ def test_empty_work_is_ok_without_device(lib):
     assert lib.kp_rmsnorm_fwd_bf16(L.ptr_array([None]), one, 1, None, 8, 8, None, 8, None, 8, None, 0, 8, 1e-5,
                                    None) == L.KP_OK
     assert lib.kp_unshard_bf16(None, 8, 64, None, None, None, 0, None) == L.KP_OK
+
+
+def test_stream_probe_validation(lib):
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 4, 64, L.ptr_array([32]), 1, 64, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 60, L.ptr_array([32]), 1, 64, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, None)
+    assert lib.kp_stream_probe(None, 0, 0, L.ptr_array([32]), 1, 0, None) == L.KP_OK  # nothing to stream
