@@ -106,10 +106,6 @@ __device__ __forceinline__ float wave_sum(float v) {
   return (r0 + r1) + (r2 + r3);
 }
 
-// Register barrier: the compiler must assume v changed, so values derived
-// from it earlier (e.g. unpacked fp32 copies) are not kept live across this
-// point; cheap re-derivation beats halving occupancy.  Emits no instruction.
-__device__ __forceinline__ void reg_barrier(u32x4& v) { asm volatile("" : "+v"(v)); }
 
 __host__ __device__ __forceinline__ int64_t ceil_div_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
 

@@ -129,23 +129,21 @@ __device__ __forceinline__ void load_weight(u32x4 (&wv)[VPL], const uint16_t* w,
 // ------------------------------------------------------------------ forward
 // One row (this wave's column segment of it): bf16 term sum, sum of squares,
 // cross-wave combine, y = bf16(h * rstd * w), optional h and rstd stores.
+// The summed row is unpacked to fp32 once for both passes and the weight
+// stays in fp32 registers for the whole kernel (see bwd_row).
 template <int VPL, int WPR, int NX>
-__device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, NX>& cur, u32x4 (&wv)[VPL],
+__device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, NX>& cur, const float (&wf)[VPL * 8],
                                         float (&red)[2][4], int64_t row, int64_t col, int lane, int wave, int part,
                                         int rloc, int it) {
   const bool valid = row < a.M;
   u32x4 hv[VPL];
   sum_raw<VPL, NX>(hv, cur);
+  float hf[VPL * 8];
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
+  for (int i = 0; i < VPL; ++i) unpack8(hv[i], hf + i * 8);
   float ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    float f[8];
-    unpack8(hv[i], f);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) ss = fmaf(f[e], f[e], ss);
-  }
+  for (int j = 0; j < VPL * 8; ++j) ss = fmaf(hf[j], hf[j], ss);
   ss = wave_sum(ss);
   if constexpr (WPR > 1) {
     if (lane == 0) red[it & 1][wave] = ss;
@@ -156,17 +154,13 @@ __device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, N
     ss = t;
   }
   const float r = 1.0f / sqrtf(ss / (float)a.N + a.eps);
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) reg_barrier(hv[i]);
   if (valid) {
     uint16_t* yrow = a.y + row * a.ys + col;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      float f[8], wf[8], o[8];
-      unpack8(hv[i], f);
-      unpack8(wv[i], wf);
+      float o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[e] = (f[e] * r) * wf[e];
+      for (int e = 0; e < 8; ++e) o[e] = (hf[i * 8 + e] * r) * wf[i * 8 + e];
       st16_stream(yrow + i * 512, pack8(o));
     }
     if (NX > 1 && a.h != nullptr) {
@@ -193,8 +187,13 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   const int part = wave % WPR, rloc = wave / WPR;
   const int64_t col = (int64_t)part * SEG + lane * 8;
 
-  u32x4 wv[VPL];
-  load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
+  float wf[VPL * 8];
+  {
+    u32x4 wv[VPL];
+    load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) unpack8(wv[i], wf + i * 8);
+  }
 
   const int64_t ngroups = ceil_div_dev(a.M, RB);
   const int64_t G = gridDim.x;
@@ -205,7 +204,7 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   load_raw<VPL, NX>(S, a.x, a.xs, clamp_row(KP_ROW(g), a.M), col); \
   __builtin_amdgcn_sched_barrier(0)
 #define KP_PROC(S, g)                                                               \
-  fwd_row<VPL, WPR, NX>(a, S, wv, red, KP_ROW(g), col, lane, wave, part, rloc, it); \
+  fwd_row<VPL, WPR, NX>(a, S, wf, red, KP_ROW(g), col, lane, wave, part, rloc, it); \
   ++it
   // Exact trip count: the grid never exceeds the row-group count, so every
   // block owns nb >= 1 groups and nothing is prefetched past its last one.
@@ -275,31 +274,35 @@ __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& 
 
 // One row of the backward: dx (with the residual epilogue) and this row's
 // contribution dy * xhat to the per-column weight-gradient accumulators.
+// The row's x and dy are unpacked to fp32 once and kept across both passes,
+// and the weight stays in fp32 registers for the whole kernel: unpacking
+// them again in the second pass (to save registers) made the loop ~16 VALU
+// instructions per element against ~10 now, and the backward grids run one
+// wave per SIMD, so the registers are free.
 template <int VPL, int WPR, int NX, int NDY, bool RES, int NW>
 __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, NX>& xr, const RawRow<VPL, NDY>& dr,
-                                        const RawRow<VPL, 1>& rr, float rq, u32x4 (&wv)[VPL], float (&acc)[VPL * 8],
-                                        float (&red)[2][NW][2], int64_t row, int64_t col, int lane, int wave, int rloc,
-                                        int it) {
+                                        const RawRow<VPL, 1>& rr, float rq, const float (&wf)[VPL * 8],
+                                        float (&acc)[VPL * 8], float (&red)[2][NW][2], int64_t row, int64_t col,
+                                        int lane, int wave, int rloc, int it) {
   const bool valid = row < a.M;
   const float inv_n = 1.0f / (float)a.N;
-  u32x4 xv[VPL], dv[VPL];
-  sum_raw<VPL, NX>(xv, xr);
-  sum_raw<VPL, NDY>(dv, dr);
+  float xf[VPL * 8], df[VPL * 8];
+  {
+    u32x4 xv[VPL], dv[VPL];
+    sum_raw<VPL, NX>(xv, xr);
+    sum_raw<VPL, NDY>(dv, dr);
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) reg_barrier(wv[i]);
+    for (int i = 0; i < VPL; ++i) {
+      unpack8(xv[i], xf + i * 8);
+      unpack8(dv[i], df + i * 8);
+    }
+  }
   // sum(x * g) and, when rstd is not supplied, sum(x^2), in one sweep.
   float sxg = 0.f, ss = 0.f;
 #pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    float xf[8], df[8], wf[8];
-    unpack8(xv[i], xf);
-    unpack8(dv[i], df);
-    unpack8(wv[i], wf);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      sxg = fmaf(xf[e], df[e] * wf[e], sxg);
-      ss = fmaf(xf[e], xf[e], ss);
-    }
+  for (int j = 0; j < VPL * 8; ++j) {
+    sxg = fmaf(xf[j], df[j] * wf[j], sxg);
+    ss = fmaf(xf[j], xf[j], ss);
   }
   sxg = wave_sum(sxg);
   if (a.rstd == nullptr) ss = wave_sum(ss);
@@ -321,26 +324,18 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
   const float r = (a.rstd != nullptr) ? rq : 1.0f / sqrtf(ss / (float)a.N + a.eps);
   // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
   const float cN = (r * sxg) * inv_n;
-#pragma unroll
-  for (int i = 0; i < VPL; ++i) {
-    reg_barrier(xv[i]);
-    reg_barrier(dv[i]);
-    reg_barrier(wv[i]);
-  }
   if (valid) {
     uint16_t* dxrow = a.dx + row * a.dxs + col;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      float xf[8], df[8], wf[8], o[8];
-      unpack8(xv[i], xf);
-      unpack8(dv[i], df);
-      unpack8(wv[i], wf);
+      float o[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float xh = xf[e] * r;
-        const float gg = df[e] * wf[e];
+        const int j = i * 8 + e;
+        const float xh = xf[j] * r;
+        const float gg = df[j] * wf[j];
         o[e] = (gg - xh * cN) * r;
-        acc[i * 8 + e] = fmaf(df[e], xh, acc[i * 8 + e]);
+        acc[j] = fmaf(df[j], xh, acc[j]);
       }
       u32x4 ov = pack8(o);
       if constexpr (RES) ov = add_bf8(rr.v[0][i], ov);
@@ -362,8 +357,13 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   const int part = wave % WPR, rloc = wave / WPR;
   const int64_t col = (int64_t)part * SEG + lane * 8;
 
-  u32x4 wv[VPL];
-  load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
+  float wf[VPL * 8];
+  {
+    u32x4 wv[VPL];
+    load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) unpack8(wv[i], wf + i * 8);
+  }
 
   float acc[VPL * 8];
 #pragma unroll
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   bwd_load<VPL, NX, NDY, RES>(x##S, d##S, r##S, q##S, a, clamp_row(KP_ROW(g), a.M), col); \
   __builtin_amdgcn_sched_barrier(0)
 #define KP_PROC(S, g)                                                                                               \
-  bwd_row<VPL, WPR, NX, NDY, RES, NW>(a, x##S, d##S, r##S, q##S, wv, acc, red, KP_ROW(g), col, lane, wave, rloc, it); \
+  bwd_row<VPL, WPR, NX, NDY, RES, NW>(a, x##S, d##S, r##S, q##S, wf, acc, red, KP_ROW(g), col, lane, wave, rloc, it); \
   ++it
   // Exact trip count (see rms_fwd_vec): nb >= 1 groups per block.
   const int64_t nb = (ngroups - 1 - blockIdx.x) / G + 1;
