@@ -140,3 +140,27 @@ def test_embedding_bwd_empty(gpu):
     out = kp.embedding_dense_backward(torch.empty((0, 64), dtype=torch.bfloat16, device=gpu),
                                       torch.empty(0, dtype=torch.int64, device=gpu), 10)
     assert out.shape == (10, 64) and torch.count_nonzero(out) == 0
+
+
+def test_embedding_bwd_on_side_stream_repeated(gpu, oracle_lib):
+    """Calls issued on a non-default torch stream, back to back, must give the
+    oracle's rows and identical bits each time: the window tickets that let
+    the last window block of a spanning run finish it are cleared by every
+    call, and all of a call's work stays ordered on the caller's stream."""
+    g = gen(26)
+    V, D, T = 3000, 2048, 8192
+    ids = zipf_ids(T, V, 1.1, g)
+    grad = randn_bf16((T, D), g)
+    exact = oracle_lib.embedding_bwd_dense(to_u16(grad), ids.numpy(), V)
+    side = torch.cuda.Stream(device=gpu)
+    gd, idd = grad.to(gpu), ids.to(gpu)
+    torch.cuda.synchronize()
+    outs = []
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            o = kp.embedding_dense_backward(gd, idd, V)
+            outs.append(o.clone())  # enqueued on `side` after the join
+    torch.cuda.synchronize()
+    for o in outs[1:]:
+        assert torch.equal(o, outs[0])
+    np.testing.assert_allclose(outs[0].cpu().numpy(), exact, rtol=1e-5, atol=1e-5)
