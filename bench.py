@@ -14,6 +14,8 @@ BASELINE.json configurations:
   c4   RoPE rotate-half       q [4, 4096, 32, 128], k [4, 4096, 8, 128], pos 0..4095, theta 5e5
   c5f  add + RMSNorm forward  x, res [16384, 8192]        -> h, y bf16
   c5b  add + RMSNorm backward x, res, dy [16384, 8192]    -> dx bf16, dw fp32
+  swf  SwiGLU gate forward    a, b [8192, 14336]          -> bf16(silu(a)) * b        (v8/c68dae22972b)
+  swb  SwiGLU gate backward   g, s, b, a [8192, 14336]    -> db, da bf16              (v8/385e1beb9bb9)
 
 Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 ~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
@@ -312,6 +314,53 @@ class Rope(Workload):
         torch_ref.rope_half(self.q, self.k, self.pos, self.theta)
 
 
+# ------------------------------------------------------------------ SwiGLU
+class SwiGlu(Workload):
+    """The feed-forward gate region at its reference shape: forward reads the
+    w1 / w3 outputs and writes the gate product; backward reads the product's
+    gradient, silu(w1 out), w3 out, w1 out and writes both branch gradients."""
+
+    def __init__(self, dev, M=8192, N=14336, backward=False, name="swf"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        self.backward = backward
+        g = _gen(0)
+        n_in, n_out = (4, 2) if backward else (2, 1)
+        self.ops = [_randn((M, N), g) for _ in range(n_in)]
+        self.bytes_per_call = (n_in + n_out) * M * N * 2
+        self.dominant_bytes = self.bytes_per_call
+        self.dominant_kernel = "swiglu_bwd_vec" if backward else "swiglu_fwd_vec"
+        self.probe_mix = (n_in, n_out, M * N * 2, M * N * 2,
+                          f"{n_in} reads + {n_out} write(s) of {M * N * 2 / 1e6:.1f} MB")
+        if backward:
+            self.description = (f"SwiGLU gate backward (v8/385e1beb9bb9): g, silu(a), b, a [{M},{N}] bf16 -> "
+                                f"db = g*silu(a), da = silu_backward(g*b, a) bf16")
+        else:
+            self.description = f"SwiGLU gate forward (v8/c68dae22972b): a, b [{M},{N}] bf16 -> bf16(silu(a)) * b bf16"
+        R = self.rotations(self.bytes_per_call)
+        dev_ops = [t.to(dev) for t in self.ops]
+        fn = L.lib().kp_swiglu_bwd_bf16 if backward else L.lib().kp_swiglu_fwd_bf16
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for r in range(R):
+            ins = [t if r == 0 else t.clone() for t in dev_ops]
+            outs = [torch.empty((M, N), dtype=torch.bfloat16, device=dev) for _ in range(n_out)]
+            ptrs = []
+            for t in ins + outs:
+                ptrs += [t.data_ptr(), N]
+            args = (*ptrs, M, N, stream)
+            self.sets.append((fn, args, (ins, outs)))
+        self.cpu_sample = f"full [{M},{N}] call"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        if self.backward:
+            torch_ref.swiglu_bwd(*self.ops)
+        else:
+            torch_ref.swiglu_fwd(*self.ops)
+
+
 def make_workload(name, dev):
     if name == "c1":
         return RmsFwd(dev, 4096, 4096, 1e-6, "c1")
@@ -327,10 +376,14 @@ def make_workload(name, dev):
         return RmsFwd(dev, 16384, 8192, 1e-5, "c5f", residual=True, rstd=False)
     if name == "c5b":
         return RmsBwd(dev, 16384, 8192, 1e-5, "c5b", residual=True)
+    if name == "swf":
+        return SwiGlu(dev, name="swf")
+    if name == "swb":
+        return SwiGlu(dev, backward=True, name="swb")
     raise SystemExit(f"unknown workload {name!r}")
 
 
-ALL = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
+ALL = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b", "swf", "swb"]
 
 
 # ------------------------------------------------------------------ measure

@@ -56,8 +56,9 @@ const char* kp_last_error_message(void);
  * stop_event (hipEvent_t, timing enabled) at that kernel's own start and
  * completion: the row kernel of the RMSNorm entry points, the gather kernel
  * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
- * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16 and the
- * kernel of kp_stream_probe.
+ * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16, the
+ * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16 and the kernel of
+ * kp_stream_probe.
  * Pass NULL, NULL to clear.  Per calling thread. */
 void kp_profile_dominant_kernel(void* start_event, void* stop_event);
 
@@ -123,7 +124,7 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
 
 /* ------------------------------------------------------------------------
  * Streaming-ceiling probe (a measurement aid; no counterpart in the
- * reference).  Reads n_in (0..3) arrays of in_bytes each and writes n_out
+ * reference).  Reads n_in (0..4) arrays of in_bytes each and writes n_out
  * (1..2) arrays of out_bytes each (sizes multiples of 16, arrays 16-byte
  * aligned) with the fragment kernels' access form: 16-byte non-temporal
  * loads and stores, 1 KiB per wave instruction, one-shot grid.  bench.py
@@ -226,6 +227,38 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
  */
 int kp_unshard_bf16(const void* src, int64_t shards, int64_t shard_stride,
                     const int64_t* col_off, const int64_t* col_len, void* const* dst, int n_seg, void* stream);
+
+/* ------------------------------------------------------------------------
+ * SwiGLU gate forward: out = bf16(bf16(silu(a)) * b), silu(x) = x / (1 + exp(-x))
+ * in fp32 (eager bf16 silu rounds its result to bf16 before the multiply).
+ *
+ * Replaces the silu.default -> mul.Tensor region at
+ * v8/c68dae22972b/problem.py:15-28 (a = w1 output mm_4, b = w3 output mm_5,
+ * bf16 [8192, 14336]).
+ * a, b, out: bf16 [M, N] with unit inner stride and the given row strides
+ * (elements; ignored when M == 1).  out may be one of the inputs (in place);
+ * partial overlap is undefined.
+ */
+int kp_swiglu_fwd_bf16(const void* a, int64_t a_stride, const void* b, int64_t b_stride,
+                       void* out, int64_t out_stride, int64_t M, int64_t N, void* stream);
+
+/* ------------------------------------------------------------------------
+ * SwiGLU gate backward:
+ *   db = bf16(g * s)
+ *   da = bf16(t * sig * (1 + a * (1 - sig))),  t = bf16(g * b),  sig = 1 / (1 + exp(-a))
+ * all in fp32 from bf16 operands (aten mul.Tensor, then silu_backward).
+ *
+ * Replaces the mul.Tensor, mul.Tensor -> silu_backward.default region at
+ * v8/385e1beb9bb9/problem.py:17-33: g = mm_662 (gradient of the gate
+ * product), s = silu_recomputed, b = _unsafe_view_5_recomputed (w3 output),
+ * a = _unsafe_view_4_recomputed (w1 output); db is the first output (the w3
+ * branch gradient), da the second (the w1 branch gradient).
+ * All arrays bf16 [M, N], unit inner stride, row strides in elements.
+ */
+int kp_swiglu_bwd_bf16(const void* g, int64_t g_stride, const void* s, int64_t s_stride,
+                       const void* b, int64_t b_stride, const void* a, int64_t a_stride,
+                       void* db, int64_t db_stride, void* da, int64_t da_stride,
+                       int64_t M, int64_t N, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,7 +1,7 @@
 """MI355X (gfx950) kernels for the memory-bound fused graph fragments of
 SherlockNoMad/KernelProblems: RMSNorm forward/backward (with residual-add and
 gradient epilogues), embedding gather and its dense deterministic backward,
-and rotary position embedding on q/k.
+rotary position embedding on q/k, and the SwiGLU gate forward/backward.
 
 Layers:
   * ``include/kp.h`` + ``csrc/*.hip``  -- the C ABI and the HIP kernels;
@@ -21,6 +21,8 @@ from .fused import (
     rms_norm_backward,
     rope,
     set_index_checking,
+    swiglu,
+    swiglu_backward,
     unshard,
 )
 
@@ -36,6 +38,8 @@ __all__ = [
     "rms_norm_backward",
     "rope",
     "set_index_checking",
+    "swiglu",
+    "swiglu_backward",
     "unshard",
     "version",
 ]

@@ -22,6 +22,8 @@ FRAGMENTS = (
     # RoPE (interleaved complex, table) forward / backward
     "v7/e29b92927600", "v8/493cad38cac9", "v8/c8c60d8f7015", "v8/97032595d968", "v7/0f38bc55457c",
     "v7/5c65f62b0422", "v7/bfe872e373e4",
+    # SwiGLU gate forward / backward
+    "v8/c68dae22972b", "v8/385e1beb9bb9",
 )
 
 

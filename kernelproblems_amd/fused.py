@@ -433,3 +433,49 @@ def unshard(flat: torch.Tensor, shards: int, split_sizes: Sequence[int], keep: S
             L.ptr_array([outs[i].data_ptr() for i in sel]), len(sel), _stream(flat.device),
         )
     return outs
+
+
+# ---------------------------------------------------------------- SwiGLU gate
+def _same_rows(name: str, ts: Sequence[torch.Tensor]):
+    """Views of same-shape bf16 GPU tensors as [rows, N] (unit inner stride)."""
+    shape = ts[0].shape
+    for i, t in enumerate(ts):
+        _need_gpu(f"{name} operand {i}", t)
+        if t.numel() != ts[0].numel() or (t.dim() and t.shape[-1] != shape[-1]):
+            raise RuntimeError(f"{name}: operand {i} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+        if t.device != ts[0].device:
+            raise RuntimeError(f"{name}: operands on different devices")
+    n = shape[-1] if len(shape) else 1
+    if n == 0 or ts[0].numel() == 0:
+        return [(t, max(n, 1), 0) for t in ts], n
+    return [_as_rows(t, n) for t in ts], n
+
+
+def swiglu(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
+    """bf16(bf16(silu(a)) * b): the silu -> mul region between the w1/w3 and
+    w2 projections of a feed-forward block (v8/c68dae22972b/problem.py:15-28),
+    fp32 arithmetic (silu = a / (1 + exp(-a))).  Returns a contiguous tensor
+    of a's shape."""
+    (ra, rb), n = _same_rows("swiglu", [a, b])
+    out = torch.empty(a.shape, dtype=torch.bfloat16, device=a.device)
+    m = ra[2]
+    if m:
+        L.call("kp_swiglu_fwd_bf16", ra[0].data_ptr(), ra[1], rb[0].data_ptr(), rb[1], out.data_ptr(), n, m, n,
+               _stream(a.device))
+    return out
+
+
+def swiglu_backward(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.Tensor):
+    """Gradients of the SwiGLU gate out = s * b, s = silu(a), given g = dout
+    (v8/385e1beb9bb9/problem.py:17-33): db = bf16(g * s) and
+    da = silu_backward(bf16(g * b), a) = t * sig * (1 + a * (1 - sig)).
+    s is the recomputed silu(a) the graph keeps.  Returns contiguous
+    (db, da) of g's shape."""
+    (rg, rs, rb, ra), n = _same_rows("swiglu_backward", [g, s, b, a])
+    db = torch.empty(g.shape, dtype=torch.bfloat16, device=g.device)
+    da = torch.empty(g.shape, dtype=torch.bfloat16, device=g.device)
+    m = rg[2]
+    if m:
+        L.call("kp_swiglu_bwd_bf16", rg[0].data_ptr(), rg[1], rs[0].data_ptr(), rs[1], rb[0].data_ptr(), rb[1],
+               ra[0].data_ptr(), ra[1], db.data_ptr(), n, da.data_ptr(), n, m, n, _stream(g.device))
+    return db, da

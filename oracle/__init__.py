@@ -31,6 +31,12 @@ rope (theta)           ``torch.polar`` angles in fp64 (pos = 0 identity, norm
                        preservation, conj inverse), rotate-half ==
                        interleaved up to the (2i, 2i+1) <-> (i, i + D/2)
                        permutation.
+swiglu_fwd             torch CPU eager ``silu`` * b, fp64 ``x * expit(x)``
+                       (scipy), closed forms (silu(0) = 0, silu(x) -
+                       silu(-x) = x, saturation), every bf16 input value.
+swiglu_bwd             torch CPU eager ``mul`` / ``silu_backward``, central
+                       finite differences of fp64 silu, closed forms
+                       (silu'(0) = 1/2, the zero of silu' near -1.2785).
 =====================  =====================================================
 
 bf16 tensors are handled as numpy ``uint16`` bit patterns.
@@ -62,6 +68,8 @@ _SIGS = {
     "kpo_embedding_bwd_rows": (i64, [vp, i64, vp, i64, i64, i64, i64, i32, vp, vp, vp, vp, vp]),
     "kpo_embedding_bwd_dense": (i64, [vp, i64, vp, i64, i64, i64, i64, i32, i32, vp]),
     "kpo_rope": (i64, [vp, pi64, vp, pi64, i64, i64, i64, i64, vp, i64, i64, i32, f64, vp, i64, i64, i32]),
+    "kpo_swiglu_fwd": (None, [vp, vp, vp, i64]),
+    "kpo_swiglu_bwd": (None, [vp, vp, vp, vp, vp, vp, i64]),
 }
 
 
@@ -245,3 +253,24 @@ def rope(x: np.ndarray, pos: Optional[np.ndarray] = None, *, pairing: str = "hal
     if bad < 0:
         raise MemoryError("kpo_rope")
     return out
+
+
+# ---------------------------------------------------------------- SwiGLU
+def swiglu_fwd(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """bf16(bf16(silu(a)) * b) elementwise; uint16 arrays of one shape."""
+    a, b = _c(a, np.uint16), _c(b, np.uint16)
+    if a.shape != b.shape:
+        raise ValueError("swiglu_fwd: a and b differ in shape")
+    out = np.empty_like(a)
+    lib().kpo_swiglu_fwd(_p(a), _p(b), _p(out), a.size)
+    return out
+
+
+def swiglu_bwd(g: np.ndarray, s: np.ndarray, b: np.ndarray, a: np.ndarray):
+    """(db, da) = (bf16(g * s), bf16(silu_backward(bf16(g * b), a))); uint16 arrays of one shape."""
+    arrs = [_c(t, np.uint16) for t in (g, s, b, a)]
+    if any(t.shape != arrs[0].shape for t in arrs):
+        raise ValueError("swiglu_bwd: operands differ in shape")
+    db, da = np.empty_like(arrs[0]), np.empty_like(arrs[0])
+    lib().kpo_swiglu_bwd(*(_p(t) for t in arrs), _p(db), _p(da), arrs[0].size)
+    return db, da

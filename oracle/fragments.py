@@ -179,6 +179,19 @@ def _rope_bwd(g, table):                 # v7/5c65f62b0422/problem.py:16-40, v7/
     return aten.view.default(out, [out.shape[1], -1])
 
 
+def _swiglu_fwd(mm4, mm5):               # v8/c68dae22972b/problem.py:15-28
+    a = aten._unsafe_view.default(mm4, [1, *mm4.shape])
+    b = aten._unsafe_view.default(mm5, [1, *mm5.shape])
+    return aten.view.default(aten.mul.Tensor(aten.silu.default(a), b), list(mm4.shape))
+
+
+def _swiglu_bwd(g, s, b, a):             # v8/385e1beb9bb9/problem.py:17-33
+    gv = aten.view.default(g, [1, *g.shape])
+    db = aten.view.default(aten.mul.Tensor(gv, s), list(g.shape))
+    da = aten.silu_backward.default(aten.mul.Tensor(gv, b), a)
+    return db, aten.view.default(da, list(g.shape))
+
+
 _FRAGMENTS = {
     "v7/59f786beb25f": _rms_fwd_y_rstd,
     "v8/4b90e2d83144": _rms_fwd_3views,
@@ -205,6 +218,8 @@ _FRAGMENTS = {
     "v7/0f38bc55457c": _rope_qk(True),
     "v7/5c65f62b0422": _rope_bwd,
     "v7/bfe872e373e4": _rope_bwd,
+    "v8/c68dae22972b": _swiglu_fwd,
+    "v8/385e1beb9bb9": _swiglu_bwd,
 }
 
 

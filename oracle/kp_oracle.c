@@ -333,3 +333,40 @@ int64_t kpo_rope(const uint16_t* x, const int64_t* xs, uint16_t* out, const int6
   free(sv);
   return bad;
 }
+
+/* ---------------------------------------------------------------- SwiGLU
+ * Forward (v8/c68dae22972b/problem.py:15-28): silu.default of the w1 output
+ * a, materialised as bf16, then mul.Tensor with the w3 output b:
+ *   out = bf16(bf16(silu(a)) * b),  silu(x) = x / (1 + e^-x).
+ * Backward (v8/385e1beb9bb9/problem.py:17-33): db = mul.Tensor(g, s);
+ * t = mul.Tensor(g, b); da = silu_backward(t, a) =
+ *   t * sig * (1 + a * (1 - sig)),  sig = 1 / (1 + e^-a)
+ * (the derivative of x * sig(x); aten silu_backward as decomposed at
+ * torch/_decomp/decompositions.py:297-302).
+ * silu and silu_backward are evaluated in double and rounded once to bf16,
+ * the exactly rounded value of the fp32 formula's limit.  bf16 x bf16
+ * products are exact in double, so db, t and the final multiply of the
+ * forward carry exactly one rounding, as in fp32.  Contiguous arrays. */
+static double silu_d(double x) { return x / (1.0 + exp(-x)); }
+
+static double silu_bwd_d(double t, double x) {
+  const double sig = 1.0 / (1.0 + exp(-x));
+  return t * sig * (1.0 + x * (1.0 - sig));
+}
+
+void kpo_swiglu_fwd(const uint16_t* a, const uint16_t* b, uint16_t* out, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double s = (double)bf2f(d2bf(silu_d((double)bf2f(a[i]))));
+    out[i] = d2bf(s * (double)bf2f(b[i]));
+  }
+}
+
+void kpo_swiglu_bwd(const uint16_t* g, const uint16_t* s, const uint16_t* b, const uint16_t* a, uint16_t* db,
+                    uint16_t* da, int64_t n) {
+  for (int64_t i = 0; i < n; ++i) {
+    const double gv = (double)bf2f(g[i]);
+    db[i] = d2bf(gv * (double)bf2f(s[i]));
+    const double t = (double)bf2f(d2bf(gv * (double)bf2f(b[i])));
+    da[i] = d2bf(silu_bwd_d(t, (double)bf2f(a[i])));
+  }
+}

@@ -95,3 +95,13 @@ def rope_complex(x: torch.Tensor, freqs_cis: torch.Tensor):
     B, S, H, D = x.shape
     xc = torch.view_as_complex(x.to(torch.float32).reshape(B, S, H, D // 2, 2))
     return torch.view_as_real(xc * freqs_cis).reshape(B, S, H, D).to(torch.bfloat16)
+
+
+def swiglu_fwd(a: torch.Tensor, b: torch.Tensor):
+    """v8/c68dae22972b/problem.py:15-28: silu.default -> mul.Tensor."""
+    return aten.mul.Tensor(aten.silu.default(a), b)
+
+
+def swiglu_bwd(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.Tensor):
+    """v8/385e1beb9bb9/problem.py:17-33: mul.Tensor(g, s); silu_backward(mul.Tensor(g, b), a)."""
+    return aten.mul.Tensor(g, s), aten.silu_backward.default(aten.mul.Tensor(g, b), a)

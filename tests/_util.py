@@ -86,8 +86,9 @@ _BF16_TABLE = None
 def bf16_round_exact(v: np.ndarray) -> np.ndarray:
     """Correctly rounded (nearest, ties to even) float64 -> bf16 bit patterns,
     by search over the sorted table of all finite bf16 values; saturates to
-    +-inf beyond the largest finite value's rounding boundary.  Independent
-    of any float32 intermediate (no double rounding)."""
+    +-inf beyond the largest finite value's rounding boundary; NaN -> the
+    quiet NaN 0x7FC0.  Independent of any float32 intermediate (no double
+    rounding)."""
     global _BF16_TABLE
     if _BF16_TABLE is None:
         pats = np.arange(0x10000, dtype=np.uint32).astype(np.uint16)
@@ -113,5 +114,6 @@ def bf16_round_exact(v: np.ndarray) -> np.ndarray:
     res = np.where(v >= big + ulp / 2, 0x7F80, res)
     res = np.where(v <= -(big + ulp / 2), 0xFF80, res)
     res = np.where(v == 0, np.where(np.signbit(v), 0x8000, 0x0000), res)
+    res = np.where(np.isnan(v), 0x7FC0, res)
     out[:] = res
     return out.reshape(np.shape(v))

@@ -1,8 +1,9 @@
 """Writes tests/golden/golden.npz: small seeded inputs and their expected
 outputs, computed here with torch library ops in float64 (F.rms_norm and
 its autograd, torch's decomposition of _fused_rms_norm_backward, index_add_,
-torch.polar / complex multiply with torchtitan's frequency formula) and one
-correctly rounded bf16 conversion.  None of it calls the oracle or the HIP
+torch.polar / complex multiply with torchtitan's frequency formula, silu and
+the autograd of x * sigmoid(x)) and one correctly rounded bf16 conversion
+per rounding point of the reference op sequence.  None of it calls the oracle or the HIP
 kernels, which tests/test_golden.py checks against these vectors.
 
 Run from the repository root:  python -m tests.golden.make_golden
@@ -89,11 +90,36 @@ def rope_cases(d):
              rope_table=table.numpy(), rope_tpos=tpos.numpy(), rope_inter=inter.numpy())
 
 
+def swiglu_cases(d):
+    """v8/c68dae22972b (silu -> mul) and v8/385e1beb9bb9 (mul, mul ->
+    silu_backward) on a ragged [17, 43] block whose first row holds special
+    gate values (zeros, the zero of silu' near -1.2785, saturation, overflow
+    of e^-x, infinities)."""
+    g = _g(400)
+    M, N = 17, 43
+    a, b, gr, s = (_bf((M, N), g, std=3.0) for _ in range(4))
+    special = torch.tensor([0.0, -0.0, 1.0, -1.0, -1.2785, -1.28, 20.0, -20.0, 88.0, -88.0, 90.0, -90.0, 1e-30,
+                            -1e-30, 3e38, -3e38, float("inf"), float("-inf")])
+    a[0, : special.numel()] = special.to(torch.bfloat16)
+    ad = a.double()
+    s16 = bf16_round_exact(torch.nn.functional.silu(ad).numpy()).reshape(M, N)
+    sv = torch.from_numpy(s16.view(np.int16)).view(torch.bfloat16).double()
+    out = bf16_round_exact((sv * b.double()).numpy())
+    t16 = bf16_round_exact((gr.double() * b.double()).numpy()).reshape(M, N)
+    t = torch.from_numpy(t16.view(np.int16)).view(torch.bfloat16)
+    x = ad.clone().requires_grad_(True)
+    (x * torch.sigmoid(x)).backward(t.double())
+    d.update(swiglu_a=to_u16(a), swiglu_b=to_u16(b), swiglu_g=to_u16(gr), swiglu_s=to_u16(s),
+             swiglu_out=out.reshape(M, N), swiglu_db=bf16_round_exact((gr.double() * s.double()).numpy()).reshape(M, N),
+             swiglu_da_exact=x.grad.numpy())
+
+
 def main():
     d = {}
     rms_cases(d)
     embedding_cases(d)
     rope_cases(d)
+    swiglu_cases(d)
     np.savez_compressed(OUT, **d)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(d)} arrays)")
 

@@ -105,10 +105,20 @@ def test_empty_work_is_ok_without_device(lib):
     assert lib.kp_rmsnorm_fwd_bf16(L.ptr_array([None]), one, 1, None, 8, 8, None, 8, None, 8, None, 0, 8, 1e-5,
                                    None) == L.KP_OK
     assert lib.kp_unshard_bf16(None, 8, 64, None, None, None, 0, None) == L.KP_OK
+    assert lib.kp_swiglu_fwd_bf16(None, 8, None, 8, None, 8, 0, 8, None) == L.KP_OK
+    assert lib.kp_swiglu_bwd_bf16(None, 8, None, 8, None, 8, None, 8, None, 8, None, 8, 4, 0, None) == L.KP_OK
+
+
+def test_swiglu_validation(lib):
+    _expect(lib, L.KP_EINVAL, "kp_swiglu_fwd_bf16", 16, 8, 32, 8, 48, 8, -1, 8, None)  # negative M
+    _expect(lib, L.KP_EINVAL, "kp_swiglu_fwd_bf16", 16, 8, None, 8, 48, 8, 2, 8, None)  # NULL b
+    _expect(lib, L.KP_EINVAL, "kp_swiglu_fwd_bf16", 16, 8, 32, 4, 48, 8, 2, 8, None)  # b rows overlap
+    _expect(lib, L.KP_EINVAL, "kp_swiglu_bwd_bf16", 16, 8, 32, 8, 48, 8, 64, 8, 80, 8, None, 8, 2, 8, None)  # NULL da
+    _expect(lib, L.KP_EINVAL, "kp_swiglu_bwd_bf16", 16, 8, 32, 8, 48, 8, 64, 7, 80, 8, 96, 8, 2, 8, None)
 
 
 def test_stream_probe_validation(lib):
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 4, 64, L.ptr_array([32]), 1, 64, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 5, 64, L.ptr_array([32]), 1, 64, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 60, L.ptr_array([32]), 1, 64, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, None)

@@ -76,6 +76,36 @@ def test_oracle_rope_golden():
     _check_rope(out, G["rope_inter"])
 
 
+def _check_swiglu(out, db, da, exact=True):
+    if exact:
+        assert np.array_equal(out, G["swiglu_out"])
+    else:
+        # fp32 evaluation: e^-a overflows for a < -88.7, so silu(a) is -0 there
+        # where the exact value is a tiny negative number; NaN may carry a sign
+        ov, ev = bf(out), bf(G["swiglu_out"])
+        nan = np.isnan(ev)
+        assert np.array_equal(np.isnan(ov), nan)
+        fin = np.isfinite(ev)
+        assert np.array_equal(ov[~fin & ~nan], ev[~fin & ~nan])
+        assert ulp_bf16(out, G["swiglu_out"])[fin & (np.abs(ev) > 1e-30)].max() <= 1
+        assert np.all(np.abs(ov - ev)[fin] <= 1e-30 + 2.0**-8 * np.abs(ev[fin]))
+    assert np.array_equal(db, G["swiglu_db"])
+    ex = G["swiglu_da_exact"]
+    v = bf(da)
+    nan = np.isnan(ex)
+    assert np.array_equal(np.isnan(v), nan)
+    # one bf16 rounding of the exact value (signed zeros compare equal); in
+    # fp32, sig underflows to 0 for a < -88.7 where the exact da is ~1e-37
+    slack = 0.0 if exact else 1e-30
+    assert np.all(np.abs(v[~nan] - ex[~nan]) <= 2.0**-8 * np.abs(ex[~nan]) + slack)
+
+
+def test_oracle_swiglu_golden():
+    out = oracle.swiglu_fwd(G["swiglu_a"], G["swiglu_b"])
+    db, da = oracle.swiglu_bwd(G["swiglu_g"], G["swiglu_s"], G["swiglu_b"], G["swiglu_a"])
+    _check_swiglu(out, db, da)
+
+
 # ---------------------------------------------------------------- GPU: kernels
 @pytest.mark.gpu
 def test_kernels_rms_golden(gpu):
@@ -122,3 +152,14 @@ def test_kernels_rope_golden(gpu):
     tab = torch.from_numpy(G["rope_table"]).to(gpu)
     out, _ = kp.rope(x, positions=torch.from_numpy(G["rope_tpos"]).to(gpu), freqs_cis=tab, pairing="interleaved")
     _check_rope(out.cpu().view(torch.int16).numpy().view(np.uint16), G["rope_inter"])
+
+
+@pytest.mark.gpu
+def test_kernels_swiglu_golden(gpu):
+    import kernelproblems_amd as kp
+
+    a, b, g, s = (from_u16(G[f"swiglu_{k}"], gpu) for k in "abgs")
+    out = kp.swiglu(a, b)
+    db, da = kp.swiglu_backward(g, s, b, a)
+    u16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
+    _check_swiglu(u16(out), u16(db), u16(da), exact=False)

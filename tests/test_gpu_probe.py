@@ -7,7 +7,7 @@ from kernelproblems_amd import _lib as L
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("n_in,n_out,in_b,out_b", [(2, 1, 1 << 16, 1 << 16), (3, 2, 48, 48), (1, 1, 4096, 65536),
+@pytest.mark.parametrize("n_in,n_out,in_b,out_b", [(2, 1, 1 << 16, 1 << 16), (3, 2, 48, 48), (4, 2, 1 << 15, 1 << 15), (1, 1, 4096, 65536),
                                                    (0, 2, 0, 20000 * 16)])
 def test_stream_probe_outputs(gpu, n_in, n_out, in_b, out_b):
     g = torch.Generator().manual_seed(n_in * 10 + n_out)

@@ -23,6 +23,8 @@ TAB = (C64, (8192, 64), (64, 1))
 FC = (C64, (1, 8192, 1, 64), (524288, 64, 64, 1))
 FLAT_EMB = (BF, (525336576,), (1,))
 FLAT_LAYER = (BF, (218112000,), (1,))
+FFN = (BF, (8192, 14336), (14336, 1))
+FFN3 = (BF, (1, 8192, 14336), (117440512, 14336, 1))
 
 SIGNATURES = {
     "v7/59f786beb25f": [("embedding", X), ("_unsafe_view_432", W)],
@@ -52,6 +54,9 @@ SIGNATURES = {
     "v7/0f38bc55457c": [("mm", MM), ("mm_1", MM1), ("arg586_1", POS), ("arg582_1", TAB)],
     "v7/5c65f62b0422": [("getitem_642", (BF, (1, 8, 8192, 128), (8388608, 128, 1024, 1))), ("clone_62", FC)],
     "v7/bfe872e373e4": [("getitem_641", (BF, (1, 32, 8192, 128), (33554432, 128, 4096, 1))), ("clone_63", FC)],
+    "v8/c68dae22972b": [("mm_4", FFN), ("mm_5", FFN)],
+    "v8/385e1beb9bb9": [("mm_662", FFN), ("silu_recomputed", FFN3), ("_unsafe_view_5_recomputed", FFN3),
+                        ("_unsafe_view_4_recomputed", FFN3)],
 }
 
 
@@ -87,6 +92,10 @@ def test_tensor_api_refuses_cpu_tensors():
         kp.rope(torch.zeros(1, 2, 1, 8, dtype=BF), theta=1e4)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         kp.unshard(torch.zeros(16, dtype=BF), 2, (8,), (0,))
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        kp.swiglu(x, x)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        kp.swiglu_backward(x, x, x, x)
 
 
 def test_aten_drop_ins_refuse_cpu_tensors():
