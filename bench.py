@@ -16,6 +16,8 @@ BASELINE.json configurations:
   c5b  add + RMSNorm backward x, res, dy [16384, 8192]    -> dx bf16, dw fp32
   swf  SwiGLU gate forward    a, b [8192, 14336]          -> bf16(silu(a)) * b        (v8/c68dae22972b)
   swb  SwiGLU gate backward   g, s, b, a [8192, 14336]    -> db, da bf16              (v8/385e1beb9bb9)
+  cef  cross-entropy forward  logits [8192, 128256] bf16, targets -> loss, total_weight (v8/71f1d2c9f38b)
+  ceb  cross-entropy backward log-softmax [8192, 128256] fp32, targets -> bf16 grad   (v8/622c35f5d1c6)
 
 Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 ~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
@@ -361,6 +363,71 @@ class SwiGlu(Workload):
             torch_ref.swiglu_fwd(*self.ops)
 
 
+# ------------------------------------------------------------------ cross-entropy
+class CrossEntropy(Workload):
+    """Token cross-entropy at the reference's shape (8192 tokens, V = 128256,
+    targets uniform over the vocabulary, every 16th ignored).  Forward reads
+    the bf16 logits once; backward reads the fp32 log-softmax and writes the
+    bf16 logits gradient."""
+
+    def __init__(self, dev, M=8192, V=128256, backward=False, name="cef"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name, self.backward = name, backward
+        g = _gen(0)
+        self.targets = torch.randint(0, V, (M,), generator=g)
+        self.targets[::16] = -100
+        td = self.targets.to(dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        if backward:
+            x = torch.randn(M, V, generator=g) * 2
+            self.lsm = torch.log_softmax(x, 1)
+            del x
+            self.bytes_per_call = M * V * (4 + 2)
+            self.dominant_kernel = "xent_bwd_vec"
+            self.probe_mix = (1, 1, M * V * 4, M * V * 2,
+                              f"read {M * V * 4 / 1e9:.2f} GB + write {M * V * 2 / 1e9:.2f} GB")
+            self.description = (f"cross-entropy backward (v8/622c35f5d1c6): log-softmax [{M},{V}] fp32, targets "
+                                f"int64 -> grad bf16 [{M},{V}]")
+            fn = L.lib().kp_cross_entropy_bwd_bf16
+            src = self.lsm.to(dev)
+            for r in range(self.rotations(self.bytes_per_call)):
+                Ld = src if r == 0 else src.clone()
+                out = torch.empty((M, V), dtype=torch.bfloat16, device=dev)
+                args = (Ld.data_ptr(), V, td.data_ptr(), 8, -100, 1.0 / 8192.0, out.data_ptr(), V, M, V, None, stream)
+                self.sets.append((fn, args, (Ld, out)))
+        else:
+            self.logits = _randn((M, V), g, 0.0, 2.0)
+            self.bytes_per_call = M * V * 2 + M * 8
+            self.dominant_kernel = "xent_fwd_vec"
+            # read-only mix: the probe's one output array is a single 16-byte chunk
+            self.probe_mix = (1, 1, M * V * 2, 16, f"read of {M * V * 2 / 1e9:.2f} GB")
+            self.description = (f"cross-entropy forward (v8/71f1d2c9f38b): logits [{M},{V}] bf16, targets int64 "
+                                f"-> loss, total_weight fp32 (log-softmax not materialised)")
+            fn = L.lib().kp_cross_entropy_fwd_bf16
+            ws_bytes = int(L.lib().kp_cross_entropy_fwd_workspace_size(M))
+            src = self.logits.to(dev)
+            for r in range(self.rotations(self.bytes_per_call)):
+                xd = src if r == 0 else src.clone()
+                loss = torch.empty((), dtype=torch.float32, device=dev)
+                tw = torch.empty((), dtype=torch.float32, device=dev)
+                ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+                args = (xd.data_ptr(), V, M, V, td.data_ptr(), 8, -100, 1.0 / 8192.0, loss.data_ptr(), tw.data_ptr(),
+                        None, None, ws.data_ptr(), ws_bytes, stream)
+                self.sets.append((fn, args, (xd, loss, tw, ws)))
+        self.dominant_bytes = M * V * (6 if backward else 2)
+        self.keep = td
+        self.cpu_sample = f"full [{M},{V}] call"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        if self.backward:
+            torch_ref.cross_entropy_bwd(self.lsm, self.targets, 1.0 / 8192.0)
+        else:
+            torch_ref.cross_entropy_fwd(self.logits, self.targets, 1.0 / 8192.0)
+
+
 def make_workload(name, dev):
     if name == "c1":
         return RmsFwd(dev, 4096, 4096, 1e-6, "c1")
@@ -380,10 +447,14 @@ def make_workload(name, dev):
         return SwiGlu(dev, name="swf")
     if name == "swb":
         return SwiGlu(dev, backward=True, name="swb")
+    if name == "cef":
+        return CrossEntropy(dev, name="cef")
+    if name == "ceb":
+        return CrossEntropy(dev, backward=True, name="ceb")
     raise SystemExit(f"unknown workload {name!r}")
 
 
-ALL = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b", "swf", "swb"]
+ALL = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b", "swf", "swb", "cef", "ceb"]
 
 
 # ------------------------------------------------------------------ measure

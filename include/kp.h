@@ -57,8 +57,9 @@ const char* kp_last_error_message(void);
  * completion: the row kernel of the RMSNorm entry points, the gather kernel
  * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
  * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16, the
- * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16 and the kernel of
- * kp_stream_probe.
+ * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16, the row kernel of
+ * kp_cross_entropy_fwd_bf16, the kernel of kp_cross_entropy_bwd_bf16 and
+ * the kernel of kp_stream_probe.
  * Pass NULL, NULL to clear.  Per calling thread. */
 void kp_profile_dominant_kernel(void* start_event, void* stop_event);
 
@@ -259,6 +260,48 @@ int kp_swiglu_bwd_bf16(const void* g, int64_t g_stride, const void* s, int64_t s
                        const void* b, int64_t b_stride, const void* a, int64_t a_stride,
                        void* db, int64_t db_stride, void* da, int64_t da_stride,
                        int64_t M, int64_t N, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Cross-entropy forward over a vocabulary, sum reduction:
+ *   lse_i = log(sum_j exp(x_ij)),  x = fp32 of the bf16 logits
+ *   *loss = scale * sum over {i : targets[i] != ignore_index} of (lse_i - x_{i, targets[i]})
+ *   *total_weight = number of such rows (fp32)
+ *
+ * Replaces the _to_copy(f32) -> _log_softmax -> nll_loss_forward(weight None,
+ * reduction sum, ignore_index) -> div(8192) region at
+ * v8/71f1d2c9f38b/problem.py:15-40 (logits mm_224 bf16 [8192, 128256],
+ * targets i64 [8192]; scale = 1/8192), without materialising the fp32
+ * log-softmax.  logits: bf16 [M, V], unit inner stride, row stride
+ * row_stride.  targets: M integers of target_bytes (4 or 8).  loss,
+ * total_weight: one fp32 each (device).  row_lse: optional fp32 [M] (lse_i).
+ * A target outside [0, V) that is not ignore_index counts as ignored and,
+ * when error_flag != NULL, sets *error_flag = 1.  workspace: at least
+ * kp_cross_entropy_fwd_workspace_size(M) bytes, 8-byte aligned.  The sum over
+ * rows is taken in fp64 in a fixed order (bitwise reproducible).
+ */
+size_t kp_cross_entropy_fwd_workspace_size(int64_t M);
+int kp_cross_entropy_fwd_bf16(const void* logits, int64_t row_stride, int64_t M, int64_t V,
+                              const void* targets, int target_bytes, int64_t ignore_index, float scale,
+                              float* loss, float* total_weight, float* row_lse, int32_t* error_flag,
+                              void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Cross-entropy backward from the saved log-softmax, to bf16:
+ *   out_ij = bf16(grad_ij - exp(L_ij) * s_i),  grad_ij = -grad_loss if j == targets[i] else 0,
+ *   s_i = sum_j grad_ij (-grad_loss, or 0 for an ignored row)
+ * in fp32 (expf), as nll_loss_backward(reduction sum) then
+ * _log_softmax_backward_data then _to_copy(bf16) evaluate it.
+ *
+ * Replaces v8/622c35f5d1c6/problem.py:16-33 (L = _log_softmax fp32
+ * [8192, 128256], targets i64 [8192], grad_loss = ones_like(div) / 8192;
+ * the total_weight input is unused by the sum reduction).
+ * log_softmax: fp32 [M, V], row stride lsm_row_stride; grad_logits: bf16
+ * [M, V], row stride out_row_stride.  Targets and error_flag as in the
+ * forward (an out-of-range target's row gets s_i = 0).
+ */
+int kp_cross_entropy_bwd_bf16(const float* log_softmax, int64_t lsm_row_stride, const void* targets,
+                              int target_bytes, int64_t ignore_index, float grad_loss, void* grad_logits,
+                              int64_t out_row_stride, int64_t M, int64_t V, int32_t* error_flag, void* stream);
 
 #ifdef __cplusplus
 }

@@ -1,7 +1,8 @@
 """MI355X (gfx950) kernels for the memory-bound fused graph fragments of
 SherlockNoMad/KernelProblems: RMSNorm forward/backward (with residual-add and
 gradient epilogues), embedding gather and its dense deterministic backward,
-rotary position embedding on q/k, and the SwiGLU gate forward/backward.
+rotary position embedding on q/k, the SwiGLU gate forward/backward and the
+vocabulary cross-entropy loss forward/backward.
 
 Layers:
   * ``include/kp.h`` + ``csrc/*.hip``  -- the C ABI and the HIP kernels;
@@ -14,6 +15,8 @@ Layers:
 from . import aten, fused
 from ._lib import KPError, LIB_PATH, version
 from .fused import (
+    cross_entropy_backward,
+    cross_entropy_loss,
     embedding,
     embedding_dense_backward,
     index_checking,
@@ -30,6 +33,8 @@ __all__ = [
     "KPError",
     "LIB_PATH",
     "aten",
+    "cross_entropy_backward",
+    "cross_entropy_loss",
     "embedding",
     "embedding_dense_backward",
     "fused",

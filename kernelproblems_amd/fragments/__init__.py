@@ -24,6 +24,8 @@ FRAGMENTS = (
     "v7/5c65f62b0422", "v7/bfe872e373e4",
     # SwiGLU gate forward / backward
     "v8/c68dae22972b", "v8/385e1beb9bb9",
+    # token cross-entropy forward / backward
+    "v8/71f1d2c9f38b", "v8/622c35f5d1c6",
 )
 
 

@@ -479,3 +479,65 @@ def swiglu_backward(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.
         L.call("kp_swiglu_bwd_bf16", rg[0].data_ptr(), rg[1], rs[0].data_ptr(), rs[1], rb[0].data_ptr(), rb[1],
                ra[0].data_ptr(), ra[1], db.data_ptr(), n, da.data_ptr(), n, m, n, _stream(g.device))
     return db, da
+
+
+# ---------------------------------------------------------------- cross-entropy
+def _targets(targets: torch.Tensor, M: int, device: torch.device):
+    if not isinstance(targets, torch.Tensor) or targets.device != device:
+        raise RuntimeError("cross_entropy: targets must be a tensor on the logits' device")
+    if targets.dtype not in (torch.int64, torch.int32):
+        raise RuntimeError(f"cross_entropy: targets must be int64 or int32, got {targets.dtype}")
+    if targets.numel() != M:
+        raise RuntimeError(f"cross_entropy: {targets.numel()} targets for {M} rows")
+    t = targets.reshape(-1)
+    if M > 1 and t.stride(0) != 1:
+        t = t.contiguous()
+    return t, t.element_size()
+
+
+def cross_entropy_loss(logits: torch.Tensor, targets: torch.Tensor, *, ignore_index: int = -100, scale: float = 1.0,
+                       return_lse: bool = False):
+    """Summed token cross-entropy of bf16 logits [..., V] against integer
+    targets [...]: loss = scale * sum over rows with target != ignore_index of
+    (logsumexp(fp32 logits) - logit[target]), the fp32 _log_softmax ->
+    nll_loss_forward(reduction sum) -> div region of v8/71f1d2c9f38b/problem.py:15-40
+    without materialising the log-softmax.  Returns 0-dim fp32 tensors
+    (loss, total_weight) and, with return_lse, the fp32 per-row logsumexp."""
+    _need_gpu("cross_entropy logits", logits)
+    dev = logits.device
+    V = logits.shape[-1] if logits.dim() else 1
+    lt, rs, M = _as_rows(logits, V)
+    t, tb = _targets(targets, M, dev)
+    loss = torch.empty((), dtype=torch.float32, device=dev)
+    tw = torch.empty((), dtype=torch.float32, device=dev)
+    lse = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev) if return_lse else None
+    ws_bytes = int(L.lib().kp_cross_entropy_fwd_workspace_size(M))
+    ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
+    flag = _flag(dev)
+    L.call("kp_cross_entropy_fwd_bf16", lt.data_ptr(), rs, M, V, t.data_ptr(), tb, int(ignore_index), float(scale),
+           loss.data_ptr(), tw.data_ptr(), _ptr(lse), _ptr(flag), ws.data_ptr(), ws_bytes, _stream(dev))
+    _raise_if_flagged(flag, "cross_entropy")
+    return (loss, tw, lse) if return_lse else (loss, tw)
+
+
+def cross_entropy_backward(log_softmax: torch.Tensor, targets: torch.Tensor, grad_loss: float, *,
+                           ignore_index: int = -100) -> torch.Tensor:
+    """Gradient of the summed cross-entropy w.r.t. the logits, in bf16, from
+    the saved fp32 log-softmax L [..., V]: out = grad - exp(L) * sum(grad) with
+    grad = -grad_loss at each non-ignored row's target
+    (v8/622c35f5d1c6/problem.py:16-33: nll_loss_backward(sum) ->
+    _log_softmax_backward_data -> _to_copy(bf16)).  grad_loss is the
+    upstream gradient of the loss as a Python float (a constant in the
+    fragment: 1 / 8192).  Returns a contiguous bf16 tensor of L's shape."""
+    _need_gpu("cross_entropy log_softmax", log_softmax, torch.float32)
+    dev = log_softmax.device
+    V = log_softmax.shape[-1] if log_softmax.dim() else 1
+    lt, rs, M = _as_rows(log_softmax, V)
+    t, tb = _targets(targets, M, dev)
+    out = torch.empty(log_softmax.shape, dtype=torch.bfloat16, device=dev)
+    flag = _flag(dev)
+    if M:
+        L.call("kp_cross_entropy_bwd_bf16", lt.data_ptr(), rs, t.data_ptr(), tb, int(ignore_index), float(grad_loss),
+               out.data_ptr(), V, M, V, _ptr(flag), _stream(dev))
+    _raise_if_flagged(flag, "cross_entropy_backward")
+    return out

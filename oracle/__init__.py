@@ -37,6 +37,13 @@ swiglu_fwd             torch CPU eager ``silu`` * b, fp64 ``x * expit(x)``
 swiglu_bwd             torch CPU eager ``mul`` / ``silu_backward``, central
                        finite differences of fp64 silu, closed forms
                        (silu'(0) = 1/2, the zero of silu' near -1.2785).
+cross_entropy_fwd      torch fp64 ``log_softmax`` + ``nll_loss`` (sum,
+                       ignore_index), closed forms (uniform row: log V,
+                       dominant logit: 0), shift invariance, ignored rows.
+cross_entropy_bwd      torch fp64 ``nll_loss_backward`` +
+                       ``_log_softmax_backward_data`` (bit-exact after one
+                       rounding), the autograd of the forward, rows summing
+                       to zero for a true log-softmax, ignored rows zero.
 =====================  =====================================================
 
 bf16 tensors are handled as numpy ``uint16`` bit patterns.
@@ -70,6 +77,8 @@ _SIGS = {
     "kpo_rope": (i64, [vp, pi64, vp, pi64, i64, i64, i64, i64, vp, i64, i64, i32, f64, vp, i64, i64, i32]),
     "kpo_swiglu_fwd": (None, [vp, vp, vp, i64]),
     "kpo_swiglu_bwd": (None, [vp, vp, vp, vp, vp, vp, i64]),
+    "kpo_cross_entropy_fwd": (i64, [vp, i64, i64, vp, i64, f64, vp, vp, vp]),
+    "kpo_cross_entropy_bwd": (i64, [vp, i64, i64, vp, i64, f64, vp]),
 }
 
 
@@ -274,3 +283,29 @@ def swiglu_bwd(g: np.ndarray, s: np.ndarray, b: np.ndarray, a: np.ndarray):
     db, da = np.empty_like(arrs[0]), np.empty_like(arrs[0])
     lib().kpo_swiglu_bwd(*(_p(t) for t in arrs), _p(db), _p(da), arrs[0].size)
     return db, da
+
+
+# ---------------------------------------------------------------- cross-entropy
+def cross_entropy_fwd(logits: np.ndarray, targets: np.ndarray, ignore_index: int = -100, scale: float = 1.0):
+    """logits uint16 bf16 [M, V]; targets int [M].  Returns (loss, total_weight,
+    lse [M], n_out_of_range) in float64: loss = scale * sum over non-ignored
+    rows of (lse_i - x_{i, t_i})."""
+    x = _c(logits, np.uint16)
+    M, V = x.shape
+    t = _c(targets, np.int64).reshape(M)
+    loss, tw = C.c_double(), C.c_double()
+    lse = np.empty(M, dtype=np.float64)
+    bad = lib().kpo_cross_entropy_fwd(_p(x), M, V, _p(t), int(ignore_index), float(scale), C.byref(loss), C.byref(tw),
+                                      _p(lse))
+    return loss.value, tw.value, lse, int(bad)
+
+
+def cross_entropy_bwd(log_softmax: np.ndarray, targets: np.ndarray, grad_loss: float, ignore_index: int = -100):
+    """bf16 (uint16) [M, V] = grad - exp(L) * sum(grad) for the nll (sum) gradient
+    grad = -grad_loss at each row's target; returns (out, n_out_of_range)."""
+    L = _c(log_softmax, np.float32)
+    M, V = L.shape
+    t = _c(targets, np.int64).reshape(M)
+    out = np.empty((M, V), dtype=np.uint16)
+    bad = lib().kpo_cross_entropy_bwd(_p(L), M, V, _p(t), int(ignore_index), float(grad_loss), _p(out))
+    return out, int(bad)

@@ -192,6 +192,22 @@ def _swiglu_bwd(g, s, b, a):             # v8/385e1beb9bb9/problem.py:17-33
     return db, aten.view.default(da, list(g.shape))
 
 
+def _xent_fwd(t, logits):               # v8/71f1d2c9f38b/problem.py:15-40
+    tv = aten.view.default(t, [t.numel()])
+    x = aten.view.default(aten._unsafe_view.default(logits, [1, *logits.shape]), list(logits.shape))
+    lsm = aten._log_softmax.default(aten._to_copy.default(x, dtype=torch.float32), 1, False)
+    loss, tw = aten.nll_loss_forward.default(lsm, tv, None, 2, -100)
+    return aten.div.Tensor(loss, 8192.0), tw
+
+
+def _xent_bwd(div, lsm, t, tw):          # v8/622c35f5d1c6/problem.py:16-33
+    g = aten.div.Tensor(aten.ones_like.default(div, pin_memory=False, memory_format=torch.preserve_format), 8192.0)
+    gi = aten.nll_loss_backward.default(g, lsm, t, None, 2, -100, tw)
+    d = aten._log_softmax_backward_data.default(gi, lsm, 1, torch.float32)
+    out = aten._to_copy.default(d, dtype=torch.bfloat16, layout=torch.strided, device=lsm.device)
+    return aten.view.default(aten.view.default(out, [1, *out.shape]), list(out.shape))
+
+
 _FRAGMENTS = {
     "v7/59f786beb25f": _rms_fwd_y_rstd,
     "v8/4b90e2d83144": _rms_fwd_3views,
@@ -220,6 +236,8 @@ _FRAGMENTS = {
     "v7/bfe872e373e4": _rope_bwd,
     "v8/c68dae22972b": _swiglu_fwd,
     "v8/385e1beb9bb9": _swiglu_bwd,
+    "v8/71f1d2c9f38b": _xent_fwd,
+    "v8/622c35f5d1c6": _xent_bwd,
 }
 
 

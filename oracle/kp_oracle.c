@@ -370,3 +370,71 @@ void kpo_swiglu_bwd(const uint16_t* g, const uint16_t* s, const uint16_t* b, con
     da[i] = d2bf(silu_bwd_d(t, (double)bf2f(a[i])));
   }
 }
+
+/* ---------------------------------------------------------------- cross-entropy
+ * Forward (v8/71f1d2c9f38b/problem.py:15-40): _to_copy(f32) of the bf16
+ * logits, _log_softmax over the vocabulary, nll_loss_forward with weight
+ * None, reduction sum and ignore_index, div by a constant:
+ *   lse_i = m_i + log(sum_j exp(x_ij - m_i)),  m_i = max_j x_ij
+ *   loss  = scale * sum_{i: t_i != ignore} (lse_i - x_{i, t_i}),  total_weight = #{i: t_i != ignore}
+ * (log_softmax(x)_ij = x_ij - lse_i, torch/_decomp/decompositions.py:1198-1221
+ * (_log_softmax); nll picks -lsm[i, t_i] and counts the non-ignored rows,
+ * :4099-4150 (_nll_loss_forward)), all in double.  Targets outside [0, V)
+ * other than ignore_index are counted in the return value and treated as
+ * ignored.
+ * Backward (v8/622c35f5d1c6/problem.py:16-33): nll_loss_backward puts -g at
+ * (i, t_i) of valid rows (decompositions.py:485-514, _nll_loss_backward);
+ * _log_softmax_backward_data gives
+ *   out_ij = grad_ij - exp(L_ij) * sum_j grad_ij
+ * (decompositions.py:879-889), rounded once to bf16 from double. */
+int64_t kpo_cross_entropy_fwd(const uint16_t* logits, int64_t M, int64_t V, const int64_t* targets, int64_t ignore,
+                              double scale, double* loss, double* total_weight, double* lse_out) {
+  double acc = 0.0, cnt = 0.0;
+  int64_t bad = 0;
+  for (int64_t i = 0; i < M; ++i) {
+    const uint16_t* x = logits + i * V;
+    double m = -INFINITY;
+    for (int64_t j = 0; j < V; ++j) {
+      const double v = (double)bf2f(x[j]);
+      if (v > m || isnan(v)) m = v;
+    }
+    double lse;
+    if (isinf(m) || isnan(m)) {
+      lse = m; /* all -inf: -inf; any +inf or NaN: propagates */
+      if (m > 0) lse = NAN;
+    } else {
+      double s = 0.0;
+      for (int64_t j = 0; j < V; ++j) s += exp((double)bf2f(x[j]) - m);
+      lse = m + log(s);
+    }
+    if (lse_out) lse_out[i] = lse;
+    const int64_t t = targets[i];
+    if (t == ignore) continue;
+    if (t < 0 || t >= V) {
+      ++bad;
+      continue;
+    }
+    acc += lse - (double)bf2f(x[t]);
+    cnt += 1.0;
+  }
+  *loss = acc * scale;
+  *total_weight = cnt;
+  return bad;
+}
+
+int64_t kpo_cross_entropy_bwd(const float* lsm, int64_t M, int64_t V, const int64_t* targets, int64_t ignore, double g,
+                              uint16_t* out) {
+  int64_t bad = 0;
+  for (int64_t i = 0; i < M; ++i) {
+    const int64_t t = targets[i];
+    const int in_range = t >= 0 && t < V;
+    if (t != ignore && !in_range) ++bad;
+    const int valid = t != ignore && in_range;
+    const double sum = valid ? -g : 0.0;
+    for (int64_t j = 0; j < V; ++j) {
+      const double grad = (valid && j == t) ? -g : 0.0;
+      out[i * V + j] = d2bf(grad - exp((double)lsm[i * V + j]) * sum);
+    }
+  }
+  return bad;
+}

@@ -105,3 +105,21 @@ def swiglu_fwd(a: torch.Tensor, b: torch.Tensor):
 def swiglu_bwd(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.Tensor):
     """v8/385e1beb9bb9/problem.py:17-33: mul.Tensor(g, s); silu_backward(mul.Tensor(g, b), a)."""
     return aten.mul.Tensor(g, s), aten.silu_backward.default(aten.mul.Tensor(g, b), a)
+
+
+def cross_entropy_fwd(logits: torch.Tensor, targets: torch.Tensor, scale: float):
+    """v8/71f1d2c9f38b/problem.py:15-40: _to_copy(f32) -> _log_softmax ->
+    nll_loss_forward(sum, ignore_index=-100) -> div."""
+    lsm = aten._log_softmax.default(aten._to_copy.default(logits, dtype=torch.float32), 1, False)
+    loss, tw = aten.nll_loss_forward.default(lsm, targets, None, 2, -100)
+    return aten.mul.Tensor(loss, scale), tw
+
+
+def cross_entropy_bwd(lsm: torch.Tensor, targets: torch.Tensor, grad_loss: float):
+    """v8/622c35f5d1c6/problem.py:16-33: nll_loss_backward(sum) ->
+    _log_softmax_backward_data -> _to_copy(bf16)."""
+    g = torch.tensor(grad_loss, dtype=torch.float32, device=lsm.device)
+    tw = (targets != -100).sum().to(torch.float32)
+    gi = aten.nll_loss_backward.default(g, lsm, targets, None, 2, -100, tw)
+    d = aten._log_softmax_backward_data.default(gi, lsm, 1, torch.float32)
+    return aten._to_copy.default(d, dtype=torch.bfloat16)

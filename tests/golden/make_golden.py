@@ -2,7 +2,8 @@
 outputs, computed here with torch library ops in float64 (F.rms_norm and
 its autograd, torch's decomposition of _fused_rms_norm_backward, index_add_,
 torch.polar / complex multiply with torchtitan's frequency formula, silu and
-the autograd of x * sigmoid(x)) and one correctly rounded bf16 conversion
+the autograd of x * sigmoid(x), log_softmax / nll_loss and their backward
+ops) and one correctly rounded bf16 conversion
 per rounding point of the reference op sequence.  None of it calls the oracle or the HIP
 kernels, which tests/test_golden.py checks against these vectors.
 
@@ -114,12 +115,33 @@ def swiglu_cases(d):
              swiglu_da_exact=x.grad.numpy())
 
 
+def loss_cases(d):
+    """v8/71f1d2c9f38b (log_softmax -> nll_loss sum -> / 8192) and
+    v8/622c35f5d1c6 (nll_loss_backward -> _log_softmax_backward_data ->
+    bf16) on [6, 333] with an ignored row, through torch's fp64 ops."""
+    g = _g(500)
+    M, V, scale = 6, 333, 1.0 / 8192
+    x = _bf((M, V), g, std=3.0)
+    t = torch.randint(0, V, (M,), generator=g)
+    t[4] = -100
+    lsm64 = torch.log_softmax(x.double(), 1)
+    loss = torch.nn.functional.nll_loss(lsm64, t, reduction="sum", ignore_index=-100) * scale
+    L = torch.log_softmax(x.float(), 1)                        # the saved fp32 log-softmax
+    gi = torch.ops.aten.nll_loss_backward(torch.tensor(scale, dtype=torch.float64), L.double(), t, None, 2, -100,
+                                          torch.tensor(float((t != -100).sum()), dtype=torch.float64))
+    grad = torch.ops.aten._log_softmax_backward_data(gi, L.double(), 1, torch.float64)
+    d.update(xent_x=to_u16(x), xent_t=t.numpy(), xent_scale=np.float64(scale), xent_loss=np.float64(loss.item()),
+             xent_tw=np.float64((t != -100).sum().item()), xent_lse=torch.logsumexp(x.double(), 1).numpy(),
+             xent_L=L.numpy(), xent_grad=bf16_round_exact(grad.numpy()).reshape(M, V))
+
+
 def main():
     d = {}
     rms_cases(d)
     embedding_cases(d)
     rope_cases(d)
     swiglu_cases(d)
+    loss_cases(d)
     np.savez_compressed(OUT, **d)
     print(f"wrote {OUT} ({OUT.stat().st_size} bytes, {len(d)} arrays)")
 

@@ -107,6 +107,8 @@ def test_empty_work_is_ok_without_device(lib):
     assert lib.kp_unshard_bf16(None, 8, 64, None, None, None, 0, None) == L.KP_OK
     assert lib.kp_swiglu_fwd_bf16(None, 8, None, 8, None, 8, 0, 8, None) == L.KP_OK
     assert lib.kp_swiglu_bwd_bf16(None, 8, None, 8, None, 8, None, 8, None, 8, None, 8, 4, 0, None) == L.KP_OK
+    assert lib.kp_cross_entropy_bwd_bf16(None, 8, None, 8, -100, 1.0, None, 8, 0, 8, None, None) == L.KP_OK
+    assert lib.kp_cross_entropy_fwd_workspace_size(0) == 0
 
 
 def test_swiglu_validation(lib):
@@ -115,6 +117,21 @@ def test_swiglu_validation(lib):
     _expect(lib, L.KP_EINVAL, "kp_swiglu_fwd_bf16", 16, 8, 32, 4, 48, 8, 2, 8, None)  # b rows overlap
     _expect(lib, L.KP_EINVAL, "kp_swiglu_bwd_bf16", 16, 8, 32, 8, 48, 8, 64, 8, 80, 8, None, 8, 2, 8, None)  # NULL da
     _expect(lib, L.KP_EINVAL, "kp_swiglu_bwd_bf16", 16, 8, 32, 8, 48, 8, 64, 7, 80, 8, 96, 8, 2, 8, None)
+
+
+def test_cross_entropy_validation(lib):
+    ws = int(lib.kp_cross_entropy_fwd_workspace_size(4))
+    assert ws >= 4 * 12
+    fwd = "kp_cross_entropy_fwd_bf16"
+    _expect(lib, L.KP_EINVAL, fwd, 16, 8, 4, 8, 32, 2, -100, 1.0, 48, 64, None, None, 128, ws, None)  # 2-byte ids
+    _expect(lib, L.KP_EINVAL, fwd, 16, 8, 4, 8, 32, 8, -100, 1.0, None, 64, None, None, 128, ws, None)  # no loss
+    _expect(lib, L.KP_EWORKSPACE, fwd, 16, 8, 4, 8, 32, 8, -100, 1.0, 48, 64, None, None, 128, ws - 1, None)
+    _expect(lib, L.KP_EINVAL, fwd, 16, 4, 4, 8, 32, 8, -100, 1.0, 48, 64, None, None, 128, ws, None)  # stride < V
+    _expect(lib, L.KP_EINVAL, fwd, 16, 8, 4, 8, 32, 8, -100, 1.0, 48, 64, None, None, 132, ws, None)  # misaligned ws
+    bwd = "kp_cross_entropy_bwd_bf16"
+    _expect(lib, L.KP_EINVAL, bwd, 16, 8, 32, 8, -100, 1.0, None, 8, 4, 8, None, None)  # no output
+    _expect(lib, L.KP_EINVAL, bwd, 16, 8, 32, 3, -100, 1.0, 64, 8, 4, 8, None, None)    # 3-byte ids
+    _expect(lib, L.KP_EINVAL, bwd, 16, 8, 32, 8, -100, 1.0, 64, 8, 4, 0, None, None)    # V = 0
 
 
 def test_stream_probe_validation(lib):

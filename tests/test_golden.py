@@ -106,6 +106,15 @@ def test_oracle_swiglu_golden():
     _check_swiglu(out, db, da)
 
 
+def test_oracle_loss_golden():
+    loss, tw, lse, bad = oracle.cross_entropy_fwd(G["xent_x"], G["xent_t"], scale=float(G["xent_scale"]))
+    assert bad == 0 and tw == float(G["xent_tw"])
+    assert loss == pytest.approx(float(G["xent_loss"]), rel=1e-13)
+    np.testing.assert_allclose(lse, G["xent_lse"], rtol=1e-13)
+    out, _ = oracle.cross_entropy_bwd(G["xent_L"], G["xent_t"], float(G["xent_scale"]))
+    assert np.array_equal(out, G["xent_grad"])
+
+
 # ---------------------------------------------------------------- GPU: kernels
 @pytest.mark.gpu
 def test_kernels_rms_golden(gpu):
@@ -163,3 +172,19 @@ def test_kernels_swiglu_golden(gpu):
     db, da = kp.swiglu_backward(g, s, b, a)
     u16 = lambda t: t.cpu().view(torch.int16).numpy().view(np.uint16)
     _check_swiglu(u16(out), u16(db), u16(da), exact=False)
+
+
+@pytest.mark.gpu
+def test_kernels_loss_golden(gpu):
+    import kernelproblems_amd as kp
+
+    x = from_u16(G["xent_x"], gpu)
+    t = torch.from_numpy(G["xent_t"]).to(gpu)
+    loss, tw, lse = kp.cross_entropy_loss(x, t, scale=float(G["xent_scale"]), return_lse=True)
+    assert float(tw) == float(G["xent_tw"])
+    # fp32 exponentials and sums over 333 terms: well inside 1e-6 relative
+    assert float(loss) == pytest.approx(float(G["xent_loss"]), rel=1e-6)
+    np.testing.assert_allclose(lse.cpu().double().numpy(), G["xent_lse"], rtol=1e-6)
+    out = kp.cross_entropy_backward(torch.from_numpy(G["xent_L"]).to(gpu), t, float(G["xent_scale"]))
+    u = ulp_bf16(out.cpu().view(torch.int16).numpy().view(np.uint16), G["xent_grad"])
+    assert u.max() <= 1 and (u == 0).mean() > 0.99

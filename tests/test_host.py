@@ -57,6 +57,9 @@ SIGNATURES = {
     "v8/c68dae22972b": [("mm_4", FFN), ("mm_5", FFN)],
     "v8/385e1beb9bb9": [("mm_662", FFN), ("silu_recomputed", FFN3), ("_unsafe_view_5_recomputed", FFN3),
                         ("_unsafe_view_4_recomputed", FFN3)],
+    "v8/71f1d2c9f38b": [("arg584_1", IDS), ("mm_224", (BF, (8192, 128256), (128256, 1)))],
+    "v8/622c35f5d1c6": [("div", (F32, (), ())), ("_log_softmax", (F32, (8192, 128256), (128256, 1))),
+                        ("view_805", (I64, (8192,), (1,))), ("getitem_419", (F32, (), ()))],
 }
 
 
@@ -96,6 +99,10 @@ def test_tensor_api_refuses_cpu_tensors():
         kp.swiglu(x, x)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         kp.swiglu_backward(x, x, x, x)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        kp.cross_entropy_loss(x, torch.zeros(4, dtype=I64))
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        kp.cross_entropy_backward(x.float(), torch.zeros(4, dtype=I64), 1.0)
 
 
 def test_aten_drop_ins_refuse_cpu_tensors():

@@ -78,3 +78,29 @@ def test_rope_half_and_complex():
     e = oracle.rope(to_u16(q[:1]), None, pairing="interleaved", freqs=freqs.numpy())
     u = ulp_bf16(to_u16(xo), e)
     assert not ((u > 1) & (np.abs(bf(to_u16(xo)) - bf(e)) > 4e-6)).any()
+
+
+def test_swiglu_fwd_and_bwd():
+    g = gen(9)
+    a, b, gr, s = (randn_bf16((16, 700), g, std=3.0) for _ in range(4))
+    _close_ulp(to_u16(torch_ref.swiglu_fwd(a, b)), oracle.swiglu_fwd(to_u16(a), to_u16(b)), min_exact=0.99)
+    db, da = torch_ref.swiglu_bwd(gr, s, b, a)
+    edb, eda = oracle.swiglu_bwd(to_u16(gr), to_u16(s), to_u16(b), to_u16(a))
+    assert np.array_equal(to_u16(db), edb)
+    u = ulp_bf16(to_u16(da), eda)
+    assert (u == 0).mean() > 0.99
+
+
+def test_cross_entropy_fwd_and_bwd():
+    g = gen(10)
+    M, V = 12, 5000
+    x = randn_bf16((M, V), g, std=2.0)
+    t = torch.randint(0, V, (M,), generator=g)
+    t[3] = -100
+    loss, tw = torch_ref.cross_entropy_fwd(x, t, 1 / 8192)
+    lo, two, _, _ = oracle.cross_entropy_fwd(to_u16(x), t.numpy(), scale=1 / 8192)
+    assert float(tw) == two and abs(float(loss) - lo) <= 1e-5 * abs(lo)
+    L = torch.log_softmax(x.float(), 1)
+    out = torch_ref.cross_entropy_bwd(L, t, 1 / 8192)
+    eo, _ = oracle.cross_entropy_bwd(L.numpy(), t.numpy(), 1 / 8192)
+    _close_ulp(to_u16(out), eo, min_exact=0.99)
