@@ -31,8 +31,9 @@ kernel's own start and completion (kp_profile_dominant_kernel ->
 hipExtLaunchKernel), on the stream the kernel runs on.  roofline.ceiling is
 the same measurement for kp_stream_probe -- plain one-shot streaming of the
 workload's byte mix (same number and sizes of arrays read and written,
-16-byte non-temporal accesses) -- so kernel_frac_of_ceiling says how close
-the kernel comes to what this GPU streams for those bytes.  The
+16-byte non-temporal accesses, 1 or 4 chunks per thread, the faster of the
+two) -- so kernel_frac_of_ceiling says how close the kernel comes to what
+this GPU streams for those bytes.  The
 cpu_baseline is the torch CPU eager restatement of the
 fragment (oracle/torch_ref.py) on the same seeded inputs.
 """
@@ -386,8 +387,10 @@ class CrossEntropy(Workload):
             del x
             self.bytes_per_call = M * V * (4 + 2)
             self.dominant_kernel = "xent_bwd_vec"
-            self.probe_mix = (1, 1, M * V * 4, M * V * 2,
-                              f"read {M * V * 4 / 1e9:.2f} GB + write {M * V * 2 / 1e9:.2f} GB")
+            # 4 bytes read per 2 written, interleaved through the whole stream:
+            # two read arrays and one write array of equal size
+            self.probe_mix = (2, 1, M * V * 2, M * V * 2,
+                              f"2 reads + 1 write of {M * V * 2 / 1e9:.2f} GB (4.20 GB read, 2.10 GB written)")
             self.description = (f"cross-entropy backward (v8/622c35f5d1c6): log-softmax [{M},{V}] fp32, targets "
                                 f"int64 -> grad bf16 [{M},{V}]")
             fn = L.lib().kp_cross_entropy_bwd_bf16
@@ -508,7 +511,8 @@ def measure_gpu(wl, steps, warmup):
 def measure_probe(wl, steps, warmup):
     """The streaming ceiling of the workload's byte mix: kp_stream_probe over
     fresh arrays of the same sizes (rotated past the Infinity Cache like the
-    workload's own), timed per launch like the dominant kernel."""
+    workload's own), timed per launch like the dominant kernel, at 1 and at 4
+    chunks per thread; the faster tile size is the ceiling."""
     import torch
     from kernelproblems_amd import _lib as L
     if wl.probe_mix is None:
@@ -526,28 +530,33 @@ def measure_probe(wl, steps, warmup):
             t.fill_(1)
         sets.append((L.ptr_array([t.data_ptr() for t in ins]), L.ptr_array([t.data_ptr() for t in outs]), ins, outs))
 
-    def launch(i):
+    def launch(i, per_thread):
         ip, op, _, _ = sets[i % R]
-        st = lib.kp_stream_probe(ip, n_in, in_b, op, n_out, out_b, stream)
+        st = lib.kp_stream_probe(ip, n_in, in_b, op, n_out, out_b, per_thread, stream)
         if st != 0:
             raise L.KPError("kp_stream_probe", st, lib.kp_last_error_message().decode())
 
-    for i in range(warmup):
-        launch(i)
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-    for e in starts + stops:
-        e.record()
-    torch.cuda.synchronize()
-    for i in range(steps):
-        lib.kp_profile_dominant_kernel(starts[i].cuda_event, stops[i].cuda_event)
-        launch(warmup + i)
-    lib.kp_profile_dominant_kernel(None, None)
-    torch.cuda.synchronize()
-    ms = sum(starts[i].elapsed_time(stops[i]) for i in range(steps)) / steps
+    per_tile = {}
+    for per_thread in (1, 4):
+        for i in range(warmup):
+            launch(i, per_thread)
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        for e in starts + stops:
+            e.record()
+        torch.cuda.synchronize()
+        for i in range(steps):
+            lib.kp_profile_dominant_kernel(starts[i].cuda_event, stops[i].cuda_event)
+            launch(warmup + i, per_thread)
+        lib.kp_profile_dominant_kernel(None, None)
+        torch.cuda.synchronize()
+        per_tile[per_thread] = sum(starts[i].elapsed_time(stops[i]) for i in range(steps)) / steps
     del sets
     torch.cuda.empty_cache()
-    return {"GBps": per_set / (ms * 1e-3) / 1e9, "us": ms * 1e3, "mix": text, "bytes": per_set}
+    best = min(per_tile, key=per_tile.get)
+    ms = per_tile[best]
+    return {"GBps": per_set / (ms * 1e-3) / 1e9, "us": ms * 1e3, "mix": text, "bytes": per_set,
+            "chunks_per_thread": best, "us_by_tile": {str(k): round(v * 1e3, 3) for k, v in per_tile.items()}}
 
 
 def measure_cpu(wl, seconds):
@@ -579,7 +588,8 @@ def _ceiling_json(r):
     if not c:
         return None
     return {"GBps": round(c["GBps"], 1), "frac_of_peak": round(c["GBps"] / PEAK_GBS, 4), "probe_us": round(c["us"], 3),
-            "mix": c["mix"], "kernel_frac_of_ceiling": round(r["achieved"] / c["GBps"], 4)}
+            "probe_us_by_chunks_per_thread": c["us_by_tile"], "mix": c["mix"],
+            "kernel_frac_of_ceiling": round(r["achieved"] / c["GBps"], 4)}
 
 
 def load_traffic(name):
@@ -627,7 +637,7 @@ def main():
         r["ceiling"] = None if args.no_probe else measure_probe(wl, args.steps, args.warmup)
         if r["ceiling"]:
             c = r["ceiling"]
-            print(f"[bench] {name}: streaming ceiling of its mix ({c['mix']}): {c['us']:.1f} us -> {c['GBps']:.0f} GB/s; "
+            print(f"[bench] {name}: streaming ceiling of its mix ({c['mix']}): {c['us']:.1f} us at {c['chunks_per_thread']} chunk(s)/thread -> {c['GBps']:.0f} GB/s; "
                   f"dominant kernel at {r['achieved'] / c['GBps']:.1%} of it", file=sys.stderr, flush=True)
         cpu = None
         if with_cpu:

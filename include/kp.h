@@ -128,12 +128,13 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
  * reference).  Reads n_in (0..4) arrays of in_bytes each and writes n_out
  * (1..2) arrays of out_bytes each (sizes multiples of 16, arrays 16-byte
  * aligned) with the fragment kernels' access form: 16-byte non-temporal
- * loads and stores, 1 KiB per wave instruction, one-shot grid.  bench.py
- * times it on each workload's byte mix to report the bandwidth plain
- * streaming of those bytes reaches on this GPU.
+ * loads and stores, 1 KiB per wave instruction, one-shot grid of 256-thread
+ * blocks holding chunks_per_thread (1 or 4) chunks per thread per array.
+ * bench.py times it on each workload's byte mix, at both tile sizes, to
+ * report the bandwidth plain streaming of those bytes reaches on this GPU.
  */
 int kp_stream_probe(const void* const* in, int n_in, int64_t in_bytes, void* const* out, int n_out,
-                    int64_t out_bytes, void* stream);
+                    int64_t out_bytes, int chunks_per_thread, void* stream);
 
 /* ------------------------------------------------------------------------
  * Embedding forward: out[t, :] = table[indices[t], :] (bit copy).

@@ -253,36 +253,45 @@ __device__ __forceinline__ float xent_grad(float l, bool is_target, float g, flo
   return grad - expf(l) * sum;
 }
 
-constexpr int kBwdPer = 4;                                    // 8-element chunks per thread
-constexpr int64_t kBwdBlockChunks = (int64_t)kThreads * kBwdPer;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
-// Rows of V = 8k elements, lsm and out rows 16-byte aligned: block b covers row b / bpr, 8-element chunks [(b % bpr) * 1024, +1024);
-// thread t holds chunks t + 256 u (two 16-byte loads, one 16-byte store each).
+// Rows of V = 4k elements, lsm rows 16-byte and out rows 8-byte aligned.  A
+// block covers 2048 consecutive elements of one row (block b: row b / bpr,
+// float4 groups [(b % bpr) * 512, +512)); wave w takes groups
+// [w * 128, +128) as two 1 KiB load instructions (lane l: groups l and
+// 64 + l) and writes each group's 4 bf16 as one 8-byte store.  Measured on
+// MI355X for this 4-byte-read / 2-byte-write stream: one group per lane per
+// instruction beats 2-4 (1086-1144 us at [8192, 128256] against 996 us), and
+// lanes holding 8 consecutive elements (two loads 32 bytes apart, one
+// 16-byte store) ran at 1144 us.
+constexpr int64_t kBwdBlockGroups = (int64_t)kThreads * 2;  // float4 groups per block
+
 __global__ __launch_bounds__(kThreads) void xent_bwd_vec(BwdArgs a) {
   const int64_t row = (int64_t)((int)blockIdx.x / a.bpr);
-  const int64_t c0 = (int64_t)((int)blockIdx.x - (int)row * a.bpr) * kBwdBlockChunks;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
+  const int64_t g0 = (int64_t)((int)blockIdx.x - (int)row * a.bpr) * kBwdBlockGroups + (int64_t)wave * 128;
   float sum;
-  const int64_t t = row_target(a, row, c0 == 0 && threadIdx.x == 0, sum);
-  const int64_t cpr = a.V / 8;
+  const int64_t t = row_target(a, row, g0 == 0 && lane == 0, sum);
+  const int64_t gpr = a.V / 4;
   const f32x4* p = reinterpret_cast<const f32x4*>(a.lsm + row * a.rs);
-  u32x4* q = reinterpret_cast<u32x4*>(a.out + row * a.ors);
-  f32x4 v[kBwdPer][2];
-  int64_t c[kBwdPer];
-  bool ok[kBwdPer];
+  u32x2* q = reinterpret_cast<u32x2*>(a.out + row * a.ors);
+  f32x4 v[2];
+  int64_t gi[2];
+  bool ok[2];
 #pragma unroll
-  for (int u = 0; u < kBwdPer; ++u) {
-    c[u] = c0 + threadIdx.x + (int64_t)u * kThreads;
-    ok[u] = c[u] < cpr;
-    const int64_t cc = ok[u] ? c[u] : 0;
-    v[u][0] = __builtin_nontemporal_load(p + 2 * cc);
-    v[u][1] = __builtin_nontemporal_load(p + 2 * cc + 1);
+  for (int h = 0; h < 2; ++h) {
+    gi[h] = g0 + h * kWave + lane;
+    ok[h] = gi[h] < gpr;
+    v[h] = __builtin_nontemporal_load(p + (ok[h] ? gi[h] : 0));
   }
 #pragma unroll
-  for (int u = 0; u < kBwdPer; ++u) {
-    float o[8];
+  for (int h = 0; h < 2; ++h) {
+    const bool has = (t >> 2) == gi[h];  // t = -1 for rows without a target column
+    float o[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) o[i] = xent_grad(v[u][i >> 2][i & 3], c[u] * 8 + i == t, a.g, sum);
-    if (ok[u]) st16_stream(q + c[u], pack8(o));
+    for (int i = 0; i < 4; ++i) o[i] = xent_grad(v[h][i], has && (t & 3) == i, a.g, sum);
+    const u32x2 r = {pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3])};
+    if (ok[h]) __builtin_nontemporal_store(r, q + gi[h]);
   }
 }
 
@@ -375,11 +384,11 @@ int kp_cross_entropy_bwd_bf16(const float* log_softmax, int64_t lsm_row_stride, 
   a.ignore = ignore_index;
   a.g = grad_loss;
   a.err = error_flag;
-  const bool vec = V % 8 == 0 && aligned16(log_softmax) && aligned16(grad_logits) &&
-                   (M == 1 || (lsm_row_stride % 8 == 0 && out_row_stride % 8 == 0));
+  const bool vec = V % 4 == 0 && aligned16(log_softmax) && (reinterpret_cast<uintptr_t>(grad_logits) & 7) == 0 &&
+                   (M == 1 || (lsm_row_stride % 4 == 0 && out_row_stride % 4 == 0));
   void* args[] = {&a};
   if (vec) {
-    const int64_t bpr = ceil_div(V / 8, kBwdBlockChunks);
+    const int64_t bpr = ceil_div(V / 4, kBwdBlockGroups);
     if (bpr * M > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: too many blocks", who);
     a.bpr = (int)bpr;
     launch_dominant_raw(reinterpret_cast<const void*>(xent_bwd_vec), dim3((unsigned)(bpr * M)), dim3(kThreads), args,

@@ -135,8 +135,9 @@ def test_cross_entropy_validation(lib):
 
 
 def test_stream_probe_validation(lib):
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 5, 64, L.ptr_array([32]), 1, 64, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 60, L.ptr_array([32]), 1, 64, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, None)
-    assert lib.kp_stream_probe(None, 0, 0, L.ptr_array([32]), 1, 0, None) == L.KP_OK  # nothing to stream
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 5, 64, L.ptr_array([32]), 1, 64, 4, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, 4, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 60, L.ptr_array([32]), 1, 64, 4, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, 4, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 1, 64, 2, None)
+    assert lib.kp_stream_probe(None, 0, 0, L.ptr_array([32]), 1, 0, 1, None) == L.KP_OK  # nothing to stream

@@ -108,7 +108,7 @@ def test_fwd_deterministic_and_empty(gpu):
     assert float(loss) == 0.0 and float(tw) == 0.0
 
 
-BWD_CASES = [("contig", 1, 8), ("contig", 5, 1000), ("contig", 9, 128256), ("contig", 7, 1003),
+BWD_CASES = [("contig", 1, 8), ("contig", 5, 1000), ("contig", 9, 128256), ("contig", 7, 1003), ("contig", 3, 1004),
              ("rows", 6, 4096), ("unaligned", 4, 2000)]
 
 
