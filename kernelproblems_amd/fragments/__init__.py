@@ -26,6 +26,8 @@ FRAGMENTS = (
     "v8/c68dae22972b", "v8/385e1beb9bb9",
     # token cross-entropy forward / backward
     "v8/71f1d2c9f38b", "v8/622c35f5d1c6",
+    # chain: RMSNorm forward -> backward (+ gradient adds, residual) -> embedding backward
+    "v6/0b493aad68f0", "v5/118d525f44e0",
 )
 
 

@@ -1,0 +1,41 @@
+"""First-layer attention RMSNorm forward, its backward with a three-term
+gradient and residual epilogue, and the token-embedding backward of the
+result: v6/0b493aad68f0/problem.py:10-56 (inputs :59-67).
+
+Three launches of the fused kernels: the norm forward (y, returned as three
+views, and the rstd the backward uses); the backward with
+dy = bf16(bf16(mm_670 + mm_672) + mm_674), g = bf16(add_220 + dx) and the
+fp32-widened bf16 weight gradient; the dense embedding backward of g
+(fp32 accumulation, rounded once to bf16 like the eager bf16 table, stored
+fp32).  g is the one intermediate that reaches HBM: the embedding backward
+reads its rows in sorted-id order, not in the token order they are made in."""
+from .. import fused as F
+from ._common import EPS, randint, randn, rows2d
+
+NUM_WEIGHTS = 128256
+
+
+def get_inputs(device="cuda", generator=None):
+    return [randn([1, 8192, 4096], device=device, generator=generator),
+            randn([4096], device=device, generator=generator),
+            randn([8192, 4096], device=device, generator=generator),
+            randn([8192, 4096], device=device, generator=generator),
+            randn([8192, 4096], device=device, generator=generator),
+            randn([1, 8192, 4096], device=device, generator=generator),
+            randint(100, [1, 8192], device=device, generator=generator)]
+
+
+def chain(x, w, dy_terms, residual, ids):
+    """(y as three views, fp32 dw, fp32 table gradient) of the chain."""
+    import torch
+
+    n = x.shape[-1]
+    _, y, rstd = F.rms_norm([x], w, EPS, n)
+    g, dw = F.rms_norm_backward(dy_terms, [x], rstd, w, EPS, n, dx_residual=residual, dw="f32_bf16")
+    table = F.embedding_dense_backward(g, ids, NUM_WEIGHTS, -1, False, out_dtype=torch.float32, round_to_bf16=True)
+    v = rows2d(y)
+    return v, v.view(v.shape), v.view(v.shape), dw.view(-1), table  # dw: f32[N] whatever the weight view
+
+
+def kernel_function(embedding, _unsafe_view_432, mm_670, mm_672, mm_674, add_220, arg583_1):
+    return chain(embedding, _unsafe_view_432, [mm_670, mm_672, mm_674], add_220, arg583_1)

@@ -208,6 +208,21 @@ def _xent_bwd(div, lsm, t, tw):          # v8/622c35f5d1c6/problem.py:16-33
     return aten.view.default(aten.view.default(out, [1, *out.shape]), list(out.shape))
 
 
+def _norm_emb_bwd_chain(x, w, mm_a, mm_b, mm_c, res, ids):  # v6/0b493aad68f0/problem.py:16-56
+    y, r = _norm(x, w)
+    dy = aten.add.Tensor(aten.add.Tensor(aten.view.default(mm_a, list(x.shape)), aten.view.default(mm_b, list(x.shape))),
+                         aten.view.default(mm_c, list(x.shape)))
+    dx, dw = _norm_bwd(dy, x, r, w)
+    g = aten.add.Tensor(res, dx)
+    table = aten.embedding_dense_backward.default(g, ids, 128256, -1, False)
+    return (*_views(y, 3), aten._to_copy.default(dw, dtype=torch.float32),
+            aten._to_copy.default(table, dtype=torch.float32))
+
+
+def _norm_emb_bwd_chain_fsdp(wv, x, mm_a, mm_b, mm_c, res, ids):  # v5/118d525f44e0/problem.py:16-59
+    return _norm_emb_bwd_chain(x, _clone_weight(wv), mm_a, mm_b, mm_c, res, ids)
+
+
 _FRAGMENTS = {
     "v7/59f786beb25f": _rms_fwd_y_rstd,
     "v8/4b90e2d83144": _rms_fwd_3views,
@@ -238,6 +253,8 @@ _FRAGMENTS = {
     "v8/385e1beb9bb9": _swiglu_bwd,
     "v8/71f1d2c9f38b": _xent_fwd,
     "v8/622c35f5d1c6": _xent_bwd,
+    "v6/0b493aad68f0": _norm_emb_bwd_chain,
+    "v5/118d525f44e0": _norm_emb_bwd_chain_fsdp,
 }
 
 

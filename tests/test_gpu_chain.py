@@ -1,0 +1,65 @@
+"""GPU parity of the RMSNorm forward -> backward -> embedding backward chain
+(v6/0b493aad68f0, v5/118d525f44e0) link by link against torch-ROCm eager:
+the norm output and weight gradient within the bf16 tolerance, the summed
+gradient rows g = add_220 + dx within the bf16 tolerance, the table gradient
+against eager's embedding_dense_backward of our own g (accumulation order
+only), and against eager's whole chain within the bound that the summands'
+differences allow: |table - table_eager| <= sum over the id's tokens of
+|g - g_eager| + one bf16 rounding of each side."""
+import pytest
+import torch
+
+from kernelproblems_amd import fragments as fr
+from kernelproblems_amd import fused as F
+from tests._util import BF16_ATOL, BF16_RTOL
+
+pytestmark = pytest.mark.gpu
+aten = torch.ops.aten
+V = 128256
+EPS = 1e-05
+
+
+def _close(a, e, what, rtol=BF16_RTOL, atol=BF16_ATOL):
+    bad = (a.double() - e.double()).abs() > atol + rtol * e.double().abs()
+    assert int(bad.sum()) == 0, f"{what}: {int(bad.sum())} of {a.numel()} outside rtol={rtol} atol={atol}"
+
+
+@pytest.mark.parametrize("fid", ["v6/0b493aad68f0", "v5/118d525f44e0"])
+def test_chain_link_by_link(gpu, fid):
+    print(f"[chain] {fid}", flush=True)
+    mod = fr.load(fid)
+    gen = torch.Generator(device=gpu).manual_seed(7)
+    inputs = mod.get_inputs(device=gpu, generator=gen)
+    if fid == "v6/0b493aad68f0":
+        x, w, a, b, c, res, ids = inputs
+        w_eager = w
+    else:
+        wv, x, a, b, c, res, ids = inputs
+        w = wv
+        w_eager = aten._unsafe_view.default(aten.clone.default(wv, memory_format=torch.contiguous_format), [-1])
+    y0, y1, y2, dw, table = mod.kernel_function(*inputs)
+
+    # eager chain, link by link
+    ye, re = aten._fused_rms_norm.default(x, [x.shape[-1]], w_eager, EPS)
+    dy = aten.add.Tensor(aten.add.Tensor(a.view(x.shape), b.view(x.shape)), c.view(x.shape))
+    dxe, dwe = aten._fused_rms_norm_backward.default(dy, x, [x.shape[-1]], re, w_eager, [True, True])
+    ge = aten.add.Tensor(res, dxe)
+    _close(y0, ye.view(y0.shape), "y")
+    assert y1.data_ptr() == y0.data_ptr() == y2.data_ptr()
+    _close(dw, dwe.float(), "dw")
+
+    # our g (the chain's middle link) against eager's
+    _, _, rstd = F.rms_norm([x], w, EPS, x.shape[-1])
+    g, _ = F.rms_norm_backward([a, b, c], [x], rstd, w, EPS, x.shape[-1], dx_residual=res, dw=None)
+    _close(g, ge, "g = add_220 + dx")
+
+    # the table from our g: eager's bf16 embedding backward of the same rows
+    t_same = aten.embedding_dense_backward.default(g, ids, V, -1, False).float()
+    _close(table, t_same, "table vs eager(our g)")
+
+    # against eager's whole chain: bounded by the summands' differences
+    te = aten.embedding_dense_backward.default(ge, ids, V, -1, False).float()
+    dsum = aten.embedding_dense_backward.default((g.float() - ge.float()).abs(), ids, V, -1, False)
+    bound = dsum + 2.0**-8 * (table.abs() + te.abs()) + 1e-6
+    excess = (table - te).abs() - bound
+    assert float(excess.max()) <= 0, f"table vs eager chain: max excess over the bound {float(excess.max()):.4g}"

@@ -19,6 +19,11 @@ EXACT = {
     "v8/7815074de963": set(range(3, 10)),
     "v8/12545c1e9b06": set(range(3, 9)),
 }
+# Token-sum outputs of chains whose summed rows come from an earlier kernel
+# of the chain: each summand may differ from eager's by one bf16 ulp, and the
+# sum amplifies that near cancellation.  Their values are checked in
+# tests/test_gpu_chain.py against a bound built from the summands themselves.
+CHECKED_IN_CHAIN_TEST = {"v6/0b493aad68f0": {4}, "v5/118d525f44e0": {4}}
 # fp32 outputs that carry no bf16 rounding (complex-multiply result):
 # fp32 reassociation / contraction differences only.
 F32_TOL = {"v7/0f38bc55457c": {0}}
@@ -38,6 +43,8 @@ def _check_close(fid, i, a, e):
     assert a.stride() == e.stride(), f"{what}: strides {a.stride()} vs {e.stride()}"
     if i in EXACT.get(fid, ()):
         assert torch.equal(a, e), f"{what}: not a bit-exact copy"
+        return
+    if i in CHECKED_IN_CHAIN_TEST.get(fid, ()):
         return
     if a.dtype == torch.float32 and i in F32_TOL.get(fid, ()):
         rtol, atol = 1e-5, 1e-5

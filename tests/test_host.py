@@ -58,6 +58,10 @@ SIGNATURES = {
     "v8/385e1beb9bb9": [("mm_662", FFN), ("silu_recomputed", FFN3), ("_unsafe_view_5_recomputed", FFN3),
                         ("_unsafe_view_4_recomputed", FFN3)],
     "v8/71f1d2c9f38b": [("arg584_1", IDS), ("mm_224", (BF, (8192, 128256), (128256, 1)))],
+    "v6/0b493aad68f0": [("embedding", X), ("_unsafe_view_432", W), ("mm_670", MM), ("mm_672", MM), ("mm_674", MM),
+                        ("add_220", X), ("arg583_1", IDS)],
+    "v5/118d525f44e0": [("getitem_791", WV), ("embedding", X), ("mm_670", MM), ("mm_672", MM), ("mm_674", MM),
+                        ("add_220", X), ("arg583_1", IDS)],
     "v8/622c35f5d1c6": [("div", (F32, (), ())), ("_log_softmax", (F32, (8192, 128256), (128256, 1))),
                         ("view_805", (I64, (8192,), (1,))), ("getitem_419", (F32, (), ()))],
 }
