@@ -16,6 +16,7 @@ BASELINE.json configurations:
   c5b  add + RMSNorm backward x, res, dy [16384, 8192]    -> dx bf16, dw fp32
   swf  SwiGLU gate forward    a, b [8192, 14336]          -> bf16(silu(a)) * b        (v8/c68dae22972b)
   swb  SwiGLU gate backward   g, s, b, a [8192, 14336]    -> db, da bf16              (v8/385e1beb9bb9)
+  c3n  embedding -> RMSNorm  table [128256, 4096], ids [8, 2048] Zipf(1.1) -> y [8, 2048, 4096] in one launch (v8/12545c1e9b06)
   cef  cross-entropy forward  logits [8192, 128256] bf16, targets -> loss, total_weight (v8/71f1d2c9f38b)
   ceb  cross-entropy backward log-softmax [8192, 128256] fp32, targets -> bf16 grad   (v8/622c35f5d1c6)
 
@@ -242,6 +243,43 @@ class EmbFwd(Workload):
         torch_ref.embedding_fwd(self.table, self.ids)
 
 
+class EmbNorm(Workload):
+    """The token embedding fused into the first RMSNorm (the gathered rows
+    never reach HBM), at the C3 embedding configuration."""
+
+    def __init__(self, dev, V=128256, D=4096, B=8, S=2048, name="c3n"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        self.ids = _zipf(B * S, V, 1.1, _gen(0)).view(B, S)
+        self.table = _randn((V, D), _gen(1), 0.0, 0.02)
+        self.w = _randn(D, _gen(2), 1.0, 0.02)
+        T = B * S
+        self.bytes_per_call = 2 * T * D * 2 + T * 8 + D * 2
+        self.dominant_bytes = self.bytes_per_call
+        self.dominant_kernel = "rms_fwd_vec"
+        self.probe_mix = (1, 1, T * D * 2, T * D * 2, f"copy of {T * D * 2 / 1e6:.1f} MB (gathered rows in, y out)")
+        self.description = (f"embedding -> RMSNorm fused (v8/12545c1e9b06 region): table [{V},{D}] bf16, ids "
+                            f"[{B},{S}] int64 Zipf(1.1) -> y [{B},{S},{D}] bf16 (eps=1e-5), no HBM intermediate")
+        uniq = int(torch.unique(self.ids).numel())
+        R = max(2, math.ceil(MIN_ROTATION_BYTES / (uniq * D * 2 + T * D * 2)))
+        tab_d, ids_d, w_d = self.table.to(dev), self.ids.to(dev), self.w.to(dev)
+        fn = L.lib().kp_embedding_rmsnorm_fwd_bf16
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for r in range(R):
+            tab = tab_d if r == 0 else tab_d.clone()
+            y = torch.empty((B, S, D), dtype=torch.bfloat16, device=dev)
+            args = (tab.data_ptr(), V, D, ids_d.data_ptr(), 8, T, w_d.data_ptr(), D, D, None, D, y.data_ptr(), D,
+                    None, D, 1e-5, None, stream)
+            self.sets.append((fn, args, (tab, y, w_d, ids_d)))
+        self.cpu_sample = f"full [{B},{S}] gather + norm"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        torch_ref.embedding_rms_norm_fwd(self.table, self.ids, self.w, 1e-5)
+
+
 class EmbBwd(Workload):
     def __init__(self, dev, V=128256, D=4096, B=8, S=2048, name="c3b"):
         super().__init__(dev)
@@ -440,6 +478,8 @@ def make_workload(name, dev):
         return EmbFwd(dev)
     if name == "c3b":
         return EmbBwd(dev)
+    if name == "c3n":
+        return EmbNorm(dev)
     if name == "c4":
         return Rope(dev)
     if name == "c5f":
@@ -457,7 +497,7 @@ def make_workload(name, dev):
     raise SystemExit(f"unknown workload {name!r}")
 
 
-ALL = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b", "swf", "swb", "cef", "ceb"]
+ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c5f", "c5b", "swf", "swb", "cef", "ceb"]
 
 
 # ------------------------------------------------------------------ measure

@@ -54,7 +54,8 @@ const char* kp_last_error_message(void);
  * in an external harness).  While set, every entry point launches its
  * dominant kernel with hipExtLaunchKernel, which stamps start_event and
  * stop_event (hipEvent_t, timing enabled) at that kernel's own start and
- * completion: the row kernel of the RMSNorm entry points, the gather kernel
+ * completion: the row kernel of the RMSNorm entry points (and of
+ * kp_embedding_rmsnorm_fwd_bf16), the gather kernel
  * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
  * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16, the
  * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16, the row kernel of
@@ -122,6 +123,30 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
                         float* dw_f32, void* dw_bf16, int dw_f32_round_bf16,
                         int64_t M, int64_t N, float eps,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Token embedding fused into the RMSNorm forward that consumes it:
+ *   h[t, :] = table[indices[t], :]   (bit copy; written only when h_out != NULL)
+ *   y[t, :] = bf16(fp32(h) * rstd_t * fp32(w)),  rstd_t = 1 / sqrt(sum(h^2) / N + eps)
+ * in one launch: the gathered rows go straight from the table into the norm's
+ * registers instead of through an HBM intermediate.
+ *
+ * Replaces embedding.default -> _fused_rms_norm.default at
+ * v8/12545c1e9b06/problem.py:24-42 (table = [128256, 4096] view of an FSDP
+ * flat buffer, ids i64 [1, 8192], the norm weight read in place from the
+ * layer buffer).  table: bf16 [V, N] rows (row stride table_row_stride);
+ * indices: T integers of index_bytes (4 or 8); weight as in
+ * kp_rmsnorm_fwd_bf16; y / h_out: bf16 [T, N] with the given row strides;
+ * rstd: fp32 [T] or NULL.  An index outside [0, V) reads nothing: its h and
+ * y rows are zero and, when error_flag != NULL, *error_flag is set to 1.
+ * Rows, strides and pointers must be 16-byte granular with N a fast-path row
+ * length; otherwise KP_EUNSUPPORTED (compose kp_embedding_fwd_bf16 and
+ * kp_rmsnorm_fwd_bf16 instead).
+ */
+int kp_embedding_rmsnorm_fwd_bf16(const void* table, int64_t V, int64_t table_row_stride, const void* indices,
+                                  int index_bytes, int64_t T, const void* weight, int64_t w_seg_len,
+                                  int64_t w_seg_stride, void* h_out, int64_t h_stride, void* y, int64_t y_stride,
+                                  float* rstd, int64_t N, float eps, int32_t* error_flag, void* stream);
 
 /* ------------------------------------------------------------------------
  * Streaming-ceiling probe (a measurement aid; no counterpart in the

@@ -19,6 +19,7 @@ from .fused import (
     cross_entropy_loss,
     embedding,
     embedding_dense_backward,
+    embedding_rms_norm,
     index_checking,
     rms_norm,
     rms_norm_backward,
@@ -37,6 +38,7 @@ __all__ = [
     "cross_entropy_loss",
     "embedding",
     "embedding_dense_backward",
+    "embedding_rms_norm",
     "fused",
     "index_checking",
     "rms_norm",

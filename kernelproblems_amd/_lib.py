@@ -85,6 +85,8 @@ SIGNATURES = {
     ),
     "kp_unshard_bf16": (i32, [vp, i64, i64, pi64, pi64, pvp, i32, vp]),
     "kp_stream_probe": (i32, [pvp, i32, i64, pvp, i32, i64, i32, vp]),
+    "kp_embedding_rmsnorm_fwd_bf16": (i32, [vp, i64, i64, vp, i32, i64, vp, i64, i64, vp, i64, vp, i64, vp, i64, f32,
+                                            vp, vp]),
     "kp_swiglu_fwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, i64, i64, vp]),
     "kp_swiglu_bwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, vp]),
     "kp_cross_entropy_fwd_workspace_size": (sz, [i64]),

@@ -312,6 +312,58 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
   return check_launch(who);
 }
 
+int kp_embedding_rmsnorm_fwd_bf16(const void* table, int64_t V, int64_t table_row_stride, const void* indices,
+                                  int index_bytes, int64_t T, const void* weight, int64_t w_seg_len,
+                                  int64_t w_seg_stride, void* h_out, int64_t h_stride, void* y, int64_t y_stride,
+                                  float* rstd, int64_t N, float eps, int32_t* error_flag, void* stream) {
+  static const char* who = "kp_embedding_rmsnorm_fwd_bf16";
+  if (T < 0 || N <= 0 || V <= 0) return fail(KP_EINVAL, "%s: need T >= 0, N > 0, V > 0", who);
+  if (index_bytes != 4 && index_bytes != 8) return fail(KP_EINVAL, "%s: index_bytes must be 4 or 8", who);
+  if (T > 0 && (table == nullptr || indices == nullptr || y == nullptr))
+    return fail(KP_EINVAL, "%s: table, indices and y are required", who);
+  if (table_row_stride < N || y_stride < 0 || (h_out != nullptr && h_stride < 0))
+    return fail(KP_EINVAL, "%s: bad row stride", who);
+  if (weight != nullptr && (w_seg_len <= 0 || w_seg_stride < 0))
+    return fail(KP_EINVAL, "%s: weight segment length must be > 0", who);
+  if (T == 0) return KP_OK;
+
+  RmsFwdArgs a{};
+  a.x[0] = static_cast<const uint16_t*>(table);
+  a.xs[0] = table_row_stride;
+  a.n_x = 1;
+  a.idx = indices;
+  a.idx_bytes = index_bytes;
+  a.idx_rows = V;
+  a.err = error_flag;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.w_seg_len = weight ? w_seg_len : N;
+  a.w_seg_stride = weight ? w_seg_stride : N;
+  a.h = static_cast<uint16_t*>(h_out);
+  a.hs = h_stride;
+  a.y = static_cast<uint16_t*>(y);
+  a.ys = y_stride;
+  a.rstd = rstd;
+  a.M = T;
+  a.N = N;
+  a.eps = eps;
+
+  int vpl = 0, wpr = 0;
+  bool vec = pick_vec(N, true, &vpl, &wpr) && aligned16(table) && (table_row_stride & 7) == 0 && aligned16(y) &&
+             (y_stride & 7) == 0;
+  if (vec && h_out) vec = aligned16(h_out) && (h_stride & 7) == 0;
+  if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
+  const FwdKernel fk = vec ? fwd_gather_kernel(vpl, wpr) : nullptr;
+  if (fk == nullptr)
+    return fail(KP_EUNSUPPORTED, "%s: row shape / alignment without a fused kernel (N=%lld)", who, (long long)N);
+  const int rb = 4 / wpr;
+  const int64_t groups = ceil_div(T, rb);
+  const int64_t cap = (int64_t)cu_count() * fwd_bpc((int64_t)vpl * 1024);
+  const int grid = (int)(groups < cap ? groups : cap);
+  void* args[] = {&a};
+  launch_dominant_raw(reinterpret_cast<const void*>(fk), dim3(grid), dim3(kThreads), args, 0, as_stream(stream));
+  return check_launch(who);
+}
+
 size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N) {
   if (M <= 0 || N <= 0) return 16;
   // Partial rows: at most one per row block; the block count never exceeds 4 per

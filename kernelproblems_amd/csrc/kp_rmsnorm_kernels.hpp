@@ -28,6 +28,12 @@ struct RmsFwdArgs {
   const uint16_t* x[3];
   int64_t xs[3];
   int n_x;
+  // Gather variant: row r of term 0 is x[0] row idx[r] (idx_bytes 4 or 8);
+  // an id outside [0, idx_rows) reads nothing, gives a zero row and sets *err.
+  const void* idx;
+  int idx_bytes;
+  int64_t idx_rows;
+  int32_t* err;
   const uint16_t* w;
   int64_t w_seg_len, w_seg_stride;
   uint16_t* h;
@@ -131,13 +137,20 @@ __device__ __forceinline__ void load_weight(u32x4 (&wv)[VPL], const uint16_t* w,
 // cross-wave combine, y = bf16(h * rstd * w), optional h and rstd stores.
 // The summed row is unpacked to fp32 once for both passes and the weight
 // stays in fp32 registers for the whole kernel (see bwd_row).
-template <int VPL, int WPR, int NX>
-__device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, NX>& cur, const float (&wf)[VPL * 8],
-                                        float (&red)[2][4], int64_t row, int64_t col, int lane, int wave, int part,
-                                        int rloc, int it) {
+template <int VPL, int WPR, int NX, bool GATHER>
+__device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, NX>& cur, bool id_ok,
+                                        const float (&wf)[VPL * 8], float (&red)[2][4], int64_t row, int64_t col,
+                                        int lane, int wave, int part, int rloc, int it) {
   const bool valid = row < a.M;
   u32x4 hv[VPL];
   sum_raw<VPL, NX>(hv, cur);
+  if constexpr (GATHER) {
+    if (!id_ok) {
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) hv[i] = u32x4{0u, 0u, 0u, 0u};
+      if (valid && part == 0 && lane == 0 && a.err) *a.err = 1;
+    }
+  }
   float hf[VPL * 8];
 #pragma unroll
   for (int i = 0; i < VPL; ++i) unpack8(hv[i], hf + i * 8);
@@ -163,7 +176,7 @@ __device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, N
       for (int e = 0; e < 8; ++e) o[e] = (hf[i * 8 + e] * r) * wf[i * 8 + e];
       st16_stream(yrow + i * 512, pack8(o));
     }
-    if (NX > 1 && a.h != nullptr) {
+    if ((NX > 1 || GATHER) && a.h != nullptr) {
       uint16_t* hrow = a.h + row * a.hs + col;
 #pragma unroll
       for (int i = 0; i < VPL; ++i) st16_stream(hrow + i * 512, hv[i]);
@@ -178,7 +191,16 @@ __device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, N
 // separate named variables, and the loop is unrolled two steps per pass so
 // that no slot is ever copied: an array of slots indexed by the step ends up
 // in scratch memory, and a slot copy makes the wave wait for the prefetch.
-template <int VPL, int WPR, int NX>
+// The source row of a gathered row: ids[row] when in [0, idx_rows), else row
+// 0 (always readable) with ok = false.  row is wave-uniform: a scalar load.
+__device__ __forceinline__ int64_t gather_src(const RmsFwdArgs& a, int64_t row, bool& ok) {
+  const int64_t id = a.idx_bytes == 8 ? static_cast<const int64_t*>(a.idx)[row]
+                                      : (int64_t) static_cast<const int32_t*>(a.idx)[row];
+  ok = id >= 0 && id < a.idx_rows;
+  return ok ? id : 0;
+}
+
+template <int VPL, int WPR, int NX, bool GATHER>
 __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   constexpr int RB = 4 / WPR;
   constexpr int SEG = 512 * VPL;
@@ -198,13 +220,17 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   const int64_t ngroups = ceil_div_dev(a.M, RB);
   const int64_t G = gridDim.x;
   RawRow<VPL, NX> s0, s1;
+  bool s0ok = true, s1ok = true;
   int it = 0;
 #define KP_ROW(g) ((g) * RB + rloc)
-#define KP_LOAD(S, g)                                              \
-  load_raw<VPL, NX>(S, a.x, a.xs, clamp_row(KP_ROW(g), a.M), col); \
+#define KP_LOAD(S, g)                                                                                 \
+  {                                                                                                   \
+    const int64_t row_ = clamp_row(KP_ROW(g), a.M);                                                   \
+    load_raw<VPL, NX>(S, a.x, a.xs, GATHER ? gather_src(a, row_, S##ok) : row_, col);                 \
+  }                                                                                                   \
   __builtin_amdgcn_sched_barrier(0)
-#define KP_PROC(S, g)                                                               \
-  fwd_row<VPL, WPR, NX>(a, S, wf, red, KP_ROW(g), col, lane, wave, part, rloc, it); \
+#define KP_PROC(S, g)                                                                               \
+  fwd_row<VPL, WPR, NX, GATHER>(a, S, S##ok, wf, red, KP_ROW(g), col, lane, wave, part, rloc, it); \
   ++it
   // Exact trip count: the grid never exceeds the row-group count, so every
   // block owns nb >= 1 groups and nothing is prefetched past its last one.
@@ -435,6 +461,8 @@ typedef void (*BwdKernel)(RmsBwdArgs);
 // kp_rms_bwd_<VPL>.hip the backward shapes with VPL chunks per lane.
 // Each getter returns nullptr for a shape or term combination it lacks.
 FwdKernel fwd_kernel(int vpl, int wpr, int nx);
+// Gather variants (one term, row ids): kp_rms_fwd_gather.hip.
+FwdKernel fwd_gather_kernel(int vpl, int wpr);
 BwdKernel bwd_kernel_vpl1(int wpr, int nx, int ndy, bool res);
 BwdKernel bwd_kernel_vpl2(int wpr, int nx, int ndy, bool res);
 BwdKernel bwd_kernel_vpl3(int wpr, int nx, int ndy, bool res);
@@ -445,9 +473,9 @@ BwdKernel bwd_kernel_vpl68(int vpl, int wpr, int nx, int ndy, bool res);
 template <int VPL, int WPR>
 FwdKernel fwd_for_terms(int nx) {
   switch (nx) {
-    case 1: return rms_fwd_vec<VPL, WPR, 1>;
-    case 2: return rms_fwd_vec<VPL, WPR, 2>;
-    case 3: return rms_fwd_vec<VPL, WPR, 3>;
+    case 1: return rms_fwd_vec<VPL, WPR, 1, false>;
+    case 2: return rms_fwd_vec<VPL, WPR, 2, false>;
+    case 3: return rms_fwd_vec<VPL, WPR, 3, false>;
   }
   return nullptr;
 }

@@ -259,6 +259,51 @@ def embedding(table: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
     return out
 
 
+def embedding_rms_norm(
+    table: torch.Tensor,
+    indices: torch.Tensor,
+    weight: Optional[torch.Tensor],
+    eps: float,
+    *,
+    return_h: bool = False,
+    return_rstd: bool = True,
+):
+    """RMSNorm of embedding rows: h = table[indices] (bit copy), y =
+    bf16(h * rstd * w), in one launch that reads each gathered row straight
+    into the norm (the embedding.default -> _fused_rms_norm region of
+    v8/12545c1e9b06/problem.py:24-42).  The weight may be a segmented FSDP
+    view as in rms_norm.  Returns (h or None, y, rstd or None), shaped
+    indices.shape + [D].  Row shapes without a fused kernel run the gather
+    and the norm as two launches (same results)."""
+    _need_gpu("embedding_rms_norm table", table)
+    if table.dim() != 2:
+        raise RuntimeError("embedding_rms_norm: table must be 2-D")
+    idx, ib = _index_info(indices)
+    V, D = table.shape
+    dev = table.device
+    tt, trs, _ = _as_rows(table, D)
+    T = idx.numel()
+    y = torch.empty((*indices.shape, D), dtype=torch.bfloat16, device=dev)
+    h = torch.empty_like(y) if return_h else None
+    rstd = torch.empty(indices.shape, dtype=torch.float32, device=dev) if return_rstd else None
+    w_t, seg_len, seg_stride = (None, D, D)
+    if weight is not None:
+        _need_gpu("embedding_rms_norm weight", weight)
+        w_t, seg_len, seg_stride = _weight_segments(weight, D)
+    flag = _flag(dev)
+    st = L.lib().kp_embedding_rmsnorm_fwd_bf16(
+        tt.data_ptr(), V, trs, idx.data_ptr(), ib, T, _ptr(w_t), seg_len, seg_stride, _ptr(h), D, y.data_ptr(), D,
+        _ptr(rstd), D, float(eps), _ptr(flag), _stream(dev))
+    if st == L.KP_EUNSUPPORTED:
+        emb = embedding(table, indices)
+        _, y, r = rms_norm([emb], weight, eps, D, return_rstd=return_rstd)
+        return (emb if return_h else None), y, (r.view(indices.shape) if return_rstd else None)
+    if st != L.KP_OK:
+        raise L.KPError("kp_embedding_rmsnorm_fwd_bf16", st, L.lib().kp_last_error_message().decode())
+    _raise_if_flagged(flag, "embedding_rms_norm")
+    return h, y, rstd
+
+
 def embedding_dense_backward(
     grad_output: torch.Tensor,
     indices: torch.Tensor,

@@ -123,3 +123,9 @@ def cross_entropy_bwd(lsm: torch.Tensor, targets: torch.Tensor, grad_loss: float
     gi = aten.nll_loss_backward.default(g, lsm, targets, None, 2, -100, tw)
     d = aten._log_softmax_backward_data.default(gi, lsm, 1, torch.float32)
     return aten._to_copy.default(d, dtype=torch.bfloat16)
+
+
+def embedding_rms_norm_fwd(table: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, eps: float):
+    """v8/12545c1e9b06/problem.py:24-42: embedding.default -> _fused_rms_norm."""
+    x = aten.embedding.default(table, ids)
+    return aten._fused_rms_norm.default(x, [x.shape[-1]], w, eps)[0]

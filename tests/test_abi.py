@@ -134,6 +134,17 @@ def test_cross_entropy_validation(lib):
     _expect(lib, L.KP_EINVAL, bwd, 16, 8, 32, 8, -100, 1.0, 64, 8, 4, 0, None, None)    # V = 0
 
 
+def test_embedding_rmsnorm_validation(lib):
+    fn = "kp_embedding_rmsnorm_fwd_bf16"
+    _expect(lib, L.KP_EINVAL, fn, 16, 100, 64, 32, 3, 8, None, 64, 64, None, 64, 48, 64, None, 64, 1e-5, None, None)
+    _expect(lib, L.KP_EINVAL, fn, 16, 100, 32, 32, 8, 8, None, 64, 64, None, 64, 48, 64, None, 64, 1e-5, None, None)
+    _expect(lib, L.KP_EINVAL, fn, 16, 100, 64, 32, 8, 8, None, 64, 64, None, 64, None, 64, None, 64, 1e-5, None, None)
+    _expect(lib, L.KP_EUNSUPPORTED, fn, 16, 100, 64, 32, 8, 8, None, 64, 64, None, 64, 48, 64, None, 60, 1e-5, None,
+            None)  # no fast-path row shape for N = 60
+    assert lib.kp_embedding_rmsnorm_fwd_bf16(None, 100, 64, None, 8, 0, None, 64, 64, None, 64, None, 64, None, 64,
+                                             1e-5, None, None) == L.KP_OK
+
+
 def test_stream_probe_validation(lib):
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 5, 64, L.ptr_array([32]), 1, 64, 4, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, 4, None)

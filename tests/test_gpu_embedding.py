@@ -4,7 +4,8 @@ import pytest
 import torch
 
 import kernelproblems_amd as kp
-from tests._util import bf, gen, randn_bf16, to_u16, zipf_ids
+import oracle
+from tests._util import bf, gen, randn_bf16, to_u16, ulp_bf16, zipf_ids
 
 pytestmark = pytest.mark.gpu
 
@@ -164,3 +165,46 @@ def test_embedding_bwd_on_side_stream_repeated(gpu, oracle_lib):
     for o in outs[1:]:
         assert torch.equal(o, outs[0])
     np.testing.assert_allclose(outs[0].cpu().numpy(), exact, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("V,D,T,idx_dtype", [(1000, 4096, 777, torch.int64), (5000, 8192, 300, torch.int32),
+                                              (300, 2048, 64, torch.int64), (50, 100, 33, torch.int64)])
+def test_embedding_rms_norm_equals_the_two_launch_composition(gpu, V, D, T, idx_dtype):
+    """The fused gather + norm (D = 100: the two-launch fallback) against
+    embedding() then rms_norm(): h, y and rstd bit for bit, and y within the
+    oracle's tolerance."""
+    print(f"[emb+rms] V={V} D={D} T={T} {idx_dtype}", flush=True)
+    g = torch.Generator().manual_seed(V + D + T)
+    table = (torch.randn(V, D, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    w = (1 + 0.02 * torch.randn(D, generator=g)).to(torch.bfloat16).to(gpu)
+    ids = torch.randint(0, V, (T,), generator=g).to(idx_dtype).to(gpu)
+    h, y, r = kp.embedding_rms_norm(table, ids, w, 1e-5, return_h=True)
+    emb = kp.embedding(table, ids)
+    _, y2, r2 = kp.rms_norm([emb], w, 1e-5, D)
+    assert torch.equal(h, emb) and torch.equal(y, y2) and torch.equal(r, r2.view(r.shape))
+    _, yo, _ = oracle.rmsnorm_fwd([to_u16(emb)], to_u16(w), 1e-5, D)
+    assert (ulp_bf16(to_u16(y), yo) <= 1).all()
+
+
+def test_embedding_rms_norm_fsdp_weight_and_bad_ids(gpu):
+    """Weight as an [8, 512] row-strided view of a flat buffer; ids outside
+    [0, V) give zero h / y rows and raise with index checking on."""
+    V, D = 64, 4096
+    g = torch.Generator().manual_seed(11)
+    table = torch.randn(V, D, generator=g).to(torch.bfloat16).to(gpu)
+    flat = torch.randn(8 * 27264, generator=g).to(torch.bfloat16).to(gpu)
+    wv = flat.as_strided((8, 512), (27264, 1))
+    ids = torch.tensor([[3, 63, 0, 17]], device=gpu)
+    h, y, _ = kp.embedding_rms_norm(table, ids, wv, 1e-5, return_h=True)
+    _, y2, _ = kp.rms_norm([kp.embedding(table, ids)], wv.contiguous().view(-1), 1e-5, D)
+    assert y.shape == (1, 4, D) and torch.equal(y, y2)
+    bad = torch.tensor([1, 64, -1, 5], device=gpu)
+    with pytest.raises(IndexError):
+        kp.embedding_rms_norm(table, bad, wv, 1e-5)
+    kp.set_index_checking(False)
+    try:
+        h, y, r = kp.embedding_rms_norm(table, bad, wv, 1e-5, return_h=True)
+    finally:
+        kp.set_index_checking(True)
+    assert not h[1:3].any() and not y[1:3].any()
+    assert torch.equal(h[[0, 3]], table[[1, 5]])
