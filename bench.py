@@ -599,6 +599,16 @@ def measure_probe(wl, steps, warmup):
             "chunks_per_thread": best, "us_by_tile": {str(k): round(v * 1e3, 3) for k, v in per_tile.items()}}
 
 
+def _cpu_model():
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
 def measure_cpu(wl, seconds):
     import torch
     wl.cpu_run()  # warm-up
@@ -617,6 +627,8 @@ def measure_cpu(wl, seconds):
         "unit": "GB/s",
         "ms_per_call": med * 1e3,
         "cores": torch.get_num_threads(),
+        "os_cpu_count": os.cpu_count(),
+        "cpu_model": _cpu_model(),
         "kind": "port",
         "sample": (f"torch CPU eager restatement of the fragment (oracle/torch_ref.py), {wl.cpu_sample}, "
                    f"median of {len(times)} timed calls after 1 warm-up"),
