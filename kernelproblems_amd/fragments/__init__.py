@@ -28,6 +28,9 @@ FRAGMENTS = (
     "v8/71f1d2c9f38b", "v8/622c35f5d1c6",
     # chain: RMSNorm forward -> backward (+ gradient adds, residual) -> embedding backward
     "v6/0b493aad68f0", "v5/118d525f44e0",
+    # chain: (residual add +) RMSNorm forward -> backward (+ gradient adds, residual epilogue)
+    "v6/822931829090", "v6/e9198b707240", "v5/92ce4a0c7b2c", "v5/401b52261ef5", "v4/363b7b58c971",
+    "v6/408ac0979ac5", "v4/9c745ea697a7", "v6/28b45679fca1",
 )
 
 

@@ -223,6 +223,23 @@ def _norm_emb_bwd_chain_fsdp(wv, x, mm_a, mm_b, mm_c, res, ids):  # v5/118d525f4
     return _norm_emb_bwd_chain(x, _clone_weight(wv), mm_a, mm_b, mm_c, res, ids)
 
 
+def _norm_chain(x_terms, w, dy_terms, res, n_views):
+    # v6/822931829090/problem.py:16-66 and the variants registered below: h = add(s)
+    # of the x terms, _fused_rms_norm, dy = add(s), backward with the forward's
+    # rstd (or recomputed), out = add.Tensor(res, dx), dw widened to f32
+    shape = list(x_terms[0].shape) if x_terms[0].dim() == 3 else [1, *x_terms[0].shape]
+    h = aten.view.default(x_terms[0], shape)
+    for t in x_terms[1:]:
+        h = aten.add.Tensor(h, aten.view.default(t, shape))
+    y, r = _norm(h, w)
+    dy = aten.view.default(dy_terms[0], shape)
+    for t in dy_terms[1:]:
+        dy = aten.add.Tensor(dy, aten.view.default(t, shape))
+    dx, dw = _norm_bwd(dy, h, r, w)
+    out = dx if res is None else aten.add.Tensor(res, dx)
+    return (*_views(y, n_views), out, aten._to_copy.default(dw, dtype=torch.float32))
+
+
 _FRAGMENTS = {
     "v7/59f786beb25f": _rms_fwd_y_rstd,
     "v8/4b90e2d83144": _rms_fwd_3views,
@@ -255,6 +272,14 @@ _FRAGMENTS = {
     "v8/622c35f5d1c6": _xent_bwd,
     "v6/0b493aad68f0": _norm_emb_bwd_chain,
     "v5/118d525f44e0": _norm_emb_bwd_chain_fsdp,
+    "v6/822931829090": lambda x, w, a, b, c, res: _norm_chain([x], w, [a, b, c], res, 3),
+    "v6/e9198b707240": lambda x, w, a, b, res: _norm_chain([x], w, [a, b], res, 2),
+    "v5/92ce4a0c7b2c": lambda wv, x, a, b, c, res: _norm_chain([x], _clone_weight(wv), [a, b, c], res, 3),
+    "v5/401b52261ef5": lambda wv, x, a, b, res: _norm_chain([x], _clone_weight(wv), [a, b], res, 2),
+    "v4/363b7b58c971": lambda wv, x, a, b, c, res: _norm_chain([x], _clone_weight(wv), [a, b, c], res, 3),
+    "v6/408ac0979ac5": lambda mm, emb, w, a, b, res: _norm_chain([emb, mm], w, [a, b], res, 2),
+    "v4/9c745ea697a7": lambda mm, emb, wv, a, b, res: _norm_chain([emb, mm], _clone_weight(wv), [a, b], res, 2),
+    "v6/28b45679fca1": lambda mm, x, dy, w: _norm_chain([x, mm], w, [dy], None, 0),
 }
 
 

@@ -24,6 +24,16 @@ EXACT = {
 # sum amplifies that near cancellation.  Their values are checked in
 # tests/test_gpu_chain.py against a bound built from the summands themselves.
 CHECKED_IN_CHAIN_TEST = {"v6/0b493aad68f0": {4}, "v5/118d525f44e0": {4}}
+# Residual-epilogue outputs bf16(res + bf16(dx)): output index -> index of
+# the residual input.  dx carries the backward's bf16 tolerance relative to
+# dx itself, so where res and dx nearly cancel the bound is taken relative to
+# the summands (|out| + |out - res| >= |dx| up to one rounding), not to the sum.
+RESIDUAL_SUM = {
+    "v4/363b7b58c971": {3: 5}, "v4/9c745ea697a7": {2: 5}, "v5/401b52261ef5": {2: 4},
+    "v5/92ce4a0c7b2c": {3: 5}, "v6/408ac0979ac5": {2: 5}, "v6/822931829090": {3: 5},
+    "v6/e9198b707240": {2: 4}, "v7/7f544ceb2120": {0: 5}, "v7/ed20955ec34b": {0: 6},
+    "v8/d8f596b3df34": {0: 5},
+}
 # fp32 outputs that carry no bf16 rounding (complex-multiply result):
 # fp32 reassociation / contraction differences only.
 F32_TOL = {"v7/0f38bc55457c": {0}}
@@ -37,7 +47,7 @@ def _storage(t):
     return t.untyped_storage().data_ptr()
 
 
-def _check_close(fid, i, a, e):
+def _check_close(fid, i, a, e, inputs):
     what = f"{fid} output {i}"
     assert a.shape == e.shape and a.dtype == e.dtype, f"{what}: {a.shape}/{a.dtype} vs {e.shape}/{e.dtype}"
     assert a.stride() == e.stride(), f"{what}: strides {a.stride()} vs {e.stride()}"
@@ -51,7 +61,13 @@ def _check_close(fid, i, a, e):
     else:
         rtol, atol = BF16_RTOL, BF16_ATOL
     af, ef = a.double(), e.double()
-    bad = (af - ef).abs() > atol + rtol * ef.abs()
+    scale = ef.abs()
+    if i in RESIDUAL_SUM.get(fid, {}):
+        res = inputs[RESIDUAL_SUM[fid][i]]
+        assert res.numel() == ef.numel()
+        res = res.double().reshape(ef.shape)
+        scale = scale + (ef - res).abs()
+    bad = (af - ef).abs() > atol + rtol * scale
     n_bad = int(bad.sum())
     assert n_bad == 0, f"{what}: {n_bad} of {a.numel()} outside rtol={rtol} atol={atol}; worst {(af - ef).abs().max():.4g}"
 
@@ -74,7 +90,7 @@ def test_fragment_matches_eager(fid, gpu):
     assert len(ours) == len(ref), f"{fid}: {len(ours)} outputs, expected {len(ref)}"
     for i, (a, e) in enumerate(zip(ours, ref)):
         assert a.device == e.device
-        _check_close(fid, i, a, e)
+        _check_close(fid, i, a, e, inputs)
     for i in range(len(ref)):
         for j in range(i + 1, len(ref)):
             same_ref = _storage(ref[i]) == _storage(ref[j])

@@ -62,6 +62,21 @@ SIGNATURES = {
                         ("add_220", X), ("arg583_1", IDS)],
     "v5/118d525f44e0": [("getitem_791", WV), ("embedding", X), ("mm_670", MM), ("mm_672", MM), ("mm_674", MM),
                         ("add_220", X), ("arg583_1", IDS)],
+    "v6/822931829090": [("add_1", X), ("_unsafe_view_450", W), ("mm_656", MM), ("mm_658", MM), ("mm_660", MM),
+                        ("add_215", X)],
+    "v6/e9198b707240": [("add_62_recomputed", X), ("_unsafe_view_986", W), ("mm_230", MM), ("mm_232", MM),
+                        ("getitem_420", X)],
+    "v5/92ce4a0c7b2c": [("getitem_818", WV), ("add_1", X), ("mm_656", MM), ("mm_658", MM), ("mm_660", MM),
+                        ("add_215", X)],
+    "v5/401b52261ef5": [("getitem_1624", WV), ("add_62_recomputed", X), ("mm_230", MM), ("mm_232", MM),
+                        ("getitem_420", X)],
+    "v4/363b7b58c971": [("getitem_818", WV), ("add_1", X), ("mm_656", MM), ("mm_658", MM), ("mm_660", MM),
+                        ("add_215", X)],
+    "v6/408ac0979ac5": [("mm_3", MM), ("embedding", X), ("_unsafe_view_428", W), ("mm_664", MM), ("mm_666", MM),
+                        ("add_218", X)],
+    "v4/9c745ea697a7": [("mm_3", MM), ("embedding", X), ("getitem_787", WV), ("mm_664", MM), ("mm_666", MM),
+                        ("add_218", X)],
+    "v6/28b45679fca1": [("mm_223", MM), ("add_62_recomputed", X), ("mm_226", MM), ("view_3253", W)],
     "v8/622c35f5d1c6": [("div", (F32, (), ())), ("_log_softmax", (F32, (8192, 128256), (128256, 1))),
                         ("view_805", (I64, (8192,), (1,))), ("getitem_419", (F32, (), ()))],
 }
