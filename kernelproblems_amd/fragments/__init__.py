@@ -21,7 +21,8 @@ FRAGMENTS = (
     "v7/1e49beb8a123", "v8/12545c1e9b06", "v7/a12a160cb11b",
     # RoPE (interleaved complex, table) forward / backward
     "v7/e29b92927600", "v8/493cad38cac9", "v8/c8c60d8f7015", "v8/97032595d968", "v7/0f38bc55457c",
-    "v7/5c65f62b0422", "v7/bfe872e373e4",
+    "v7/5c65f62b0422", "v7/bfe872e373e4", "v5/ca76bd89ec38", "v4/6b92d6e665ab", "v6/03d64c25b654",
+    "v6/dc55b25cdcb2", "v5/a1bb72d946b0", "v4/a1318bc813d2",
     # SwiGLU gate forward / backward
     "v8/c68dae22972b", "v8/385e1beb9bb9",
     # token cross-entropy forward / backward

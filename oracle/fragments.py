@@ -179,6 +179,26 @@ def _rope_bwd(g, table):                 # v7/5c65f62b0422/problem.py:16-40, v7/
     return aten.view.default(out, [out.shape[1], -1])
 
 
+def _rope_qk_fwd_twice(pos, table, mm, mm1):  # v5/ca76bd89ec38/problem.py:16-132, v4/6b92d6e665ab:16-132
+    out = []
+    for _ in range(2):
+        q, k = _rope_qk_fwd(pos, table, mm, mm1)
+        out += [aten.transpose.int(q, 1, 2), aten.transpose.int(k, 1, 2)]
+    return tuple(out)
+
+
+def _rope_bwd_cloned(table, g):          # v6/03d64c25b654/problem.py:16-43, v6/dc55b25cdcb2:16-43
+    return _rope_bwd(g, aten.clone.default(table))
+
+
+def _rope_bwd_qkv(c62, c63, gq, gk, gv):  # v5/a1bb72d946b0/problem.py:16-85, v4/a1318bc813d2:16-85
+    q = aten.t.default(_rope_bwd(gq, aten.clone.default(c63)))
+    k = aten.t.default(_rope_bwd(gk, aten.clone.default(c62)))
+    v = aten.transpose.int(gv, 1, 2)
+    v = aten.view.default(aten.view.default(v, [1, v.shape[1], -1]), [v.shape[1], -1])
+    return q, k, aten.t.default(v)
+
+
 def _swiglu_fwd(mm4, mm5):               # v8/c68dae22972b/problem.py:15-28
     a = aten._unsafe_view.default(mm4, [1, *mm4.shape])
     b = aten._unsafe_view.default(mm5, [1, *mm5.shape])
@@ -266,6 +286,12 @@ _FRAGMENTS = {
     "v7/0f38bc55457c": _rope_qk(True),
     "v7/5c65f62b0422": _rope_bwd,
     "v7/bfe872e373e4": _rope_bwd,
+    "v5/ca76bd89ec38": _rope_qk_fwd_twice,
+    "v4/6b92d6e665ab": _rope_qk_fwd_twice,
+    "v6/03d64c25b654": _rope_bwd_cloned,
+    "v6/dc55b25cdcb2": _rope_bwd_cloned,
+    "v5/a1bb72d946b0": _rope_bwd_qkv,
+    "v4/a1318bc813d2": _rope_bwd_qkv,
     "v8/c68dae22972b": _swiglu_fwd,
     "v8/385e1beb9bb9": _swiglu_bwd,
     "v8/71f1d2c9f38b": _xent_fwd,

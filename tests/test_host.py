@@ -25,6 +25,8 @@ FLAT_EMB = (BF, (525336576,), (1,))
 FLAT_LAYER = (BF, (218112000,), (1,))
 FFN = (BF, (8192, 14336), (14336, 1))
 FFN3 = (BF, (1, 8192, 14336), (117440512, 14336, 1))
+GQ = (BF, (1, 32, 8192, 128), (33554432, 128, 4096, 1))
+GK = (BF, (1, 8, 8192, 128), (8388608, 128, 1024, 1))
 
 SIGNATURES = {
     "v7/59f786beb25f": [("embedding", X), ("_unsafe_view_432", W)],
@@ -54,6 +56,14 @@ SIGNATURES = {
     "v7/0f38bc55457c": [("mm", MM), ("mm_1", MM1), ("arg586_1", POS), ("arg582_1", TAB)],
     "v7/5c65f62b0422": [("getitem_642", (BF, (1, 8, 8192, 128), (8388608, 128, 1024, 1))), ("clone_62", FC)],
     "v7/bfe872e373e4": [("getitem_641", (BF, (1, 32, 8192, 128), (33554432, 128, 4096, 1))), ("clone_63", FC)],
+    "v5/ca76bd89ec38": [("arg586_1", POS), ("arg582_1", TAB), ("mm_217", MM), ("mm_218", MM1)],
+    "v4/6b92d6e665ab": [("arg586_1", POS), ("arg582_1", TAB), ("mm_217", MM), ("mm_218", MM1)],
+    "v6/03d64c25b654": [("_conj_62", FC), ("getitem_642", GK)],
+    "v6/dc55b25cdcb2": [("_conj_63", FC), ("getitem_641", GQ)],
+    "v5/a1bb72d946b0": [("_conj_62", FC), ("_conj_63", FC), ("getitem_641", GQ), ("getitem_642", GK),
+                        ("getitem_643", GK)],
+    "v4/a1318bc813d2": [("_conj_62", FC), ("_conj_63", FC), ("getitem_641", GQ), ("getitem_642", GK),
+                        ("getitem_643", GK)],
     "v8/c68dae22972b": [("mm_4", FFN), ("mm_5", FFN)],
     "v8/385e1beb9bb9": [("mm_662", FFN), ("silu_recomputed", FFN3), ("_unsafe_view_5_recomputed", FFN3),
                         ("_unsafe_view_4_recomputed", FFN3)],
