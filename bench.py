@@ -16,6 +16,8 @@ BASELINE.json configurations:
   c5b  add + RMSNorm backward x, res, dy [16384, 8192]    -> dx bf16, dw fp32
   swf  SwiGLU gate forward    a, b [8192, 14336]          -> bf16(silu(a)) * b        (v8/c68dae22972b)
   swb  SwiGLU gate backward   g, s, b, a [8192, 14336]    -> db, da bf16              (v8/385e1beb9bb9)
+  silu SiLU alone            a [8192, 14336]             -> bf16(silu(a))            (v7/58e7a4d6cde3)
+  swfb SwiGLU fwd recomputed with bwd  a, b, g [8192, 14336] -> h, db, da bf16      (v6/182d2dcd0652)
   c3n  embedding -> RMSNorm  table [128256, 4096], ids [8, 2048] Zipf(1.1) -> y [8, 2048, 4096] in one launch (v8/12545c1e9b06)
   cef  cross-entropy forward  logits [8192, 128256] bf16, targets -> loss, total_weight (v8/71f1d2c9f38b)
   ceb  cross-entropy backward log-softmax [8192, 128256] fp32, targets -> bf16 grad   (v8/622c35f5d1c6)
@@ -359,30 +361,42 @@ class Rope(Workload):
 class SwiGlu(Workload):
     """The feed-forward gate region at its reference shape: forward reads the
     w1 / w3 outputs and writes the gate product; backward reads the product's
-    gradient, silu(w1 out), w3 out, w1 out and writes both branch gradients."""
+    gradient, silu(w1 out), w3 out, w1 out and writes both branch gradients;
+    silu alone reads w1 out and writes its silu; the recomputing backward
+    reads w1 out, w3 out and the gradient and writes the product and both
+    branch gradients."""
 
-    def __init__(self, dev, M=8192, N=14336, backward=False, name="swf"):
+    # mode -> (inputs, outputs, entry point, dominant kernel, description)
+    MODES = {
+        "fwd": (2, 1, "kp_swiglu_fwd_bf16", "swiglu_fwd_vec",
+                "SwiGLU gate forward (v8/c68dae22972b): a, b [{M},{N}] bf16 -> bf16(silu(a)) * b bf16"),
+        "bwd": (4, 2, "kp_swiglu_bwd_bf16", "swiglu_bwd_vec",
+                "SwiGLU gate backward (v8/385e1beb9bb9): g, silu(a), b, a [{M},{N}] bf16 -> "
+                "db = g*silu(a), da = silu_backward(g*b, a) bf16"),
+        "silu": (1, 1, "kp_silu_bf16", "silu_vec", "SiLU (v7/58e7a4d6cde3): a [{M},{N}] bf16 -> silu(a) bf16"),
+        "fwdbwd": (3, 3, "kp_swiglu_fwd_bwd_bf16", "swiglu_fwd_bwd_vec",
+                   "SwiGLU gate forward recomputed with its backward (v6/182d2dcd0652): a, b, g [{M},{N}] bf16 -> "
+                   "h = silu(a)*b, db = g*silu(a), da = silu_backward(g*b, a) bf16"),
+    }
+
+    def __init__(self, dev, M=8192, N=14336, mode="fwd", name="swf"):
         super().__init__(dev)
         import torch
         from kernelproblems_amd import _lib as L
         self.name = name
-        self.backward = backward
+        self.mode = mode
         g = _gen(0)
-        n_in, n_out = (4, 2) if backward else (2, 1)
+        n_in, n_out, entry, kernel, desc = self.MODES[mode]
         self.ops = [_randn((M, N), g) for _ in range(n_in)]
         self.bytes_per_call = (n_in + n_out) * M * N * 2
         self.dominant_bytes = self.bytes_per_call
-        self.dominant_kernel = "swiglu_bwd_vec" if backward else "swiglu_fwd_vec"
+        self.dominant_kernel = kernel
         self.probe_mix = (n_in, n_out, M * N * 2, M * N * 2,
-                          f"{n_in} reads + {n_out} write(s) of {M * N * 2 / 1e6:.1f} MB")
-        if backward:
-            self.description = (f"SwiGLU gate backward (v8/385e1beb9bb9): g, silu(a), b, a [{M},{N}] bf16 -> "
-                                f"db = g*silu(a), da = silu_backward(g*b, a) bf16")
-        else:
-            self.description = f"SwiGLU gate forward (v8/c68dae22972b): a, b [{M},{N}] bf16 -> bf16(silu(a)) * b bf16"
+                          f"{n_in} read(s) + {n_out} write(s) of {M * N * 2 / 1e6:.1f} MB")
+        self.description = desc.format(M=M, N=N)
         R = self.rotations(self.bytes_per_call)
         dev_ops = [t.to(dev) for t in self.ops]
-        fn = L.lib().kp_swiglu_bwd_bf16 if backward else L.lib().kp_swiglu_fwd_bf16
+        fn = getattr(L.lib(), entry)
         stream = torch.cuda.current_stream(dev).cuda_stream
         for r in range(R):
             ins = [t if r == 0 else t.clone() for t in dev_ops]
@@ -396,10 +410,8 @@ class SwiGlu(Workload):
 
     def cpu_run(self):
         from oracle import torch_ref
-        if self.backward:
-            torch_ref.swiglu_bwd(*self.ops)
-        else:
-            torch_ref.swiglu_fwd(*self.ops)
+        {"fwd": torch_ref.swiglu_fwd, "bwd": torch_ref.swiglu_bwd, "silu": torch_ref.silu,
+         "fwdbwd": torch_ref.swiglu_fwd_bwd}[self.mode](*self.ops)
 
 
 # ------------------------------------------------------------------ cross-entropy
@@ -489,7 +501,11 @@ def make_workload(name, dev):
     if name == "swf":
         return SwiGlu(dev, name="swf")
     if name == "swb":
-        return SwiGlu(dev, backward=True, name="swb")
+        return SwiGlu(dev, mode="bwd", name="swb")
+    if name == "silu":
+        return SwiGlu(dev, mode="silu", name="silu")
+    if name == "swfb":
+        return SwiGlu(dev, mode="fwdbwd", name="swfb")
     if name == "cef":
         return CrossEntropy(dev, name="cef")
     if name == "ceb":
@@ -497,7 +513,7 @@ def make_workload(name, dev):
     raise SystemExit(f"unknown workload {name!r}")
 
 
-ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c5f", "c5b", "swf", "swb", "cef", "ceb"]
+ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb"]
 
 
 # ------------------------------------------------------------------ measure

@@ -58,7 +58,7 @@ const char* kp_last_error_message(void);
  * kp_embedding_rmsnorm_fwd_bf16), the gather kernel
  * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
  * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16, the
- * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16, the row kernel of
+ * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16 / kp_silu_bf16 / kp_swiglu_fwd_bwd_bf16, the row kernel of
  * kp_cross_entropy_fwd_bf16, the kernel of kp_cross_entropy_bwd_bf16 and
  * the kernel of kp_stream_probe.
  * Pass NULL, NULL to clear.  Per calling thread. */
@@ -151,7 +151,7 @@ int kp_embedding_rmsnorm_fwd_bf16(const void* table, int64_t V, int64_t table_ro
 /* ------------------------------------------------------------------------
  * Streaming-ceiling probe (a measurement aid; no counterpart in the
  * reference).  Reads n_in (0..4) arrays of in_bytes each and writes n_out
- * (1..2) arrays of out_bytes each (sizes multiples of 16, arrays 16-byte
+ * (1..2; or 3 with n_in = 3) arrays of out_bytes each (sizes multiples of 16, arrays 16-byte
  * aligned) with the fragment kernels' access form: 16-byte non-temporal
  * loads and stores, 1 KiB per wave instruction, one-shot grid of 256-thread
  * blocks holding chunks_per_thread (1 or 4) chunks per thread per array.
@@ -286,6 +286,35 @@ int kp_swiglu_bwd_bf16(const void* g, int64_t g_stride, const void* s, int64_t s
                        const void* b, int64_t b_stride, const void* a, int64_t a_stride,
                        void* db, int64_t db_stride, void* da, int64_t da_stride,
                        int64_t M, int64_t N, void* stream);
+
+/* ------------------------------------------------------------------------
+ * SiLU alone: out = bf16(silu(a)), silu(x) = x / (1 + exp(-x)) in fp32.
+ *
+ * Replaces silu.default at v7/58e7a4d6cde3/problem.py:10-19 (a = w1 output
+ * mm_221, bf16 [8192, 14336]).  a, out: bf16 [M, N], unit inner stride, row
+ * strides in elements.  Same bits as torch's eager bf16 silu.
+ */
+int kp_silu_bf16(const void* a, int64_t a_stride, void* out, int64_t out_stride, int64_t M, int64_t N, void* stream);
+
+/* ------------------------------------------------------------------------
+ * SwiGLU gate forward recomputed together with its backward, s = bf16(silu(a))
+ * kept in registers:
+ *   h  = bf16(s * b)
+ *   db = bf16(g * s)
+ *   da = bf16(t * sig * (1 + a * (1 - sig))),  t = bf16(g * b),  sig = 1 / (1 + exp(-a))
+ *
+ * Replaces the silu -> mul -> mul -> mul -> silu_backward region at
+ * v6/182d2dcd0652/problem.py:10-46 (also v5/441b7bf23822/problem.py:10-48 and
+ * v4/c72358b8111e/problem.py:10-48): a = mm_4 (w1 output), b = mm_5 (w3
+ * output), g = mm_662 (gradient of the gate product); h, db, da are the
+ * fragment's three outputs in order.  3 reads and 3 writes per element where
+ * kp_swiglu_fwd_bf16 + kp_swiglu_bwd_bf16 with a stored s take 3 + 6.
+ * All arrays bf16 [M, N], unit inner stride, row strides in elements.
+ */
+int kp_swiglu_fwd_bwd_bf16(const void* a, int64_t a_stride, const void* b, int64_t b_stride,
+                           const void* g, int64_t g_stride, void* h, int64_t h_stride,
+                           void* db, int64_t db_stride, void* da, int64_t da_stride,
+                           int64_t M, int64_t N, void* stream);
 
 /* ------------------------------------------------------------------------
  * Cross-entropy forward over a vocabulary, sum reduction:

@@ -25,8 +25,10 @@ from .fused import (
     rms_norm_backward,
     rope,
     set_index_checking,
+    silu,
     swiglu,
     swiglu_backward,
+    swiglu_forward_backward,
     unshard,
 )
 
@@ -45,8 +47,10 @@ __all__ = [
     "rms_norm_backward",
     "rope",
     "set_index_checking",
+    "silu",
     "swiglu",
     "swiglu_backward",
+    "swiglu_forward_backward",
     "unshard",
     "version",
 ]

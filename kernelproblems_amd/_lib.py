@@ -89,6 +89,8 @@ SIGNATURES = {
                                             vp, vp]),
     "kp_swiglu_fwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, i64, i64, vp]),
     "kp_swiglu_bwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, vp]),
+    "kp_silu_bf16": (i32, [vp, i64, vp, i64, i64, i64, vp]),
+    "kp_swiglu_fwd_bwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, vp]),
     "kp_cross_entropy_fwd_workspace_size": (sz, [i64]),
     "kp_cross_entropy_fwd_bf16": (i32, [vp, i64, i64, i64, vp, i32, i64, f32, vp, vp, vp, vp, vp, sz, vp]),
     "kp_cross_entropy_bwd_bf16": (i32, [vp, i64, vp, i32, i64, f32, vp, i64, i64, i64, vp, vp]),

@@ -21,7 +21,7 @@ constexpr int kThreads = 256;
 
 struct ProbeArgs {
   const u32x4* in[4];
-  u32x4* out[2];
+  u32x4* out[3];
   int64_t in_chunks, out_chunks;  // 16-byte chunks per input / per output array
 };
 
@@ -63,6 +63,7 @@ ProbeKernel probe_kernel_u(int nr, int nw) {
     case 32: return stream_probe<3, 2, U>;
     case 41: return stream_probe<4, 1, U>;
     case 42: return stream_probe<4, 2, U>;
+    case 33: return stream_probe<3, 3, U>;
   }
   return nullptr;
 }
@@ -81,8 +82,8 @@ extern "C" {
 int kp_stream_probe(const void* const* in, int n_in, int64_t in_bytes, void* const* out, int n_out,
                     int64_t out_bytes, int chunks_per_thread, void* stream) {
   static const char* who = "kp_stream_probe";
-  if (n_in < 0 || n_in > 4 || n_out < 1 || n_out > 2)
-    return fail(KP_EINVAL, "%s: needs 0..4 input and 1..2 output arrays", who);
+  if (n_in < 0 || n_in > 4 || n_out < 1 || n_out > 3 || (n_out == 3 && n_in != 3))
+    return fail(KP_EINVAL, "%s: needs 0..4 input and 1..2 output arrays, or 3 and 3", who);
   if (in_bytes < 0 || out_bytes < 0 || (in_bytes & 15) != 0 || (out_bytes & 15) != 0)
     return fail(KP_EINVAL, "%s: array sizes must be non-negative multiples of 16 bytes", who);
   if (n_in > 0 && (in == nullptr)) return fail(KP_EINVAL, "%s: input pointer list is NULL", who);

@@ -4,6 +4,9 @@
 //   forward   out = bf16( bf16(silu(a)) * b )                    (2 reads, 1 write)
 //   backward  db  = bf16( g * s )                                 (4 reads, 2 writes)
 //             da  = bf16( silu'(a) applied to bf16(g * b) )
+//   silu      out = bf16( silu(a) )                               (1 read, 1 write)
+//   forward recomputed with the backward (s = bf16(silu(a)) never stored):
+//             h = bf16(s * b), db = bf16(g * s), da as above      (3 reads, 3 writes)
 //
 // with silu(x) = x / (1 + exp(-x)) and silu_backward(t, x) =
 // t * sig * (1 + x * (1 - sig)), sig = 1 / (1 + exp(-x)), all in fp32 with the
@@ -68,29 +71,50 @@ __device__ __forceinline__ float silu_bf16(float x) {
   return round_bf(q);
 }
 
-__device__ __forceinline__ u32x4 fwd8(const u32x4& a, const u32x4& b) {
-  float af[8], bf[8], o[8];
-  unpack8(a, af);
-  unpack8(b, bf);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) o[i] = silu_bf16(af[i]) * bf[i];
-  return pack8(o);
+enum Op : int { kFwd = 0, kBwd = 1, kSilu = 2, kFwdBwd = 3 };
+
+// Inputs and outputs of each op, in argument order:
+//   kFwd (a, b) -> out;  kBwd (g, s, b, a) -> (db, da);  kSilu (a) -> out;
+//   kFwdBwd (a, b, g) -> (h, db, da).
+constexpr int n_in(int op) { return op == kFwd ? 2 : op == kBwd ? 4 : op == kSilu ? 1 : 3; }
+constexpr int n_out(int op) { return op == kFwd ? 1 : op == kBwd ? 2 : op == kSilu ? 1 : 3; }
+
+// One element: x[i] are the inputs as fp32 (bf16 values), y[o] the fp32
+// results before their bf16 rounding.
+template <int OP>
+__device__ __forceinline__ void apply1(const float* x, float* y) {
+  if constexpr (OP == kFwd) {
+    y[0] = silu_bf16(x[0]) * x[1];
+  } else if constexpr (OP == kBwd) {
+    y[0] = x[0] * x[1];
+    y[1] = silu_bwd_f(round_bf(x[0] * x[2]), x[3]);
+  } else if constexpr (OP == kSilu) {
+    y[0] = silu_bf16(x[0]);
+  } else {
+    const float sv = silu_bf16(x[0]);
+    y[0] = sv * x[1];
+    y[1] = x[2] * sv;
+    y[2] = silu_bwd_f(round_bf(x[2] * x[1]), x[0]);
+  }
 }
 
-__device__ __forceinline__ void bwd8(const u32x4& g, const u32x4& s, const u32x4& b, const u32x4& a, u32x4& db,
-                                     u32x4& da) {
-  float gf[8], sf[8], bf[8], af[8], o0[8], o1[8];
-  unpack8(g, gf);
-  unpack8(s, sf);
-  unpack8(b, bf);
-  unpack8(a, af);
+template <int OP>
+__device__ __forceinline__ void apply8(const u32x4* in, u32x4* out) {
+  constexpr int NI = n_in(OP), NO = n_out(OP);
+  float x[NI][8], y[NO][8];
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    o0[i] = gf[i] * sf[i];
-    o1[i] = silu_bwd_f(round_bf(gf[i] * bf[i]), af[i]);
+  for (int i = 0; i < NI; ++i) unpack8(in[i], x[i]);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    float xe[NI], ye[NO];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) xe[i] = x[i][e];
+    apply1<OP>(xe, ye);
+#pragma unroll
+    for (int o = 0; o < NO; ++o) y[o][e] = ye[o];
   }
-  db = pack8(o0);
-  da = pack8(o1);
+#pragma unroll
+  for (int o = 0; o < NO; ++o) out[o] = pack8(y[o]);
 }
 
 // ------------------------------------------------------------------ 16-byte path
@@ -98,8 +122,8 @@ __device__ __forceinline__ void bwd8(const u32x4& g, const u32x4& s, const u32x4
 // chunks).  Block b covers row b / bpr, chunks [(b % bpr) * kBlockChunks, +kBlockChunks).
 struct VecArgs {
   const u32x4* in[4];
-  u32x4* out[2];
-  int64_t in_rs[4], out_rs[2];  // row strides in chunks
+  u32x4* out[3];
+  int64_t in_rs[4], out_rs[3];  // row strides in chunks
   int64_t cpr;                  // chunks per row
   int bpr;                      // blocks per row
 };
@@ -111,55 +135,32 @@ __device__ __forceinline__ int64_t chunk_of(const VecArgs& a, int u, int64_t c0,
   return ok ? c : 0;
 }
 
-template <bool FULL>
-__device__ __forceinline__ void fwd_tile(const VecArgs& a, int64_t row, int64_t c0) {
-  const u32x4* pa = a.in[0] + row * a.in_rs[0];
-  const u32x4* pb = a.in[1] + row * a.in_rs[1];
-  u32x4* po = a.out[0] + row * a.out_rs[0];
-  u32x4 va[kPer], vb[kPer];
+template <int OP, bool FULL>
+__device__ __forceinline__ void tile(const VecArgs& a, int64_t row, int64_t c0) {
+  constexpr int NI = n_in(OP), NO = n_out(OP);
+  u32x4 v[NI][kPer];
   int64_t c[kPer];
   bool ok[kPer];
 #pragma unroll
   for (int u = 0; u < kPer; ++u) c[u] = chunk_of<FULL>(a, u, c0, ok[u]);
 #pragma unroll
-  for (int u = 0; u < kPer; ++u) va[u] = ld16_stream(pa + c[u]);
+  for (int i = 0; i < NI; ++i) {
+    const u32x4* p = a.in[i] + row * a.in_rs[i];
 #pragma unroll
-  for (int u = 0; u < kPer; ++u) vb[u] = ld16_stream(pb + c[u]);
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) {
-    const u32x4 r = fwd8(va[u], vb[u]);
-    if (ok[u]) st16_stream(po + c[u], r);
+    for (int u = 0; u < kPer; ++u) v[i][u] = ld16_stream(p + c[u]);
   }
-}
-
-template <bool FULL>
-__device__ __forceinline__ void bwd_tile(const VecArgs& a, int64_t row, int64_t c0) {
-  const u32x4* pg = a.in[0] + row * a.in_rs[0];
-  const u32x4* ps = a.in[1] + row * a.in_rs[1];
-  const u32x4* pb = a.in[2] + row * a.in_rs[2];
-  const u32x4* pa = a.in[3] + row * a.in_rs[3];
-  u32x4* pdb = a.out[0] + row * a.out_rs[0];
-  u32x4* pda = a.out[1] + row * a.out_rs[1];
-  u32x4 vg[kPer], vs[kPer], vb[kPer], va[kPer];
-  int64_t c[kPer];
-  bool ok[kPer];
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) c[u] = chunk_of<FULL>(a, u, c0, ok[u]);
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) vg[u] = ld16_stream(pg + c[u]);
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) vs[u] = ld16_stream(ps + c[u]);
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) vb[u] = ld16_stream(pb + c[u]);
-#pragma unroll
-  for (int u = 0; u < kPer; ++u) va[u] = ld16_stream(pa + c[u]);
+  // Every load of the tile is in flight before the first use: without this
+  // fence the scheduler starts the math of chunk 0 after a few loads.
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int u = 0; u < kPer; ++u) {
-    u32x4 db, da;
-    bwd8(vg[u], vs[u], vb[u], va[u], db, da);
+    u32x4 in[NI], r[NO];
+#pragma unroll
+    for (int i = 0; i < NI; ++i) in[i] = v[i][u];
+    apply8<OP>(in, r);
     if (ok[u]) {
-      st16_stream(pdb + c[u], db);
-      st16_stream(pda + c[u], da);
+#pragma unroll
+      for (int o = 0; o < NO; ++o) st16_stream(a.out[o] + row * a.out_rs[o] + c[u], r[o]);
     }
   }
 }
@@ -167,56 +168,71 @@ __device__ __forceinline__ void bwd_tile(const VecArgs& a, int64_t row, int64_t 
 // Loads of a partial tile are clamped to chunk 0 of the row (always in
 // bounds) rather than predicated, so the load batch issues unbranched; only
 // the stores are predicated.
-__global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(VecArgs a) {
+template <int OP>
+__device__ __forceinline__ void vec_body(const VecArgs& a) {
   const int row = (int)blockIdx.x / a.bpr;
   const int64_t c0 = (int64_t)((int)blockIdx.x - row * a.bpr) * kBlockChunks;
-  if (c0 + kBlockChunks <= a.cpr) fwd_tile<true>(a, row, c0);
-  else fwd_tile<false>(a, row, c0);
+  if (c0 + kBlockChunks <= a.cpr) tile<OP, true>(a, row, c0);
+  else tile<OP, false>(a, row, c0);
 }
 
-__global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(VecArgs a) {
-  const int row = (int)blockIdx.x / a.bpr;
-  const int64_t c0 = (int64_t)((int)blockIdx.x - row * a.bpr) * kBlockChunks;
-  if (c0 + kBlockChunks <= a.cpr) bwd_tile<true>(a, row, c0);
-  else bwd_tile<false>(a, row, c0);
-}
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_vec(VecArgs a) { vec_body<kFwd>(a); }
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_vec(VecArgs a) { vec_body<kBwd>(a); }
+__global__ __launch_bounds__(kThreads) void silu_vec(VecArgs a) { vec_body<kSilu>(a); }
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_bwd_vec(VecArgs a) { vec_body<kFwdBwd>(a); }
 
 // ------------------------------------------------------------------ scalar path
 struct ScalarArgs {
   const uint16_t* in[4];
-  uint16_t* out[2];
-  int64_t in_rs[4], out_rs[2];  // row strides in elements
+  uint16_t* out[3];
+  int64_t in_rs[4], out_rs[3];  // row strides in elements
   int64_t M, N;
 };
 
-__global__ __launch_bounds__(kThreads) void swiglu_fwd_scalar(ScalarArgs a) {
+template <int OP>
+__device__ __forceinline__ void scalar_body(const ScalarArgs& a) {
+  constexpr int NI = n_in(OP), NO = n_out(OP);
   const int64_t total = a.M * a.N;
   for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += (int64_t)gridDim.x * kThreads) {
     const int64_t r = i / a.N, c = i - r * a.N;
-    const float x = bf_to_f(a.in[0][r * a.in_rs[0] + c]);
-    const float b = bf_to_f(a.in[1][r * a.in_rs[1] + c]);
-    a.out[0][r * a.out_rs[0] + c] = f_to_bf(silu_bf16(x) * b);
+    float x[NI], y[NO];
+#pragma unroll
+    for (int k = 0; k < NI; ++k) x[k] = bf_to_f(a.in[k][r * a.in_rs[k] + c]);
+    apply1<OP>(x, y);
+#pragma unroll
+    for (int k = 0; k < NO; ++k) a.out[k][r * a.out_rs[k] + c] = f_to_bf(y[k]);
   }
 }
 
-__global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(ScalarArgs a) {
-  const int64_t total = a.M * a.N;
-  for (int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x; i < total; i += (int64_t)gridDim.x * kThreads) {
-    const int64_t r = i / a.N, c = i - r * a.N;
-    const float g = bf_to_f(a.in[0][r * a.in_rs[0] + c]);
-    const float s = bf_to_f(a.in[1][r * a.in_rs[1] + c]);
-    const float b = bf_to_f(a.in[2][r * a.in_rs[2] + c]);
-    const float x = bf_to_f(a.in[3][r * a.in_rs[3] + c]);
-    a.out[0][r * a.out_rs[0] + c] = f_to_bf(g * s);
-    a.out[1][r * a.out_rs[1] + c] = f_to_bf(silu_bwd_f(round_bf(g * b), x));
-  }
-}
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_scalar(ScalarArgs a) { scalar_body<kFwd>(a); }
+__global__ __launch_bounds__(kThreads) void swiglu_bwd_scalar(ScalarArgs a) { scalar_body<kBwd>(a); }
+__global__ __launch_bounds__(kThreads) void silu_scalar(ScalarArgs a) { scalar_body<kSilu>(a); }
+__global__ __launch_bounds__(kThreads) void swiglu_fwd_bwd_scalar(ScalarArgs a) { scalar_body<kFwdBwd>(a); }
 
 // ------------------------------------------------------------------ host side
 // Validates and launches one pointwise op over nin inputs / nout outputs of an
 // [M, N] bf16 matrix (unit inner stride, row strides in elements).
-int launch_pointwise(const char* who, bool backward, const void* const* in, const int64_t* in_rs, int nin,
-                     void* const* out, const int64_t* out_rs, int nout, int64_t M, int64_t N, hipStream_t stream) {
+const void* vec_kernel(int op) {
+  switch (op) {
+    case kFwd: return reinterpret_cast<const void*>(swiglu_fwd_vec);
+    case kBwd: return reinterpret_cast<const void*>(swiglu_bwd_vec);
+    case kSilu: return reinterpret_cast<const void*>(silu_vec);
+    default: return reinterpret_cast<const void*>(swiglu_fwd_bwd_vec);
+  }
+}
+
+const void* scalar_kernel(int op) {
+  switch (op) {
+    case kFwd: return reinterpret_cast<const void*>(swiglu_fwd_scalar);
+    case kBwd: return reinterpret_cast<const void*>(swiglu_bwd_scalar);
+    case kSilu: return reinterpret_cast<const void*>(silu_scalar);
+    default: return reinterpret_cast<const void*>(swiglu_fwd_bwd_scalar);
+  }
+}
+
+int launch_pointwise(const char* who, int op, const void* const* in, const int64_t* in_rs, void* const* out,
+                     const int64_t* out_rs, int64_t M, int64_t N, hipStream_t stream) {
+  const int nin = n_in(op), nout = n_out(op);
   if (M < 0 || N < 0) return fail(KP_EINVAL, "%s: negative shape [%lld, %lld]", who, (long long)M, (long long)N);
   if (M == 0 || N == 0) return KP_OK;
   for (int i = 0; i < nin; ++i) {
@@ -261,8 +277,7 @@ int launch_pointwise(const char* who, bool backward, const void* const* in, cons
     if (blocks > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: too many blocks for one launch", who);
     a.bpr = (int)bpr;
     void* args[] = {&a};
-    launch_dominant_raw(reinterpret_cast<const void*>(backward ? swiglu_bwd_vec : swiglu_fwd_vec),
-                        dim3((unsigned)blocks), dim3(kThreads), args, 0, stream);
+    launch_dominant_raw(vec_kernel(op), dim3((unsigned)blocks), dim3(kThreads), args, 0, stream);
     return check_launch(who);
   }
   ScalarArgs a{};
@@ -280,8 +295,7 @@ int launch_pointwise(const char* who, bool backward, const void* const* in, cons
   const int64_t cap = (int64_t)cu_count() * 16;
   const unsigned blocks = (unsigned)(want < cap ? want : cap);
   void* args[] = {&a};
-  launch_dominant_raw(reinterpret_cast<const void*>(backward ? swiglu_bwd_scalar : swiglu_fwd_scalar), dim3(blocks),
-                      dim3(kThreads), args, 0, stream);
+  launch_dominant_raw(scalar_kernel(op), dim3(blocks), dim3(kThreads), args, 0, stream);
   return check_launch(who);
 }
 
@@ -298,7 +312,7 @@ int kp_swiglu_fwd_bf16(const void* a, int64_t a_rs, const void* b, int64_t b_rs,
   const int64_t in_rs[2] = {a_rs, b_rs};
   void* outs[1] = {out};
   const int64_t o_rs[1] = {out_rs};
-  return launch_pointwise("kp_swiglu_fwd_bf16", false, in, in_rs, 2, outs, o_rs, 1, M, N, as_stream(stream));
+  return launch_pointwise("kp_swiglu_fwd_bf16", kFwd, in, in_rs, outs, o_rs, M, N, as_stream(stream));
 }
 
 int kp_swiglu_bwd_bf16(const void* g, int64_t g_rs, const void* s, int64_t s_rs, const void* b, int64_t b_rs,
@@ -308,7 +322,25 @@ int kp_swiglu_bwd_bf16(const void* g, int64_t g_rs, const void* s, int64_t s_rs,
   const int64_t in_rs[4] = {g_rs, s_rs, b_rs, a_rs};
   void* outs[2] = {db, da};
   const int64_t o_rs[2] = {db_rs, da_rs};
-  return launch_pointwise("kp_swiglu_bwd_bf16", true, in, in_rs, 4, outs, o_rs, 2, M, N, as_stream(stream));
+  return launch_pointwise("kp_swiglu_bwd_bf16", kBwd, in, in_rs, outs, o_rs, M, N, as_stream(stream));
+}
+
+int kp_silu_bf16(const void* a, int64_t a_rs, void* out, int64_t out_rs, int64_t M, int64_t N, void* stream) {
+  const void* in[1] = {a};
+  const int64_t in_rs[1] = {a_rs};
+  void* outs[1] = {out};
+  const int64_t o_rs[1] = {out_rs};
+  return launch_pointwise("kp_silu_bf16", kSilu, in, in_rs, outs, o_rs, M, N, as_stream(stream));
+}
+
+int kp_swiglu_fwd_bwd_bf16(const void* a, int64_t a_rs, const void* b, int64_t b_rs, const void* g, int64_t g_rs,
+                           void* h, int64_t h_rs, void* db, int64_t db_rs, void* da, int64_t da_rs, int64_t M,
+                           int64_t N, void* stream) {
+  const void* in[3] = {a, b, g};
+  const int64_t in_rs[3] = {a_rs, b_rs, g_rs};
+  void* outs[3] = {h, db, da};
+  const int64_t o_rs[3] = {h_rs, db_rs, da_rs};
+  return launch_pointwise("kp_swiglu_fwd_bwd_bf16", kFwdBwd, in, in_rs, outs, o_rs, M, N, as_stream(stream));
 }
 
 }  // extern "C"

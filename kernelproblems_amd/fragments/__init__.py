@@ -23,8 +23,9 @@ FRAGMENTS = (
     "v7/e29b92927600", "v8/493cad38cac9", "v8/c8c60d8f7015", "v8/97032595d968", "v7/0f38bc55457c",
     "v7/5c65f62b0422", "v7/bfe872e373e4", "v5/ca76bd89ec38", "v4/6b92d6e665ab", "v6/03d64c25b654",
     "v6/dc55b25cdcb2", "v5/a1bb72d946b0", "v4/a1318bc813d2",
-    # SwiGLU gate forward / backward
-    "v8/c68dae22972b", "v8/385e1beb9bb9",
+    # SwiGLU gate forward / backward (+ silu alone, forward recomputed with the backward)
+    "v8/c68dae22972b", "v8/385e1beb9bb9", "v7/58e7a4d6cde3", "v4/65b4b565ed67", "v6/182d2dcd0652",
+    "v5/441b7bf23822", "v4/c72358b8111e",
     # token cross-entropy forward / backward
     "v8/71f1d2c9f38b", "v8/622c35f5d1c6",
     # chain: RMSNorm forward -> backward (+ gradient adds, residual) -> embedding backward

@@ -526,6 +526,31 @@ def swiglu_backward(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.
     return db, da
 
 
+def silu(a: torch.Tensor) -> torch.Tensor:
+    """bf16(silu(a)) alone (v7/58e7a4d6cde3/problem.py:10-19), the same bits as
+    eager's bf16 silu.  Returns a contiguous tensor of a's shape."""
+    (ra,), n = _same_rows("silu", [a])
+    out = torch.empty(a.shape, dtype=torch.bfloat16, device=a.device)
+    m = ra[2]
+    if m:
+        L.call("kp_silu_bf16", ra[0].data_ptr(), ra[1], out.data_ptr(), n, m, n, _stream(a.device))
+    return out
+
+
+def swiglu_forward_backward(a: torch.Tensor, b: torch.Tensor, g: torch.Tensor):
+    """The SwiGLU gate forward recomputed with its backward in one pass
+    (v6/182d2dcd0652/problem.py:10-46): with s = bf16(silu(a)) kept in
+    registers, h = bf16(s * b), db = bf16(g * s) and
+    da = silu_backward(bf16(g * b), a).  Returns contiguous (h, db, da)."""
+    (ra, rb, rg), n = _same_rows("swiglu_forward_backward", [a, b, g])
+    h, db, da = (torch.empty(a.shape, dtype=torch.bfloat16, device=a.device) for _ in range(3))
+    m = ra[2]
+    if m:
+        L.call("kp_swiglu_fwd_bwd_bf16", ra[0].data_ptr(), ra[1], rb[0].data_ptr(), rb[1], rg[0].data_ptr(), rg[1],
+               h.data_ptr(), n, db.data_ptr(), n, da.data_ptr(), n, m, n, _stream(a.device))
+    return h, db, da
+
+
 # ---------------------------------------------------------------- cross-entropy
 def _targets(targets: torch.Tensor, M: int, device: torch.device):
     if not isinstance(targets, torch.Tensor) or targets.device != device:

@@ -37,6 +37,8 @@ swiglu_fwd             torch CPU eager ``silu`` * b, fp64 ``x * expit(x)``
 swiglu_bwd             torch CPU eager ``mul`` / ``silu_backward``, central
                        finite differences of fp64 silu, closed forms
                        (silu'(0) = 1/2, the zero of silu' near -1.2785).
+silu, swiglu_fwd_bwd   compositions of swiglu_fwd / swiglu_bwd; silu also
+                       against torch CPU eager ``silu`` over every bf16 value.
 cross_entropy_fwd      torch fp64 ``log_softmax`` + ``nll_loss`` (sum,
                        ignore_index), closed forms (uniform row: log V,
                        dominant logit: 0), shift invariance, ignored rows.
@@ -283,6 +285,21 @@ def swiglu_bwd(g: np.ndarray, s: np.ndarray, b: np.ndarray, a: np.ndarray):
     db, da = np.empty_like(arrs[0]), np.empty_like(arrs[0])
     lib().kpo_swiglu_bwd(*(_p(t) for t in arrs), _p(db), _p(da), arrs[0].size)
     return db, da
+
+
+def silu(a: np.ndarray) -> np.ndarray:
+    """bf16(silu(a)) (v7/58e7a4d6cde3/problem.py:10-19): swiglu_fwd with b = 1,
+    since bf16(s * 1) = s for a bf16 s."""
+    a = _c(a, np.uint16)
+    return swiglu_fwd(a, np.full_like(a, 0x3F80))
+
+
+def swiglu_fwd_bwd(a: np.ndarray, b: np.ndarray, g: np.ndarray):
+    """(h, db, da) of v6/182d2dcd0652/problem.py:10-46: h = swiglu_fwd(a, b) and
+    swiglu_bwd(g, silu(a), b, a), the two restated ops composed."""
+    h = swiglu_fwd(a, b)
+    db, da = swiglu_bwd(g, silu(a), b, a)
+    return h, db, da
 
 
 # ---------------------------------------------------------------- cross-entropy

@@ -212,6 +212,23 @@ def _swiglu_bwd(g, s, b, a):             # v8/385e1beb9bb9/problem.py:17-33
     return db, aten.view.default(da, list(g.shape))
 
 
+def _silu_only(mm):                     # v7/58e7a4d6cde3/problem.py:14-19
+    return aten.silu.default(aten._unsafe_view.default(mm, [1, *mm.shape]))
+
+
+def _swiglu_fwd_bwd(transposed):        # v6/182d2dcd0652/problem.py:16-46, v5/441b7bf23822:16-48
+    def f(mm4, mm5, g):
+        a = aten._unsafe_view.default(mm4, [1, *mm4.shape])
+        s = aten.silu.default(a)
+        b = aten._unsafe_view.default(mm5, [1, *mm5.shape])
+        h = aten.view.default(aten.mul.Tensor(s, b), list(mm4.shape))
+        gv = aten.view.default(g, [1, *g.shape])
+        db = aten.view.default(aten.mul.Tensor(gv, s), list(g.shape))
+        da = aten.view.default(aten.silu_backward.default(aten.mul.Tensor(gv, b), a), list(g.shape))
+        return (h, aten.t.default(db), aten.t.default(da)) if transposed else (h, db, da)
+    return f
+
+
 def _xent_fwd(t, logits):               # v8/71f1d2c9f38b/problem.py:15-40
     tv = aten.view.default(t, [t.numel()])
     x = aten.view.default(aten._unsafe_view.default(logits, [1, *logits.shape]), list(logits.shape))
@@ -294,6 +311,11 @@ _FRAGMENTS = {
     "v4/a1318bc813d2": _rope_bwd_qkv,
     "v8/c68dae22972b": _swiglu_fwd,
     "v8/385e1beb9bb9": _swiglu_bwd,
+    "v7/58e7a4d6cde3": _silu_only,
+    "v4/65b4b565ed67": _swiglu_fwd,
+    "v6/182d2dcd0652": _swiglu_fwd_bwd(False),
+    "v5/441b7bf23822": _swiglu_fwd_bwd(True),
+    "v4/c72358b8111e": _swiglu_fwd_bwd(True),
     "v8/71f1d2c9f38b": _xent_fwd,
     "v8/622c35f5d1c6": _xent_bwd,
     "v6/0b493aad68f0": _norm_emb_bwd_chain,

@@ -107,6 +107,18 @@ def swiglu_bwd(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.Tenso
     return aten.mul.Tensor(g, s), aten.silu_backward.default(aten.mul.Tensor(g, b), a)
 
 
+def silu(a: torch.Tensor):
+    """v7/58e7a4d6cde3/problem.py:10-19: silu.default."""
+    return aten.silu.default(a)
+
+
+def swiglu_fwd_bwd(a: torch.Tensor, b: torch.Tensor, g: torch.Tensor):
+    """v6/182d2dcd0652/problem.py:10-46: s = silu(a); (mul(s, b), mul(g, s),
+    silu_backward(mul(g, b), a))."""
+    s = aten.silu.default(a)
+    return aten.mul.Tensor(s, b), aten.mul.Tensor(g, s), aten.silu_backward.default(aten.mul.Tensor(g, b), a)
+
+
 def cross_entropy_fwd(logits: torch.Tensor, targets: torch.Tensor, scale: float):
     """v8/71f1d2c9f38b/problem.py:15-40: _to_copy(f32) -> _log_softmax ->
     nll_loss_forward(sum, ignore_index=-100) -> div."""

@@ -119,6 +119,17 @@ def test_swiglu_validation(lib):
     _expect(lib, L.KP_EINVAL, "kp_swiglu_bwd_bf16", 16, 8, 32, 8, 48, 8, 64, 7, 80, 8, 96, 8, 2, 8, None)
 
 
+def test_silu_and_fwd_bwd_validation(lib):
+    _expect(lib, L.KP_EINVAL, "kp_silu_bf16", None, 8, 32, 8, 2, 8, None)  # NULL a
+    _expect(lib, L.KP_EINVAL, "kp_silu_bf16", 16, 8, 32, 7, 2, 8, None)    # out rows overlap
+    assert lib.kp_silu_bf16(None, 8, None, 8, 0, 8, None) == L.KP_OK
+    fb = "kp_swiglu_fwd_bwd_bf16"
+    _expect(lib, L.KP_EINVAL, fb, 16, 8, 32, 8, 48, 8, 64, 8, None, 8, 96, 8, 2, 8, None)  # NULL db
+    _expect(lib, L.KP_EINVAL, fb, 16, 8, 32, 8, None, 8, 64, 8, 80, 8, 96, 8, 2, 8, None)  # NULL g
+    _expect(lib, L.KP_EINVAL, fb, 16, 8, 32, 8, 48, 8, 64, 8, 80, 8, 96, 8, -2, 8, None)  # negative M
+    assert lib.kp_swiglu_fwd_bwd_bf16(None, 8, None, 8, None, 8, None, 8, None, 8, None, 8, 0, 8, None) == L.KP_OK
+
+
 def test_cross_entropy_validation(lib):
     ws = int(lib.kp_cross_entropy_fwd_workspace_size(4))
     assert ws >= 4 * 12
@@ -148,6 +159,7 @@ def test_embedding_rmsnorm_validation(lib):
 def test_stream_probe_validation(lib):
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 5, 64, L.ptr_array([32]), 1, 64, 4, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, 4, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16, 16]), 2, 64, L.ptr_array([32, 32, 32]), 3, 64, 4, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 60, L.ptr_array([32]), 1, 64, 4, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, 4, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 1, 64, 2, None)

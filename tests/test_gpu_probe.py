@@ -9,6 +9,7 @@ pytestmark = pytest.mark.gpu
 
 @pytest.mark.parametrize("per_thread", [1, 4])
 @pytest.mark.parametrize("n_in,n_out,in_b,out_b", [(2, 1, 1 << 16, 1 << 16), (3, 2, 48, 48), (4, 2, 1 << 15, 1 << 15), (1, 1, 4096, 65536),
+                                                   (3, 3, 1 << 16, 1 << 16),
                                                    (0, 2, 0, 20000 * 16)])
 def test_stream_probe_outputs(gpu, n_in, n_out, in_b, out_b, per_thread):
     g = torch.Generator().manual_seed(n_in * 10 + n_out)

@@ -132,3 +132,63 @@ def test_bitwise_with_torch_eager(gpu, shape):
     sl = (slice(0, 2),) + (slice(None),) * (len(shape) - 1)
     exp = oracle.swiglu_fwd(to_u16(a[sl]), to_u16(b[sl]))
     assert_bf16_close(to_u16(kp.swiglu(a[sl], b[sl])), exp, rtol=BF16_RTOL, atol=BF16_ATOL, what="slice")
+
+
+@pytest.mark.parametrize("path", ["vector", "scalar"])
+def test_silu_every_bf16_value_bitwise(gpu, path):
+    """kp.silu (v7/58e7a4d6cde3) over all 65536 bf16 patterns against torch's
+    eager silu, bit for bit (NaN payloads aside)."""
+    a = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).to(gpu).view(64, 1024)
+    if path == "scalar":
+        base = torch.empty((64, 1026), dtype=torch.bfloat16, device=gpu)
+        base[:, 2:] = a
+        a = base[:, 2:]
+    out = kp.silu(a)
+    ref = torch.nn.functional.silu(a).contiguous()
+    same = (out.view(torch.int16) == ref.view(torch.int16)) | (torch.isnan(out) & torch.isnan(ref))
+    bad = (~same).flatten().nonzero().flatten().tolist()
+    assert not bad, f"{len(bad)} values differ, e.g. a={a.flatten()[bad[:5]].tolist()}"
+
+
+@pytest.mark.parametrize("kind,M,N", CASES)
+def test_fwd_bwd_matches_oracle(gpu, kind, M, N):
+    """kp.swiglu_forward_backward (v6/182d2dcd0652) against the oracle's
+    composition of the restated forward and backward."""
+    print(f"[swiglu fwd+bwd] {kind} [{M},{N}]", flush=True)
+    g = torch.Generator().manual_seed(M * 13 + N)
+    a, b, gr = _views(kind, M, N, g, gpu, 3)
+    h, db, da = kp.swiglu_forward_backward(a, b, gr)
+    torch.cuda.synchronize()
+    eh, edb, eda = oracle.swiglu_fwd_bwd(to_u16(a), to_u16(b), to_u16(gr))
+    assert_bf16_close(to_u16(h), eh, what="h", max_ulp=1, min_exact=0.999)
+    # db = bf16(g * s): s is one rounding of silu, within 1 ulp of the oracle's
+    assert_bf16_close(to_u16(db), edb, what="db", max_ulp=1, min_exact=0.999)
+    t = np.abs((gr.float() * b.float()).cpu().numpy())
+    assert_bf16_close(to_u16(da), eda, what="da", max_ulp=1, min_exact=0.999,
+                      ulp_abs_slack=float(t.max()) * 2.0**-21)
+
+
+@pytest.mark.parametrize("shape", [(8192, 14336), (3, 1000, 77)])
+def test_fwd_bwd_bitwise_with_torch_eager(gpu, shape):
+    """silu is bit-identical to eager's (exhaustive test), and the products
+    and silu_backward use eager's fp32 operations: all three outputs equal
+    eager's bit for bit; silu alone too."""
+    print(f"[swiglu fwd+bwd eager] {shape}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(22)
+    a, b, gr = (torch.randn(shape, dtype=torch.bfloat16, device=gpu, generator=g) * 3 for _ in range(3))
+    s = torch.nn.functional.silu(a)
+    h, db, da = kp.swiglu_forward_backward(a, b, gr)
+    assert torch.equal(h, s * b)
+    assert torch.equal(db, gr * s)
+    assert torch.equal(da, torch.ops.aten.silu_backward(gr * b, a))
+    del h, db, da
+    assert torch.equal(kp.silu(a), s)
+
+
+def test_fwd_bwd_empty_and_errors(gpu):
+    e = torch.empty((0, 64), dtype=torch.bfloat16, device=gpu)
+    assert all(t.shape == (0, 64) for t in kp.swiglu_forward_backward(e, e, e))
+    assert kp.silu(e).shape == (0, 64)
+    a = torch.randn(4, 16, dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(RuntimeError):
+        kp.swiglu_forward_backward(a, a, a[:, :8])

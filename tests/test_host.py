@@ -67,6 +67,11 @@ SIGNATURES = {
     "v8/c68dae22972b": [("mm_4", FFN), ("mm_5", FFN)],
     "v8/385e1beb9bb9": [("mm_662", FFN), ("silu_recomputed", FFN3), ("_unsafe_view_5_recomputed", FFN3),
                         ("_unsafe_view_4_recomputed", FFN3)],
+    "v7/58e7a4d6cde3": [("mm_221", FFN)],
+    "v4/65b4b565ed67": [("mm_221", FFN), ("mm_222", FFN)],
+    "v6/182d2dcd0652": [("mm_4", FFN), ("mm_5", FFN), ("mm_662", FFN)],
+    "v5/441b7bf23822": [("mm_4", FFN), ("mm_5", FFN), ("mm_662", FFN)],
+    "v4/c72358b8111e": [("mm_4", FFN), ("mm_5", FFN), ("mm_662", FFN)],
     "v8/71f1d2c9f38b": [("arg584_1", IDS), ("mm_224", (BF, (8192, 128256), (128256, 1)))],
     "v6/0b493aad68f0": [("embedding", X), ("_unsafe_view_432", W), ("mm_670", MM), ("mm_672", MM), ("mm_674", MM),
                         ("add_220", X), ("arg583_1", IDS)],

@@ -158,3 +158,36 @@ def test_shapes_and_empty(shape):
     assert db.shape == da.shape == tuple(shape)
     with pytest.raises(ValueError):
         oracle.swiglu_fwd(to_u16(a), np.zeros((5,), np.uint16))
+
+
+def test_silu_every_bf16_value_matches_torch_cpu_eager():
+    """oracle.silu (v7/58e7a4d6cde3) over all non-NaN bf16 values against
+    torch's CPU bf16 silu, to one bf16 ulp (torch's CPU kernel evaluates
+    in fp32 with its own exp).  Below x ~ -88.7 fp32 exp(-x) overflows and
+    eager returns -0 where the fp64 value is a tiny number (< 1e-30)."""
+    a = _all_bf16()
+    out = oracle.silu(a)
+    ref = to_u16(torch.nn.functional.silu(from_u16(a)))
+    with np.errstate(invalid="ignore"):
+        tiny = np.abs(bf(out) - bf(ref)) < 1e-30
+    assert (_same_value(out, ref) | (ulp_bf16(out, ref) <= 1) | tiny).all()
+    differ = ~_same_value(out, ref) & (ulp_bf16(out, ref) > 1)
+    assert (bf(a)[differ] < -88.0).all()
+    assert np.array_equal(out, oracle.swiglu_fwd(a, np.full_like(a, 0x3F80)))
+
+
+def test_swiglu_fwd_bwd_is_the_composition():
+    """(h, db, da) of v6/182d2dcd0652 against torch CPU eager silu / mul /
+    silu_backward with silu materialised in bf16, as the fragment does."""
+    g = gen(13)
+    a, b, gr = (randn_bf16((32, 515), g, std=2.5) for _ in range(3))
+    h, db, da = oracle.swiglu_fwd_bwd(to_u16(a), to_u16(b), to_u16(gr))
+    s = torch.nn.functional.silu(a)
+    assert (ulp_bf16(h, to_u16(s * b)) <= 1).all()
+    assert (ulp_bf16(db, to_u16(gr * s)) <= 1).all()
+    da_ref = to_u16(torch.ops.aten.silu_backward(gr * b, a))
+    u = ulp_bf16(da, da_ref)
+    assert (u <= 1).mean() > 0.999
+    # db uses the bf16-rounded silu, not fp32 silu: a planted fp32 s differs
+    s32 = a.float() * torch.sigmoid(a.float())
+    assert not np.array_equal(db, to_u16((gr.float() * s32).to(torch.bfloat16)))
