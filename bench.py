@@ -21,6 +21,7 @@ BASELINE.json configurations:
   c3n  embedding -> RMSNorm  table [128256, 4096], ids [8, 2048] Zipf(1.1) -> y [8, 2048, 4096] in one launch (v8/12545c1e9b06)
   cef  cross-entropy forward  logits [8192, 128256] bf16, targets -> loss, total_weight (v8/71f1d2c9f38b)
   ceb  cross-entropy backward log-softmax [8192, 128256] fp32, targets -> bf16 grad   (v8/622c35f5d1c6)
+  cefb cross-entropy fwd+bwd  logits [8192, 128256] bf16, targets -> bf16 grad, one pass (v5/fb5b36393cbd)
 
 Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 ~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
@@ -481,6 +482,47 @@ class CrossEntropy(Workload):
             torch_ref.cross_entropy_fwd(self.logits, self.targets, 1.0 / 8192.0)
 
 
+class CrossEntropyFwdBwd(Workload):
+    """The whole loss region from the bf16 logits to their bf16 gradient
+    (v5/fb5b36393cbd) at the reference's shape: each logit read once, each
+    gradient entry written once (the fp32 log-softmax never stored)."""
+
+    def __init__(self, dev, M=8192, V=128256, name="cefb", cpu_rows=1024):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        g = _gen(0)
+        self.targets = torch.randint(0, V, (M,), generator=g)
+        self.targets[::16] = -100
+        td = self.targets.to(dev)
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        self.logits = _randn((M, V), g, 0.0, 2.0)
+        self.bytes_per_call = M * V * 4 + M * 8
+        self.dominant_bytes = M * V * 4 + M * 8
+        self.dominant_kernel = "xent_fwd_bwd_vec"
+        self.probe_mix = (1, 1, M * V * 2, M * V * 2, f"copy of {M * V * 2 / 1e9:.2f} GB (logits in, gradient out)")
+        self.description = (f"cross-entropy forward + backward from the logits (v5/fb5b36393cbd): logits [{M},{V}] "
+                            f"bf16, targets int64 -> grad bf16 [{M},{V}] (log-softmax not materialised)")
+        fn = L.lib().kp_cross_entropy_fwd_bwd_bf16
+        src = self.logits.to(dev)
+        for r in range(self.rotations(self.bytes_per_call)):
+            xd = src if r == 0 else src.clone()
+            out = torch.empty((M, V), dtype=torch.bfloat16, device=dev)
+            args = (xd.data_ptr(), V, M, V, td.data_ptr(), 8, -100, 1.0 / 8192.0, out.data_ptr(), V, 1.0 / 8192.0,
+                    None, None, None, None, 0, stream)
+            self.sets.append((fn, args, (xd, out)))
+        self.keep = td
+        # the CPU restatement materialises three fp32 [rows, V] arrays: time a row sample
+        self.cpu_rows = min(cpu_rows, M)
+        self.cpu_bytes = self.cpu_rows * (V * 4 + 8)
+        self.cpu_sample = f"{self.cpu_rows} of the {M} rows (rate scaled by the sample's own bytes)"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        torch_ref.cross_entropy_fwd_bwd(self.logits[:self.cpu_rows], self.targets[:self.cpu_rows], 1.0 / 8192.0)
+
+
 def make_workload(name, dev):
     if name == "c1":
         return RmsFwd(dev, 4096, 4096, 1e-6, "c1")
@@ -510,10 +552,12 @@ def make_workload(name, dev):
         return CrossEntropy(dev, name="cef")
     if name == "ceb":
         return CrossEntropy(dev, backward=True, name="ceb")
+    if name == "cefb":
+        return CrossEntropyFwdBwd(dev)
     raise SystemExit(f"unknown workload {name!r}")
 
 
-ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb"]
+ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb", "cefb"]
 
 
 # ------------------------------------------------------------------ measure
@@ -639,7 +683,7 @@ def measure_cpu(wl, seconds):
     times.sort()
     med = times[len(times) // 2]
     return {
-        "value": wl.bytes_per_call / med / 1e9,
+        "value": getattr(wl, "cpu_bytes", wl.bytes_per_call) / med / 1e9,
         "unit": "GB/s",
         "ms_per_call": med * 1e3,
         "cores": torch.get_num_threads(),

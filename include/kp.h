@@ -59,7 +59,8 @@ const char* kp_last_error_message(void);
  * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
  * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16, the
  * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16 / kp_silu_bf16 / kp_swiglu_fwd_bwd_bf16, the row kernel of
- * kp_cross_entropy_fwd_bf16, the kernel of kp_cross_entropy_bwd_bf16 and
+ * kp_cross_entropy_fwd_bf16, the kernel of kp_cross_entropy_bwd_bf16, the row
+ * kernel of kp_cross_entropy_fwd_bwd_bf16 and
  * the kernel of kp_stream_probe.
  * Pass NULL, NULL to clear.  Per calling thread. */
 void kp_profile_dominant_kernel(void* start_event, void* stop_event);
@@ -357,6 +358,35 @@ int kp_cross_entropy_fwd_bf16(const void* logits, int64_t row_stride, int64_t M,
 int kp_cross_entropy_bwd_bf16(const float* log_softmax, int64_t lsm_row_stride, const void* targets,
                               int target_bytes, int64_t ignore_index, float grad_loss, void* grad_logits,
                               int64_t out_row_stride, int64_t M, int64_t V, int32_t* error_flag, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Cross-entropy forward and backward straight from the logits, the
+ * log-softmax never stored:
+ *   out_ij = bf16( grad_ij - exp(x_ij - lse_i) * s_i ),
+ *   grad_ij = -grad_loss at (i, t_i) of counted rows, else 0;  s_i = sum_j grad_ij
+ * and, when loss / total_weight are given, the forward's
+ *   *loss = scale * sum over counted rows of (lse_i - x_{i, t_i}),  *total_weight = #counted rows.
+ *
+ * Replaces the _to_copy(f32) -> _log_softmax -> nll_loss_forward(sum) -> div
+ * -> ones_like -> div -> nll_loss_backward -> _log_softmax_backward_data ->
+ * _to_copy(bf16) region at v5/fb5b36393cbd/problem.py:16-59 (also
+ * v4/80ad8e737b06/problem.py:16-59): logits mm_224 bf16 [8192, 128256],
+ * targets i64 [8192], grad_loss = 1/8192.  fp32 arithmetic; the lse is the
+ * forward's (kp_cross_entropy_fwd_bf16).  logits / grad_logits: bf16 [M, V],
+ * unit inner stride, row strides in elements; grad_logits may be logits
+ * itself (in place).  Rows with an ignored or out-of-range target get zero
+ * gradient (out-of-range ones also set *error_flag).  loss and total_weight
+ * are both NULL (no forward outputs, no workspace) or both given; then the
+ * workspace is kp_cross_entropy_fwd_workspace_size(M) bytes, 8-byte aligned.
+ * One launch holds each row in registers when V % 8 == 0, V <= 131072 and
+ * rows are 16-byte aligned (4 bytes of HBM traffic per element); other
+ * shapes take two passes over the row.
+ */
+int kp_cross_entropy_fwd_bwd_bf16(const void* logits, int64_t row_stride, int64_t M, int64_t V,
+                                  const void* targets, int target_bytes, int64_t ignore_index,
+                                  float grad_loss, void* grad_logits, int64_t out_row_stride,
+                                  float scale, float* loss, float* total_weight, int32_t* error_flag,
+                                  void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -16,6 +16,7 @@ from . import aten, fused
 from ._lib import KPError, LIB_PATH, version
 from .fused import (
     cross_entropy_backward,
+    cross_entropy_forward_backward,
     cross_entropy_loss,
     embedding,
     embedding_dense_backward,
@@ -37,6 +38,7 @@ __all__ = [
     "LIB_PATH",
     "aten",
     "cross_entropy_backward",
+    "cross_entropy_forward_backward",
     "cross_entropy_loss",
     "embedding",
     "embedding_dense_backward",

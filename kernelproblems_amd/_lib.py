@@ -94,6 +94,7 @@ SIGNATURES = {
     "kp_cross_entropy_fwd_workspace_size": (sz, [i64]),
     "kp_cross_entropy_fwd_bf16": (i32, [vp, i64, i64, i64, vp, i32, i64, f32, vp, vp, vp, vp, vp, sz, vp]),
     "kp_cross_entropy_bwd_bf16": (i32, [vp, i64, vp, i32, i64, f32, vp, i64, i64, i64, vp, vp]),
+    "kp_cross_entropy_fwd_bwd_bf16": (i32, [vp, i64, i64, i64, vp, i32, i64, f32, vp, i64, f32, vp, vp, vp, vp, sz, vp]),
 }
 
 _lib = None

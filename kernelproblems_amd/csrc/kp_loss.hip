@@ -16,6 +16,10 @@
 // (nll_loss_backward then _log_softmax_backward_data, fp32, then _to_copy):
 // a streaming kernel, 4 bytes read and 2 written per element, evaluated in
 // the same fp32 operations as torch's kernels (expf, this order).
+//
+// Forward and backward straight from the bf16 logits (the whole region when
+// the log-softmax is not needed elsewhere): one block per row holds the row
+// in registers, so each logit is read once and each gradient written once.
 #include <math.h>
 
 #include "kp_common.hpp"
@@ -305,6 +309,247 @@ __global__ __launch_bounds__(kThreads) void xent_bwd_scalar(BwdArgs a) {
   }
 }
 
+// ------------------------------------------------------------------ forward + backward from the logits
+// out_ij = bf16( grad_ij - exp(x_ij - lse_i) * s_i ) straight from the bf16
+// logits (the _log_softmax -> nll_loss_forward -> nll_loss_backward ->
+// _log_softmax_backward_data region with the fp32 log-softmax never stored),
+// optionally with the forward's loss.  A row needs its lse before its first
+// gradient, so a whole row is held on chip: one 1024-thread block per row,
+// thread t holding chunks t + 1024 k (k < KC) in registers -- 16 chunks
+// (64 VGPRs) cover V <= 131072, e.g. the 128256-entry vocabulary (256 KB of
+// bf16 per row).  Each element is read once and written once: 4 bytes per
+// element instead of the 6 of a forward pass followed by a pass that re-reads
+// the logits.  The lse comes from the same (R, s) states as the forward
+// (exponents by one fma against R = fl(max L)), combined across the block.
+struct FbArgs {
+  const uint16_t* logits;
+  int64_t rs;  // row stride, elements
+  uint16_t* out;
+  int64_t ors;  // row stride of out, elements
+  int64_t M, V;
+  const void* targets;
+  int tbytes;
+  int64_t ignore;
+  float g;             // upstream gradient of the summed loss
+  double* row_loss;    // optional [M] (loss requested)
+  int32_t* row_valid;  // optional [M]
+  int32_t* err;
+};
+
+constexpr int kFbThreads = 1024;
+constexpr int kFbMaxChunks = 16;  // 16-byte chunks per thread held in registers
+
+// The row's combined (R, s), identical in every thread of the block: lanes
+// fold by DPP and readlane, waves through LDS in a fixed order.
+template <int NWAVES>
+__device__ __forceinline__ void block_combine(float& R, float& s, float* lds) {
+  combine_dpp<0xB1>(R, s);
+  combine_dpp<0x4E>(R, s);
+  combine_dpp<0x141>(R, s);
+  combine_dpp<0x140>(R, s);
+  float r0 = readlane_f(R, 0), s0 = readlane_f(s, 0);
+  combine(r0, s0, readlane_f(R, 16), readlane_f(s, 16));
+  float r1 = readlane_f(R, 32), s1 = readlane_f(s, 32);
+  combine(r1, s1, readlane_f(R, 48), readlane_f(s, 48));
+  combine(r0, s0, r1, s1);
+  const int w = threadIdx.x >> 6;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    lds[w] = r0;
+    lds[NWAVES + w] = s0;
+  }
+  __syncthreads();
+  R = lds[0];
+  s = lds[NWAVES];
+#pragma unroll
+  for (int i = 1; i < NWAVES; ++i) combine(R, s, lds[i], lds[NWAVES + i]);
+}
+
+struct RowTarget {
+  int64_t t;     // target column, -1 when the row has none
+  float sum;     // s_i = sum_j grad_ij: -g, or 0
+  bool valid;
+};
+
+__device__ __forceinline__ RowTarget fb_target(const FbArgs& a, int64_t row) {
+  const int64_t t = target_at(a.targets, a.tbytes, row);
+  const bool in_range = t >= 0 && t < a.V;
+  const bool valid = t != a.ignore && in_range;
+  if (t != a.ignore && !in_range && threadIdx.x == 0 && a.err) a.err[0] = 1;
+  return RowTarget{valid ? t : -1, valid ? -a.g : 0.0f, valid};
+}
+
+// Thread 0 records the row's loss lse - x_t (x_t loaded before any store of
+// the row, so out may alias the logits).  lse = (R + log2 s) / L with the
+// fp32 log2 s of the gradient (|log2 s| < 18 for V < 2^17: within 2^-24 x 18
+// of exact), summed and divided in fp64.
+__device__ __forceinline__ void fb_row_loss(const FbArgs& a, int64_t row, const RowTarget& rt, float R, float lg,
+                                            float xt) {
+  if (a.row_loss == nullptr || threadIdx.x != 0) return;
+  const double lse = ((double)R + (double)lg) / (double)kLog2e;
+  a.row_loss[row] = rt.valid ? lse - (double)xt : 0.0;
+  a.row_valid[row] = rt.valid;
+}
+
+// p = exp(x - lse) = 2^((x L - R) - log2 s): the fma is rounded relative to
+// x L - R (small for the large p), and log2 s is subtracted afterwards, so
+// p near 1 (a confident row's target, where grad - p sum cancels) carries
+// fp32 relative error rather than an absolute error of ulp(R).
+__device__ __forceinline__ float fb_grad(float x, float R, float lg, bool is_target, float g, float sum) {
+  const float p = __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -R) - lg);
+  const float grad = is_target ? -g : 0.0f;
+  return grad - p * sum;
+}
+
+// An empty asm that takes the packed chunks as in/out operands: the values
+// unpacked in one pass cannot be reused in the next, so only the 4 x KC
+// packed registers stay live across passes (reusing the 8 x KC unpacked
+// floats needs twice the registers and spills at KC = 16).
+template <int KC>
+__device__ __forceinline__ void keep_packed(u32x4* v) {
+#pragma unroll
+  for (int k = 0; k < KC; ++k) asm volatile("" : "+v"(v[k]));
+}
+
+// Rows are addressed through raw buffer descriptors: the row base and length
+// sit in SGPRs and each access takes a single 32-bit offset VGPR, where a
+// 64-bit address takes two (32 per row at KC = 16, which spill).  The range
+// check of the descriptor covers the VGPR offset: a load past the row end
+// returns zeros and a store past it is dropped, so chunks beyond the row get
+// the offset 0x80000000 (out of range for any row) instead of a branch, and
+// a descriptor of length 0 fetches nothing.  Word 3 0x00020000 is the
+// raw-buffer setting of the gfx9 family (32-bit data format).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kBufNT = 2;               // cache policy: non-temporal
+constexpr uint32_t kOutOfRange = 0x80000000u;
+
+__device__ __forceinline__ rsrc_t row_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Byte offset of chunk k of thread tid, or kOutOfRange past the row.
+__device__ __forceinline__ uint32_t fb_off(int tid, int k, int64_t cpr) {
+  const int64_t c = tid + (int64_t)k * kFbThreads;
+  return c < cpr ? (uint32_t)c * 16u : kOutOfRange;
+}
+
+// All KC loads of a row, issued together.
+template <int KC>
+__device__ __forceinline__ void fb_load_row(rsrc_t r, int tid, int64_t cpr, u32x4* v) {
+#pragma unroll
+  for (int k = 0; k < KC; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, fb_off(tid, k, cpr), 0, kBufNT);
+}
+
+// Persistent: one block per CU walks rows blockIdx.x, + gridDim.x, ...; the
+// next row's loads are issued as soon as the previous row's stores are, so
+// the store stream of one row overlaps the load stream of the next (754 us
+// against 791 us for one fresh block per row at [8192, 128256]).  Issuing
+// the next row's chunk k right after row r's chunk k is unpacked, interleaved
+// with row r's stores, measured slower (808 us).  The LDS slots of the block
+// reduction alternate between rows (a slow wave may still read row r's slots
+// while a fast one writes row r + 1's).
+template <int KC>
+__global__ __launch_bounds__(kFbThreads) void xent_fwd_bwd_vec(FbArgs a) {
+  constexpr int kWaves = kFbThreads / kWave;
+  __shared__ float red[2][2 * kWaves];
+  const int64_t cpr = a.V / 8;
+  const uint32_t row_bytes = (uint32_t)a.V * 2u;
+  u32x4 v[KC];
+  int parity = 0;
+  for (int64_t row = blockIdx.x; row < a.M; row += gridDim.x, parity ^= 1) {
+    // the thread index passes through an empty asm each row, so the chunk
+    // offsets derived from it are recomputed where they are used instead of
+    // being hoisted out of the loop (16 more live VGPRs)
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    fb_load_row<KC>(row_rsrc(a.logits + row * a.rs, row_bytes), tid, cpr, v);
+    __builtin_amdgcn_sched_barrier(0);
+    const rsrc_t ro = row_rsrc(a.out + row * a.ors, row_bytes);
+    const RowTarget rt = fb_target(a, row);
+    const float xt = (a.row_loss != nullptr && tid == 0 && rt.valid) ? bf_to_f(a.logits[row * a.rs + rt.t]) : 0.0f;
+    float m = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      if (tid + (int64_t)k * kFbThreads < cpr) {
+        float f[8];
+        unpack8(v[k], f);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) m = fmaxf(m, f[i]);
+      }
+    }
+    keep_packed<KC>(v);
+    float R = m * kLog2e, s = 0.0f;
+    if (R != -INFINITY) {
+      float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int k = 0; k < KC; ++k) {
+        if (tid + (int64_t)k * kFbThreads < cpr) {
+          float f[8];
+          unpack8(v[k], f);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) part[i & 3] += __builtin_amdgcn_exp2f(__builtin_fmaf(f[i], kLog2e, -R));
+        }
+      }
+      s = (part[0] + part[1]) + (part[2] + part[3]);
+    }
+    asm volatile("" ::"v"(xt));  // x_t has arrived before the barrier: other waves may overwrite it after
+    block_combine<kWaves>(R, s, red[parity]);
+    const float lg = log2f(s);
+    fb_row_loss(a, row, rt, R, lg, xt);
+    keep_packed<KC>(v);
+    const int64_t tc = rt.t >> 3;  // -1 >> 3 = -1: no chunk matches
+    const int ti = (int)(rt.t & 7);
+    asm volatile("" : "+v"(tid));  // the store offsets are recomputed here, not kept from the loads
+#pragma unroll
+    for (int k = 0; k < KC; ++k) {
+      const int64_t c = tid + (int64_t)k * kFbThreads;
+      float f[8], o[8];
+      unpack8(v[k], f);
+      const uint32_t off = fb_off(tid, k, cpr);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o[i] = fb_grad(f[i], R, lg, c == tc && i == ti, a.g, rt.sum);
+      __builtin_amdgcn_raw_buffer_store_b128(pack8(o), ro, off, 0, kBufNT);
+    }
+  }
+}
+
+// Any V, stride or alignment: 256 threads per row, two passes over the row
+// (the second re-reads it); each element is read before it is written by the
+// same thread, so out may alias the logits here too.
+__global__ __launch_bounds__(kThreads) void xent_fwd_bwd_scalar(FbArgs a) {
+  __shared__ float red[2 * kWavesPerBlock];
+  const int64_t row = blockIdx.x;
+  const uint16_t* x = a.logits + row * a.rs;
+  uint16_t* o = a.out + row * a.ors;
+  const RowTarget rt = fb_target(a, row);
+  const float xt = (a.row_loss != nullptr && threadIdx.x == 0 && rt.valid) ? bf_to_f(x[rt.t]) : 0.0f;
+  float R = -INFINITY, s = 0.0f;
+  for (int64_t j0 = 0; j0 < a.V; j0 += 8 * kThreads) {
+    float f[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int64_t j = j0 + i * kThreads + threadIdx.x;
+      f[i] = j < a.V ? bf_to_f(x[j]) : -INFINITY;
+    }
+    online8(R, s, f);
+  }
+  asm volatile("" ::"v"(xt));  // x_t has arrived before the barrier: other waves may overwrite it after
+  block_combine<kWavesPerBlock>(R, s, red);
+  const float lg = log2f(s);
+  fb_row_loss(a, row, rt, R, lg, xt);
+  for (int64_t j = threadIdx.x; j < a.V; j += kThreads)
+    o[j] = f_to_bf(fb_grad(bf_to_f(x[j]), R, lg, j == rt.t, a.g, rt.sum));
+}
+
+const void* fwd_bwd_vec_kernel(int kc) {
+  switch (kc) {
+    case 1: return reinterpret_cast<const void*>(xent_fwd_bwd_vec<1>);
+    case 2: return reinterpret_cast<const void*>(xent_fwd_bwd_vec<2>);
+    case 4: return reinterpret_cast<const void*>(xent_fwd_bwd_vec<4>);
+    case 8: return reinterpret_cast<const void*>(xent_fwd_bwd_vec<8>);
+    default: return reinterpret_cast<const void*>(xent_fwd_bwd_vec<16>);
+  }
+}
+
 bool valid_target_bytes(int b) { return b == 4 || b == 8; }
 
 }  // namespace
@@ -399,6 +644,67 @@ int kp_cross_entropy_bwd_bf16(const float* log_softmax, int64_t lsm_row_stride, 
     launch_dominant_raw(reinterpret_cast<const void*>(xent_bwd_scalar), dim3((unsigned)(want < cap ? want : cap)),
                         dim3(kThreads), args, 0, as_stream(stream));
   }
+  return check_launch(who);
+}
+
+int kp_cross_entropy_fwd_bwd_bf16(const void* logits, int64_t row_stride, int64_t M, int64_t V, const void* targets,
+                                  int target_bytes, int64_t ignore_index, float grad_loss, void* grad_logits,
+                                  int64_t out_row_stride, float scale, float* loss, float* total_weight,
+                                  int32_t* error_flag, void* workspace, size_t workspace_bytes, void* stream) {
+  static const char* who = "kp_cross_entropy_fwd_bwd_bf16";
+  if (M < 0 || V < 1) return fail(KP_EINVAL, "%s: bad shape [%lld, %lld]", who, (long long)M, (long long)V);
+  if (!valid_target_bytes(target_bytes)) return fail(KP_EINVAL, "%s: target_bytes must be 4 or 8", who);
+  if ((loss == nullptr) != (total_weight == nullptr))
+    return fail(KP_EINVAL, "%s: loss and total_weight are both given or both NULL", who);
+  const bool want_loss = loss != nullptr;
+  const size_t need = want_loss ? kp_cross_entropy_fwd_workspace_size(M) : 0;
+  if (workspace_bytes < need || (need && workspace == nullptr))
+    return fail(KP_EWORKSPACE, "%s: workspace of %zu bytes needed", who, need);
+  if (need && (reinterpret_cast<uintptr_t>(workspace) & 7) != 0)
+    return fail(KP_EINVAL, "%s: workspace not 8-byte aligned", who);
+  if (M > 0 && (logits == nullptr || targets == nullptr || grad_logits == nullptr))
+    return fail(KP_EINVAL, "%s: NULL operand", who);
+  if (M > 1 && (row_stride < V || out_row_stride < V)) return fail(KP_EINVAL, "%s: row stride < V", who);
+  if (M > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: too many rows", who);
+  hipStream_t st = as_stream(stream);
+  FbArgs a{};
+  a.logits = static_cast<const uint16_t*>(logits);
+  a.rs = row_stride;
+  a.out = static_cast<uint16_t*>(grad_logits);
+  a.ors = out_row_stride;
+  a.M = M;
+  a.V = V;
+  a.targets = targets;
+  a.tbytes = target_bytes;
+  a.ignore = ignore_index;
+  a.g = grad_loss;
+  a.err = error_flag;
+  if (want_loss) {
+    a.row_loss = static_cast<double*>(workspace);
+    a.row_valid = reinterpret_cast<int32_t*>(static_cast<char*>(workspace) + (size_t)M * sizeof(double));
+  }
+  if (M > 0) {
+    const int64_t cpr = V / 8;
+    const bool vec = V % 8 == 0 && aligned16(logits) && aligned16(grad_logits) &&
+                     (M == 1 || (row_stride % 8 == 0 && out_row_stride % 8 == 0)) &&
+                     cpr <= (int64_t)kFbThreads * kFbMaxChunks;
+    void* args[] = {&a};
+    if (vec) {
+      int kc = 1;
+      while ((int64_t)kc * kFbThreads < cpr) kc *= 2;
+      const int64_t cus = cu_count();
+      const unsigned blocks = (unsigned)(M < cus ? M : cus);
+      launch_dominant_raw(fwd_bwd_vec_kernel(kc), dim3(blocks), dim3(kFbThreads), args, 0, st);
+    } else {
+      launch_dominant_raw(reinterpret_cast<const void*>(xent_fwd_bwd_scalar), dim3((unsigned)M), dim3(kThreads), args,
+                          0, st);
+    }
+    const int rc = check_launch(who);
+    if (rc != KP_OK) return rc;
+  }
+  if (!want_loss) return KP_OK;
+  hipLaunchKernelGGL(xent_fwd_finish, dim3(1), dim3(kFinThreads), 0, st, a.row_loss, a.row_valid, M, (double)scale,
+                     loss, total_weight);
   return check_launch(who);
 }
 

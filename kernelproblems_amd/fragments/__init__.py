@@ -27,7 +27,7 @@ FRAGMENTS = (
     "v8/c68dae22972b", "v8/385e1beb9bb9", "v7/58e7a4d6cde3", "v4/65b4b565ed67", "v6/182d2dcd0652",
     "v5/441b7bf23822", "v4/c72358b8111e",
     # token cross-entropy forward / backward
-    "v8/71f1d2c9f38b", "v8/622c35f5d1c6",
+    "v8/71f1d2c9f38b", "v8/622c35f5d1c6", "v7/e59c6b1b5156", "v5/fb5b36393cbd", "v4/80ad8e737b06",
     # chain: RMSNorm forward -> backward (+ gradient adds, residual) -> embedding backward
     "v6/0b493aad68f0", "v5/118d525f44e0",
     # chain: (residual add +) RMSNorm forward -> backward (+ gradient adds, residual epilogue)

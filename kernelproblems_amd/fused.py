@@ -590,6 +590,44 @@ def cross_entropy_loss(logits: torch.Tensor, targets: torch.Tensor, *, ignore_in
     return (loss, tw, lse) if return_lse else (loss, tw)
 
 
+def cross_entropy_forward_backward(logits: torch.Tensor, targets: torch.Tensor, grad_loss: float, *,
+                                   ignore_index: int = -100, scale: float = 1.0, return_loss: bool = False,
+                                   in_place: bool = False):
+    """The bf16 logits gradient of the summed cross-entropy straight from the
+    bf16 logits [..., V]: out = grad - exp(x - lse) * sum(grad), grad =
+    -grad_loss at each counted row's target (v5/fb5b36393cbd/problem.py:16-59:
+    _log_softmax -> nll_loss_forward -> nll_loss_backward ->
+    _log_softmax_backward_data -> _to_copy(bf16), the fp32 log-softmax never
+    stored).  With return_loss also (loss, total_weight) as
+    cross_entropy_loss(..., scale=scale) computes them.  in_place=True writes
+    the gradient over the logits (which must then be contiguous) and
+    returns them."""
+    _need_gpu("cross_entropy logits", logits)
+    dev = logits.device
+    V = logits.shape[-1] if logits.dim() else 1
+    lt, rs, M = _as_rows(logits, V)
+    t, tb = _targets(targets, M, dev)
+    if in_place:
+        if not logits.is_contiguous():
+            raise RuntimeError("cross_entropy_forward_backward: in_place needs contiguous logits")
+        out = logits
+    else:
+        out = torch.empty(logits.shape, dtype=torch.bfloat16, device=dev)
+    loss = tw = None
+    ws, ws_bytes = None, 0
+    if return_loss:
+        loss = torch.empty((), dtype=torch.float32, device=dev)
+        tw = torch.empty((), dtype=torch.float32, device=dev)
+        ws_bytes = int(L.lib().kp_cross_entropy_fwd_workspace_size(M))
+        ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
+    flag = _flag(dev)
+    L.call("kp_cross_entropy_fwd_bwd_bf16", lt.data_ptr(), rs, M, V, t.data_ptr(), tb, int(ignore_index),
+           float(grad_loss), out.data_ptr(), V, float(scale), _ptr(loss), _ptr(tw), _ptr(flag), _ptr(ws), ws_bytes,
+           _stream(dev))
+    _raise_if_flagged(flag, "cross_entropy_forward_backward")
+    return (out, loss, tw) if return_loss else out
+
+
 def cross_entropy_backward(log_softmax: torch.Tensor, targets: torch.Tensor, grad_loss: float, *,
                            ignore_index: int = -100) -> torch.Tensor:
     """Gradient of the summed cross-entropy w.r.t. the logits, in bf16, from

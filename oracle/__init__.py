@@ -42,6 +42,8 @@ silu, swiglu_fwd_bwd   compositions of swiglu_fwd / swiglu_bwd; silu also
 cross_entropy_fwd      torch fp64 ``log_softmax`` + ``nll_loss`` (sum,
                        ignore_index), closed forms (uniform row: log V,
                        dominant logit: 0), shift invariance, ignored rows.
+cross_entropy_fwd_bwd  fp64 autograd of the forward loss (one bf16 rounding,
+                       bit-equal), cross_entropy_bwd of the fp64 log-softmax.
 cross_entropy_bwd      torch fp64 ``nll_loss_backward`` +
                        ``_log_softmax_backward_data`` (bit-exact after one
                        rounding), the autograd of the forward, rows summing
@@ -81,6 +83,7 @@ _SIGS = {
     "kpo_swiglu_bwd": (None, [vp, vp, vp, vp, vp, vp, i64]),
     "kpo_cross_entropy_fwd": (i64, [vp, i64, i64, vp, i64, f64, vp, vp, vp]),
     "kpo_cross_entropy_bwd": (i64, [vp, i64, i64, vp, i64, f64, vp]),
+    "kpo_cross_entropy_fwd_bwd": (i64, [vp, i64, i64, vp, i64, f64, vp]),
 }
 
 
@@ -325,4 +328,17 @@ def cross_entropy_bwd(log_softmax: np.ndarray, targets: np.ndarray, grad_loss: f
     t = _c(targets, np.int64).reshape(M)
     out = np.empty((M, V), dtype=np.uint16)
     bad = lib().kpo_cross_entropy_bwd(_p(L), M, V, _p(t), int(ignore_index), float(grad_loss), _p(out))
+    return out, int(bad)
+
+
+def cross_entropy_fwd_bwd(logits: np.ndarray, targets: np.ndarray, grad_loss: float, ignore_index: int = -100):
+    """The logits gradient of grad_loss * (sum over non-ignored rows of
+    lse_i - x_{i, t_i}) straight from the bf16 logits (uint16 [M, V]):
+    bf16 of grad - exp(x - lse) * sum(grad), in double.  Returns
+    (out, n_out_of_range)."""
+    x = _c(logits, np.uint16)
+    M, V = x.shape
+    t = _c(targets, np.int64).reshape(M)
+    out = np.empty((M, V), dtype=np.uint16)
+    bad = lib().kpo_cross_entropy_fwd_bwd(_p(x), M, V, _p(t), int(ignore_index), float(grad_loss), _p(out))
     return out, int(bad)

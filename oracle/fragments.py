@@ -245,6 +245,19 @@ def _xent_bwd(div, lsm, t, tw):          # v8/622c35f5d1c6/problem.py:16-33
     return aten.view.default(aten.view.default(out, [1, *out.shape]), list(out.shape))
 
 
+def _xent_fwd_bwd(t, logits):           # v5/fb5b36393cbd/problem.py:16-59, v4/80ad8e737b06:16-59
+    tv = aten.view.default(t, [t.numel()])
+    x = aten.view.default(aten._unsafe_view.default(logits, [1, *logits.shape]), list(logits.shape))
+    lsm = aten._log_softmax.default(aten._to_copy.default(x, dtype=torch.float32), 1, False)
+    loss, tw = aten.nll_loss_forward.default(lsm, tv, None, 2, -100)
+    div = aten.div.Tensor(loss, 8192.0)
+    g = aten.div.Tensor(aten.ones_like.default(div, pin_memory=False, memory_format=torch.preserve_format), 8192.0)
+    gi = aten.nll_loss_backward.default(g, lsm, tv, None, 2, -100, tw)
+    d = aten._log_softmax_backward_data.default(gi, lsm, 1, torch.float32)
+    out = aten._to_copy.default(d, dtype=torch.bfloat16, layout=torch.strided, device=lsm.device)
+    return aten.t.default(aten.view.default(aten.view.default(out, [1, *out.shape]), list(out.shape)))
+
+
 def _norm_emb_bwd_chain(x, w, mm_a, mm_b, mm_c, res, ids):  # v6/0b493aad68f0/problem.py:16-56
     y, r = _norm(x, w)
     dy = aten.add.Tensor(aten.add.Tensor(aten.view.default(mm_a, list(x.shape)), aten.view.default(mm_b, list(x.shape))),
@@ -318,6 +331,9 @@ _FRAGMENTS = {
     "v4/c72358b8111e": _swiglu_fwd_bwd(True),
     "v8/71f1d2c9f38b": _xent_fwd,
     "v8/622c35f5d1c6": _xent_bwd,
+    "v7/e59c6b1b5156": lambda logits, t: _xent_fwd(t, logits),
+    "v5/fb5b36393cbd": _xent_fwd_bwd,
+    "v4/80ad8e737b06": _xent_fwd_bwd,
     "v6/0b493aad68f0": _norm_emb_bwd_chain,
     "v5/118d525f44e0": _norm_emb_bwd_chain_fsdp,
     "v6/822931829090": lambda x, w, a, b, c, res: _norm_chain([x], w, [a, b, c], res, 3),

@@ -438,3 +438,34 @@ int64_t kpo_cross_entropy_bwd(const float* lsm, int64_t M, int64_t V, const int6
   }
   return bad;
 }
+
+/* Forward and backward from the logits in one region
+ * (v5/fb5b36393cbd/problem.py:16-59): the backward above applied to
+ * L_ij = x_ij - lse_i, with lse_i computed as in kpo_cross_entropy_fwd, all in
+ * double, one rounding to bf16:
+ *   out_ij = grad_ij - exp(x_ij - lse_i) * sum_j grad_ij. */
+int64_t kpo_cross_entropy_fwd_bwd(const uint16_t* logits, int64_t M, int64_t V, const int64_t* targets, int64_t ignore,
+                                  double g, uint16_t* out) {
+  int64_t bad = 0;
+  for (int64_t i = 0; i < M; ++i) {
+    const uint16_t* x = logits + i * V;
+    double m = -INFINITY;
+    for (int64_t j = 0; j < V; ++j) {
+      const double v = (double)bf2f(x[j]);
+      if (v > m || isnan(v)) m = v;
+    }
+    double s = 0.0;
+    for (int64_t j = 0; j < V; ++j) s += exp((double)bf2f(x[j]) - m);
+    const double lse = m + log(s);
+    const int64_t t = targets[i];
+    const int in_range = t >= 0 && t < V;
+    if (t != ignore && !in_range) ++bad;
+    const int valid = t != ignore && in_range;
+    const double sum = valid ? -g : 0.0;
+    for (int64_t j = 0; j < V; ++j) {
+      const double grad = (valid && j == t) ? -g : 0.0;
+      out[i * V + j] = d2bf(grad - exp((double)bf2f(x[j]) - lse) * sum);
+    }
+  }
+  return bad;
+}

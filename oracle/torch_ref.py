@@ -137,6 +137,18 @@ def cross_entropy_bwd(lsm: torch.Tensor, targets: torch.Tensor, grad_loss: float
     return aten._to_copy.default(d, dtype=torch.bfloat16)
 
 
+def cross_entropy_fwd_bwd(logits: torch.Tensor, targets: torch.Tensor, grad_loss: float):
+    """v5/fb5b36393cbd/problem.py:16-59: _to_copy(f32) -> _log_softmax ->
+    nll_loss_forward(sum) -> nll_loss_backward -> _log_softmax_backward_data
+    -> _to_copy(bf16)."""
+    lsm = aten._log_softmax.default(aten._to_copy.default(logits, dtype=torch.float32), 1, False)
+    _, tw = aten.nll_loss_forward.default(lsm, targets, None, 2, -100)
+    g = torch.tensor(grad_loss, dtype=torch.float32, device=logits.device)
+    gi = aten.nll_loss_backward.default(g, lsm, targets, None, 2, -100, tw)
+    d = aten._log_softmax_backward_data.default(gi, lsm, 1, torch.float32)
+    return aten._to_copy.default(d, dtype=torch.bfloat16)
+
+
 def embedding_rms_norm_fwd(table: torch.Tensor, ids: torch.Tensor, w: torch.Tensor, eps: float):
     """v8/12545c1e9b06/problem.py:24-42: embedding.default -> _fused_rms_norm."""
     x = aten.embedding.default(table, ids)

@@ -145,6 +145,18 @@ def test_cross_entropy_validation(lib):
     _expect(lib, L.KP_EINVAL, bwd, 16, 8, 32, 8, -100, 1.0, 64, 8, 4, 0, None, None)    # V = 0
 
 
+def test_cross_entropy_fwd_bwd_validation(lib):
+    fn = "kp_cross_entropy_fwd_bwd_bf16"
+    ws = int(lib.kp_cross_entropy_fwd_workspace_size(4))
+    _expect(lib, L.KP_EINVAL, fn, 16, 8, 4, 8, 32, 8, -100, 1.0, 48, 8, 1.0, 64, None, None, 128, ws, None)  # loss only
+    _expect(lib, L.KP_EWORKSPACE, fn, 16, 8, 4, 8, 32, 8, -100, 1.0, 48, 8, 1.0, 64, 72, None, 128, ws - 8, None)
+    _expect(lib, L.KP_EINVAL, fn, 16, 8, 4, 8, 32, 2, -100, 1.0, 48, 8, 1.0, None, None, None, None, 0, None)  # 2-byte ids
+    _expect(lib, L.KP_EINVAL, fn, 16, 8, 4, 8, 32, 8, -100, 1.0, None, 8, 1.0, None, None, None, None, 0, None)  # no out
+    _expect(lib, L.KP_EINVAL, fn, 16, 8, 4, 8, 32, 8, -100, 1.0, 48, 4, 1.0, None, None, None, None, 0, None)  # stride
+    assert lib.kp_cross_entropy_fwd_bwd_bf16(None, 8, 0, 8, None, 8, -100, 1.0, None, 8, 1.0, None, None, None, None,
+                                             0, None) == L.KP_OK
+
+
 def test_embedding_rmsnorm_validation(lib):
     fn = "kp_embedding_rmsnorm_fwd_bf16"
     _expect(lib, L.KP_EINVAL, fn, 16, 100, 64, 32, 3, 8, None, 64, 64, None, 64, 48, 64, None, 64, 1e-5, None, None)

@@ -72,6 +72,9 @@ SIGNATURES = {
     "v6/182d2dcd0652": [("mm_4", FFN), ("mm_5", FFN), ("mm_662", FFN)],
     "v5/441b7bf23822": [("mm_4", FFN), ("mm_5", FFN), ("mm_662", FFN)],
     "v4/c72358b8111e": [("mm_4", FFN), ("mm_5", FFN), ("mm_662", FFN)],
+    "v7/e59c6b1b5156": [("mm_224", (BF, (8192, 128256), (128256, 1))), ("view_805", (I64, (8192,), (1,)))],
+    "v5/fb5b36393cbd": [("arg584_1", IDS), ("mm_224", (BF, (8192, 128256), (128256, 1)))],
+    "v4/80ad8e737b06": [("arg584_1", IDS), ("mm_224", (BF, (8192, 128256), (128256, 1)))],
     "v8/71f1d2c9f38b": [("arg584_1", IDS), ("mm_224", (BF, (8192, 128256), (128256, 1)))],
     "v6/0b493aad68f0": [("embedding", X), ("_unsafe_view_432", W), ("mm_670", MM), ("mm_672", MM), ("mm_674", MM),
                         ("add_220", X), ("arg583_1", IDS)],

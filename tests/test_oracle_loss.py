@@ -9,7 +9,7 @@ import pytest
 import torch
 
 import oracle
-from tests._util import bf, bf16_round_exact, gen, randn_bf16, to_u16
+from tests._util import bf, bf16_round_exact, gen, randn_bf16, to_u16, ulp_bf16
 
 aten = torch.ops.aten
 
@@ -115,3 +115,36 @@ def test_bwd_out_of_range_rows():
     assert not bf(out)[:2].any()
     # exp(0) = 1: row 2 is 0.5 everywhere except 0.5 - 0.5 = 0 at the target
     assert np.array_equal(bf(out)[2], np.where(np.arange(10) == 2, 0.0, 0.5))
+
+
+@pytest.mark.parametrize("M,V,std", [(6, 513, 2.0), (4, 4099, 5.0)])
+def test_fwd_bwd_is_the_fp64_autograd_gradient(M, V, std):
+    """cross_entropy_fwd_bwd (v5/fb5b36393cbd) is the fp64 autograd gradient
+    of scale * sum(nll(log_softmax(x))) with one bf16 rounding: bit-equal."""
+    g = gen(M * 31 + V)
+    x = randn_bf16((M, V), g, std=std)
+    t = _targets(M, V, g, ignore_every=3)
+    scale = 1.0 / 8192
+    xd = x.double().requires_grad_(True)
+    loss = torch.nn.functional.nll_loss(torch.log_softmax(xd, 1), t, reduction="sum", ignore_index=-100) * scale
+    loss.backward()
+    out, bad = oracle.cross_entropy_fwd_bwd(to_u16(x), t.numpy(), scale)
+    assert bad == 0
+    assert np.array_equal(out, bf16_round_exact(xd.grad.numpy()).reshape(M, V))
+    assert not bf(out)[(t == -100).numpy()].any()
+
+
+def test_fwd_bwd_agrees_with_the_two_step_path():
+    """The same gradient as cross_entropy_bwd fed the log-softmax (rounded to
+    fp32, as the two-step graph stores it): within one bf16 ulp; and an
+    out-of-range target is counted and its row zeroed."""
+    g = gen(9)
+    M, V = 5, 3000
+    x = randn_bf16((M, V), g, std=3.0)
+    t = torch.tensor([7, -100, V, 2999, 0])
+    out, bad = oracle.cross_entropy_fwd_bwd(to_u16(x), t.numpy(), 0.5)
+    L = torch.log_softmax(x.double(), 1).float().numpy()
+    ref, bad2 = oracle.cross_entropy_bwd(L, t.numpy(), 0.5)
+    assert bad == bad2 == 1
+    assert (ulp_bf16(out, ref) <= 1).all()
+    assert not bf(out)[[1, 2]].any()

@@ -104,3 +104,7 @@ def test_cross_entropy_fwd_and_bwd():
     out = torch_ref.cross_entropy_bwd(L, t, 1 / 8192)
     eo, _ = oracle.cross_entropy_bwd(L.numpy(), t.numpy(), 1 / 8192)
     _close_ulp(to_u16(out), eo, min_exact=0.99)
+    # the whole region from the logits (v5/fb5b36393cbd)
+    fb = torch_ref.cross_entropy_fwd_bwd(x, t, 1 / 8192)
+    efb, _ = oracle.cross_entropy_fwd_bwd(to_u16(x), t.numpy(), 1 / 8192)
+    _close_ulp(to_u16(fb), efb, min_exact=0.99)
