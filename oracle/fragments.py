@@ -85,6 +85,14 @@ def _rms_fwd_strided_w(k):               # v7/215dd2e6a519/problem.py:16-38, v6/
     return f
 
 
+def _rms_fwd_ffn_unshard(wv, x, g1, g3, g2):  # v1/2a844503364a/problem.py:12-72
+    y = _norm(x, _clone_weight(wv))[0]
+    w1 = aten.t.default(_unshard(g1, [14336, 4096]))
+    w3 = aten.t.default(_unshard(g3, [14336, 4096]))
+    w2 = aten.t.default(_unshard(g2, [4096, 14336]))
+    return (*_views(y, 2), w1, w3, w2)
+
+
 def _add_rms_fwd(mm, res, w):            # v8/7884328a5557/problem.py:16-33
     h = aten.add.Tensor(res, aten._unsafe_view.default(mm, list(res.shape)))
     return _views(_norm(h, w)[0], 2)
@@ -298,6 +306,11 @@ _FRAGMENTS = {
     "v6/ac3fb0b7281f": _rms_fwd_strided_w(2),
     "v8/7884328a5557": _add_rms_fwd,
     "v8/8e33a91b7364": _add_rms_fwd_final,
+    "v1/84496d824942": _rms_fwd_strided_w(3),
+    "v1/2a844503364a": _rms_fwd_ffn_unshard,
+    "v1/18b859c50de2": lambda mm, res, flat: (lambda y, w: (y, aten.t.default(aten.t.default(w))))(
+        *_add_rms_fwd_final(mm, res, flat)),
+    "v5/013a3088b488": lambda mm, res, flat: (lambda y, w: (y, aten.t.default(w)))(*_add_rms_fwd_final(mm, res, flat)),
     "v8/94985bdb7630": _add_rms_fwd_layer(True),
     "v8/7815074de963": _add_rms_fwd_layer(False),
     "v7/45990c83cfd6": _rms_bwd_recompute,
@@ -322,6 +335,8 @@ _FRAGMENTS = {
     "v6/dc55b25cdcb2": _rope_bwd_cloned,
     "v5/a1bb72d946b0": _rope_bwd_qkv,
     "v4/a1318bc813d2": _rope_bwd_qkv,
+    "v6/c8c60d8f7015": _rope_qk_fwd,
+    "v5/c68dae22972b": _swiglu_fwd,
     "v8/c68dae22972b": _swiglu_fwd,
     "v8/385e1beb9bb9": _swiglu_bwd,
     "v7/58e7a4d6cde3": _silu_only,
@@ -344,6 +359,11 @@ _FRAGMENTS = {
     "v6/408ac0979ac5": lambda mm, emb, w, a, b, res: _norm_chain([emb, mm], w, [a, b], res, 2),
     "v4/9c745ea697a7": lambda mm, emb, wv, a, b, res: _norm_chain([emb, mm], _clone_weight(wv), [a, b], res, 2),
     "v6/28b45679fca1": lambda mm, x, dy, w: _norm_chain([x, mm], w, [dy], None, 0),
+    "v1/f7ad66842c19": lambda mm, x, dy, w: _norm_chain([x, mm], w, [dy], None, 0),
+    "v5/ac7d64b3c769": lambda mm, x, dy, w: _norm_chain([x, mm], w, [dy], None, 0),
+    "v5/cbfdd7549926": lambda mm, emb, wv, a, b, res: _norm_chain([emb, mm], _clone_weight(wv), [a, b], res, 2),
+    "v1/84c0a03c4374": lambda wv, x, a, b, res: _norm_chain([x], _clone_weight(wv), [a, b], res, 2),
+    "v1/680e4c57cdc8": _norm_emb_bwd_chain_fsdp,
 }
 
 # Fragments listed again by later or earlier rounds with the same op sequence
@@ -351,15 +371,22 @@ _FRAGMENTS = {
 _SAME_OPS = {
     "v1/1e49beb8a123": "v7/1e49beb8a123", "v1/363b7b58c971": "v4/363b7b58c971", "v1/65b4b565ed67": "v4/65b4b565ed67",
     "v1/80ad8e737b06": "v4/80ad8e737b06", "v1/9c745ea697a7": "v4/9c745ea697a7", "v1/c72358b8111e": "v4/c72358b8111e",
-    "v2/1e49beb8a123": "v7/1e49beb8a123", "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67",
-    "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/c72358b8111e": "v4/c72358b8111e",
-    "v3/1e49beb8a123": "v7/1e49beb8a123", "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67",
-    "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e",
-    "v4/1e49beb8a123": "v7/1e49beb8a123", "v5/1e49beb8a123": "v7/1e49beb8a123", "v6/1e49beb8a123": "v7/1e49beb8a123",
+    "v2/18b859c50de2": "v1/18b859c50de2", "v2/1e49beb8a123": "v7/1e49beb8a123", "v2/2a844503364a": "v1/2a844503364a",
+    "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67", "v2/680e4c57cdc8": "v1/680e4c57cdc8",
+    "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/84496d824942": "v1/84496d824942", "v2/84c0a03c4374": "v1/84c0a03c4374",
+    "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/c72358b8111e": "v4/c72358b8111e", "v2/f7ad66842c19": "v1/f7ad66842c19",
+    "v3/18b859c50de2": "v1/18b859c50de2", "v3/1e49beb8a123": "v7/1e49beb8a123", "v3/2a844503364a": "v1/2a844503364a",
+    "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67", "v3/680e4c57cdc8": "v1/680e4c57cdc8",
+    "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/84496d824942": "v1/84496d824942", "v3/84c0a03c4374": "v1/84c0a03c4374",
+    "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e", "v3/f7ad66842c19": "v1/f7ad66842c19",
+    "v4/18b859c50de2": "v1/18b859c50de2", "v4/1e49beb8a123": "v7/1e49beb8a123", "v4/2a844503364a": "v1/2a844503364a",
+    "v4/680e4c57cdc8": "v1/680e4c57cdc8", "v4/84496d824942": "v1/84496d824942", "v4/84c0a03c4374": "v1/84c0a03c4374",
+    "v4/f7ad66842c19": "v1/f7ad66842c19", "v5/1e49beb8a123": "v7/1e49beb8a123", "v6/1e49beb8a123": "v7/1e49beb8a123",
     "v6/215dd2e6a519": "v7/215dd2e6a519", "v6/622c35f5d1c6": "v8/622c35f5d1c6", "v6/71f1d2c9f38b": "v8/71f1d2c9f38b",
-    "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968", "v7/385e1beb9bb9": "v8/385e1beb9bb9",
-    "v7/493cad38cac9": "v8/493cad38cac9", "v7/622c35f5d1c6": "v8/622c35f5d1c6", "v7/8e33a91b7364": "v8/8e33a91b7364",
-    "v7/ac3fb0b7281f": "v6/ac3fb0b7281f", "v7/f4e9e58fef73": "v8/f4e9e58fef73", "v8/e29b92927600": "v7/e29b92927600",
+    "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968", "v6/c68dae22972b": "v5/c68dae22972b",
+    "v7/385e1beb9bb9": "v8/385e1beb9bb9", "v7/493cad38cac9": "v8/493cad38cac9", "v7/622c35f5d1c6": "v8/622c35f5d1c6",
+    "v7/8e33a91b7364": "v8/8e33a91b7364", "v7/ac3fb0b7281f": "v6/ac3fb0b7281f", "v7/f4e9e58fef73": "v8/f4e9e58fef73",
+    "v8/e29b92927600": "v7/e29b92927600",
 }
 for _alias, _canon in _SAME_OPS.items():
     _FRAGMENTS[_alias] = _FRAGMENTS[_canon]

@@ -18,6 +18,8 @@ EXACT = {
     "v8/94985bdb7630": set(range(3, 10)),
     "v8/7815074de963": set(range(3, 10)),
     "v8/12545c1e9b06": set(range(3, 9)),
+    "v5/013a3088b488": {1},
+    "v1/2a844503364a": {2, 3, 4},
 }
 # Token-sum outputs of chains whose summed rows come from an earlier kernel
 # of the chain: each summand may differ from eager's by one bf16 ulp, and the
@@ -50,6 +52,7 @@ def _storage(t):
 def _check_close(fid, i, a, e, inputs):
     what = f"{fid} output {i}"
     fid = fr.SAME_AS.get(fid, fid)  # a repeated fragment's outputs are classed as its canonical's
+    fid = fr.EQUIVALENT.get(fid, fid)
     assert a.shape == e.shape and a.dtype == e.dtype, f"{what}: {a.shape}/{a.dtype} vs {e.shape}/{e.dtype}"
     assert a.stride() == e.stride(), f"{what}: strides {a.stride()} vs {e.stride()}"
     if i in EXACT.get(fid, ()):

@@ -25,6 +25,7 @@ FLAT_EMB = (BF, (525336576,), (1,))
 FLAT_LAYER = (BF, (218112000,), (1,))
 FFN = (BF, (8192, 14336), (14336, 1))
 FFN3 = (BF, (1, 8192, 14336), (117440512, 14336, 1))
+FFNW = (BF, (8, 7340032), (27264000, 1))
 GQ = (BF, (1, 32, 8192, 128), (33554432, 128, 4096, 1))
 GK = (BF, (1, 8, 8192, 128), (8388608, 128, 1024, 1))
 
@@ -34,6 +35,11 @@ SIGNATURES = {
     "v8/f4e9e58fef73": [("add_recomputed", X), ("_unsafe_view_428", W)],
     "v7/215dd2e6a519": [("getitem_1614", WV), ("add_61", X)],
     "v6/ac3fb0b7281f": [("getitem_1619", WV), ("add_62", X)],
+    "v1/84496d824942": [("getitem_1614", WV), ("add_61", X)],
+    "v1/2a844503364a": [("getitem_1619", WV), ("add_62", X), ("getitem_1620", FFNW), ("getitem_1621", FFNW),
+                        ("getitem_1622", FFNW)],
+    "v1/18b859c50de2": [("mm_223", MM), ("add_62", X), ("wait_tensor_969", (BF, (525340672,), (1,)))],
+    "v5/013a3088b488": [("mm_223", MM), ("add_62", X), ("wait_tensor_969", (BF, (525340672,), (1,)))],
     "v8/7884328a5557": [("mm_220", MM), ("add_61", X), ("_unsafe_view_981", W)],
     "v8/8e33a91b7364": [("mm_223", MM), ("add_62", X), ("wait_tensor_969", (BF, (525340672,), (1,)))],
     "v8/94985bdb7630": [("mm_216", MM), ("add_60", X), ("wait_tensor_966", FLAT_LAYER)],
@@ -67,6 +73,8 @@ SIGNATURES = {
     "v8/c68dae22972b": [("mm_4", FFN), ("mm_5", FFN)],
     "v8/385e1beb9bb9": [("mm_662", FFN), ("silu_recomputed", FFN3), ("_unsafe_view_5_recomputed", FFN3),
                         ("_unsafe_view_4_recomputed", FFN3)],
+    "v5/c68dae22972b": [("mm_221", FFN), ("mm_222", FFN)],
+    "v6/c8c60d8f7015": [("arg586_1", POS), ("arg582_1", TAB), ("mm_217", MM), ("mm_218", MM1)],
     "v7/58e7a4d6cde3": [("mm_221", FFN)],
     "v4/65b4b565ed67": [("mm_221", FFN), ("mm_222", FFN)],
     "v6/182d2dcd0652": [("mm_4", FFN), ("mm_5", FFN), ("mm_662", FFN)],
@@ -94,6 +102,14 @@ SIGNATURES = {
                         ("add_218", X)],
     "v4/9c745ea697a7": [("mm_3", MM), ("embedding", X), ("getitem_787", WV), ("mm_664", MM), ("mm_666", MM),
                         ("add_218", X)],
+    "v1/f7ad66842c19": [("mm_223", MM), ("add_62_recomputed", X), ("mm_226", MM), ("wait_tensor_970", W)],
+    "v5/ac7d64b3c769": [("mm_223", MM), ("add_62_recomputed", X), ("mm_226", MM), ("wait_tensor_970", W)],
+    "v5/cbfdd7549926": [("mm_3", MM), ("embedding", X), ("getitem_787", WV), ("mm_664", MM), ("mm_666", MM),
+                        ("add_218", X)],
+    "v1/84c0a03c4374": [("getitem_1624", WV), ("add_62_recomputed", X), ("mm_230", MM), ("mm_232", MM),
+                        ("getitem_420", X)],
+    "v1/680e4c57cdc8": [("getitem_791", WV), ("embedding", X), ("mm_670", MM), ("mm_672", MM), ("mm_674", MM),
+                        ("add_220", X), ("arg583_1", IDS)],
     "v6/28b45679fca1": [("mm_223", MM), ("add_62_recomputed", X), ("mm_226", MM), ("view_3253", W)],
     "v8/622c35f5d1c6": [("div", (F32, (), ())), ("_log_softmax", (F32, (8192, 128256), (128256, 1))),
                         ("view_805", (I64, (8192,), (1,))), ("getitem_419", (F32, (), ()))],
@@ -103,15 +119,22 @@ SIGNATURES = {
 SAME_SIGNATURE = {
     "v1/1e49beb8a123": "v7/1e49beb8a123", "v1/363b7b58c971": "v4/363b7b58c971", "v1/65b4b565ed67": "v4/65b4b565ed67",
     "v1/80ad8e737b06": "v4/80ad8e737b06", "v1/9c745ea697a7": "v4/9c745ea697a7", "v1/c72358b8111e": "v4/c72358b8111e",
-    "v2/1e49beb8a123": "v7/1e49beb8a123", "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67",
-    "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/c72358b8111e": "v4/c72358b8111e",
-    "v3/1e49beb8a123": "v7/1e49beb8a123", "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67",
-    "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e",
-    "v4/1e49beb8a123": "v7/1e49beb8a123", "v5/1e49beb8a123": "v7/1e49beb8a123", "v6/1e49beb8a123": "v7/1e49beb8a123",
+    "v2/18b859c50de2": "v1/18b859c50de2", "v2/1e49beb8a123": "v7/1e49beb8a123", "v2/2a844503364a": "v1/2a844503364a",
+    "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67", "v2/680e4c57cdc8": "v1/680e4c57cdc8",
+    "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/84496d824942": "v1/84496d824942", "v2/84c0a03c4374": "v1/84c0a03c4374",
+    "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/c72358b8111e": "v4/c72358b8111e", "v2/f7ad66842c19": "v1/f7ad66842c19",
+    "v3/18b859c50de2": "v1/18b859c50de2", "v3/1e49beb8a123": "v7/1e49beb8a123", "v3/2a844503364a": "v1/2a844503364a",
+    "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67", "v3/680e4c57cdc8": "v1/680e4c57cdc8",
+    "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/84496d824942": "v1/84496d824942", "v3/84c0a03c4374": "v1/84c0a03c4374",
+    "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e", "v3/f7ad66842c19": "v1/f7ad66842c19",
+    "v4/18b859c50de2": "v1/18b859c50de2", "v4/1e49beb8a123": "v7/1e49beb8a123", "v4/2a844503364a": "v1/2a844503364a",
+    "v4/680e4c57cdc8": "v1/680e4c57cdc8", "v4/84496d824942": "v1/84496d824942", "v4/84c0a03c4374": "v1/84c0a03c4374",
+    "v4/f7ad66842c19": "v1/f7ad66842c19", "v5/1e49beb8a123": "v7/1e49beb8a123", "v6/1e49beb8a123": "v7/1e49beb8a123",
     "v6/215dd2e6a519": "v7/215dd2e6a519", "v6/622c35f5d1c6": "v8/622c35f5d1c6", "v6/71f1d2c9f38b": "v8/71f1d2c9f38b",
-    "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968", "v7/385e1beb9bb9": "v8/385e1beb9bb9",
-    "v7/493cad38cac9": "v8/493cad38cac9", "v7/622c35f5d1c6": "v8/622c35f5d1c6", "v7/8e33a91b7364": "v8/8e33a91b7364",
-    "v7/ac3fb0b7281f": "v6/ac3fb0b7281f", "v7/f4e9e58fef73": "v8/f4e9e58fef73", "v8/e29b92927600": "v7/e29b92927600",
+    "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968", "v6/c68dae22972b": "v5/c68dae22972b",
+    "v7/385e1beb9bb9": "v8/385e1beb9bb9", "v7/493cad38cac9": "v8/493cad38cac9", "v7/622c35f5d1c6": "v8/622c35f5d1c6",
+    "v7/8e33a91b7364": "v8/8e33a91b7364", "v7/ac3fb0b7281f": "v6/ac3fb0b7281f", "v7/f4e9e58fef73": "v8/f4e9e58fef73",
+    "v8/e29b92927600": "v7/e29b92927600",
 }
 for _a, _c in SAME_SIGNATURE.items():
     SIGNATURES[_a] = SIGNATURES[_c]
@@ -130,6 +153,9 @@ def test_fragment_signature_and_inputs(fid):
     assert len(inputs) == len(params)
     for t, (name, (dt, shape, stride)) in zip(inputs, SIGNATURES[fid]):
         assert (t.dtype, tuple(t.shape), t.stride()) == (dt, shape, stride), name
+        # meta tensors skip as_strided's bounds check: every view fits its storage
+        last = t.storage_offset() + sum((n - 1) * st for n, st in zip(t.shape, t.stride()))
+        assert t.numel() == 0 or (last + 1) * t.element_size() <= t.untyped_storage().nbytes(), name
     with pytest.raises(RuntimeError, match="GPU|device"):
         mod.kernel_function(*inputs)
 
@@ -165,3 +191,8 @@ def test_aten_drop_ins_refuse_cpu_tensors():
         kp.aten._fused_rms_norm(x, [8], torch.ones(8, dtype=BF), 1e-5)
     with pytest.raises(RuntimeError, match="GPU tensor"):
         kp.aten.embedding(torch.zeros(10, 8, dtype=BF), torch.zeros(3, dtype=I64))
+
+
+def test_equivalent_fragments_reexport_their_canonical():
+    for alias, canon in {**fr.SAME_AS, **fr.EQUIVALENT}.items():
+        assert fr.load(alias).kernel_function is fr.load(canon).kernel_function, alias
