@@ -57,7 +57,7 @@ const char* kp_last_error_message(void);
  * completion: the row kernel of the RMSNorm entry points (and of
  * kp_embedding_rmsnorm_fwd_bf16), the gather kernel
  * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
- * the kernel of kp_rope_bf16, the copy kernel of kp_unshard_bf16, the
+ * the kernel of kp_rope_bf16 (and of kp_rope_c64), the copy kernel of kp_unshard_bf16, the
  * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16 / kp_silu_bf16 / kp_swiglu_fwd_bwd_bf16, the row kernel of
  * kp_cross_entropy_fwd_bf16, the kernel of kp_cross_entropy_bwd_bf16, the row
  * kernel of kp_cross_entropy_fwd_bwd_bf16 and
@@ -242,6 +242,31 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
                  int pairing, double theta,
                  const float* freqs_cis, int64_t freq_rows, int64_t freq_row_stride,
                  int conj, int out_f32_mask, int32_t* error_flag, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Rotary position embedding on complex64 data: q and k already viewed as
+ * complex (fp32 (re, im) pairs), multiplied by a complex64 table row per
+ * position, complex64 out:
+ *   out[b, s, h, i] = x[b, s, h, i] * t[p, i]   (* conj(t[p, i]) when conj != 0)
+ *   (a + bi)(c + di) = (ac - bd) + (ad + bc)i in fp32.
+ *
+ * Replaces the index -> mul (-> mul) regions at
+ *   v1/075cb40f3d5d/problem.py:8-27   (q and k, table gathered by position ids)
+ *   v1/9cd8f72e74ce/problem.py:8-17   (q, table row s for position s, a conjugated table)
+ *   v1/d7efc428b2f5/problem.py:8-406  (33 q / k pairs, one gathered table)
+ * Tensor i (i = 0, 1; tensor 1 optional, x1 == NULL): x_i, out_i complex64
+ *   [B, S, H_i, P] with strides {b, s, h} in complex elements and unit stride
+ *   on P.  positions as in kp_rope_bf16 (NULL: position of (b, s) is s).
+ *   freqs_cis: complex64 [freq_rows, >= P], row stride in complex elements.
+ * A position outside [0, freq_rows) reads nothing: its output is zero and
+ * *error_flag (if non-NULL) is set to 1.
+ */
+int kp_rope_c64(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides, const int64_t* out0_strides,
+                const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,
+                int64_t B, int64_t S, int64_t P,
+                const void* positions, int pos_bytes, int64_t pos_stride_b, int64_t pos_stride_s,
+                const float* freqs_cis, int64_t freq_rows, int64_t freq_row_stride, int conj,
+                int32_t* error_flag, void* stream);
 
 /* ------------------------------------------------------------------------
  * FSDP parameter unshard: n_seg (<= 16) column ranges of a row-strided bf16

@@ -25,6 +25,7 @@ from .fused import (
     rms_norm,
     rms_norm_backward,
     rope,
+    rope_complex,
     set_index_checking,
     silu,
     swiglu,
@@ -48,6 +49,7 @@ __all__ = [
     "rms_norm",
     "rms_norm_backward",
     "rope",
+    "rope_complex",
     "set_index_checking",
     "silu",
     "swiglu",

@@ -83,6 +83,8 @@ SIGNATURES = {
         [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64,
          i32, f64, vp, i64, i64, i32, i32, vp, vp],
     ),
+    "kp_rope_c64": (i32, [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64, vp, i64, i64,
+                          i32, vp, vp]),
     "kp_unshard_bf16": (i32, [vp, i64, i64, pi64, pi64, pvp, i32, vp]),
     "kp_stream_probe": (i32, [pvp, i32, i64, pvp, i32, i64, i32, vp]),
     "kp_embedding_rmsnorm_fwd_bf16": (i32, [vp, i64, i64, vp, i32, i64, vp, i64, i64, vp, i64, vp, i64, vp, i64, f32,

@@ -355,6 +355,27 @@ def _rope_strides(t: torch.Tensor):
     return t, [t.stride(0), t.stride(1), t.stride(2)]
 
 
+def _positions(positions: Optional[torch.Tensor], B: int, S: int, dev):
+    """(pointer, bytes per id, stride over b, stride over s) of a [B, S],
+    [1, S] or [S] integer position tensor, or no positions (None)."""
+    if positions is None:
+        return None, 0, 0, 0
+    if positions.device != dev or positions.dtype not in (torch.int32, torch.int64):
+        raise RuntimeError("rope: positions must be an int32/int64 tensor on the same device")
+    if positions.dim() == 1:
+        if positions.shape[0] != S:
+            raise RuntimeError("rope: 1-D positions must have S entries")
+        psb, pss = 0, positions.stride(0)
+    elif positions.dim() == 2:
+        if positions.shape[1] != S or positions.shape[0] not in (1, B):
+            raise RuntimeError("rope: 2-D positions must be [B, S] or [1, S]")
+        psb = positions.stride(0) if positions.shape[0] == B else 0
+        pss = positions.stride(1)
+    else:
+        raise RuntimeError("rope: positions must be 1-D or 2-D")
+    return positions.data_ptr(), positions.element_size(), psb, pss
+
+
 def rope(
     q: torch.Tensor,
     k: Optional[torch.Tensor] = None,
@@ -396,22 +417,7 @@ def rope(
         k_out = torch.empty(k.shape, dtype=k_dtype, device=dev)
         k_args = [k.data_ptr(), k_out.data_ptr(), k.shape[2], L.i64_array(ks),
                   L.i64_array(list(k_out.stride()[:3]))]
-    pos_ptr, pos_bytes, psb, pss = None, 0, 0, 0
-    if positions is not None:
-        if positions.device != dev or positions.dtype not in (torch.int32, torch.int64):
-            raise RuntimeError("rope: positions must be an int32/int64 tensor on the same device")
-        if positions.dim() == 1:
-            if positions.shape[0] != S:
-                raise RuntimeError("rope: 1-D positions must have S entries")
-            psb, pss = 0, positions.stride(0)
-        elif positions.dim() == 2:
-            if positions.shape[1] != S or positions.shape[0] not in (1, B):
-                raise RuntimeError("rope: 2-D positions must be [B, S] or [1, S]")
-            psb = positions.stride(0) if positions.shape[0] == B else 0
-            pss = positions.stride(1)
-        else:
-            raise RuntimeError("rope: positions must be 1-D or 2-D")
-        pos_ptr, pos_bytes = positions.data_ptr(), positions.element_size()
+    pos_ptr, pos_bytes, psb, pss = _positions(positions, B, S, dev)
     mode = {"half": L.KP_ROPE_HALF, "interleaved": L.KP_ROPE_INTERLEAVED}.get(pairing)
     if mode is None:
         raise ValueError(f"rope: pairing must be 'half' or 'interleaved', got {pairing!r}")
@@ -438,6 +444,46 @@ def rope(
         _ptr(flag), _stream(dev),
     )
     _raise_if_flagged(flag, "rope")
+    return q_out, k_out
+
+
+def rope_complex(q: torch.Tensor, k: Optional[torch.Tensor] = None, *, freqs_cis: torch.Tensor,
+                 positions: Optional[torch.Tensor] = None, conj: bool = False):
+    """q (and k) already viewed as complex64 [B, S, H, P] times the complex64
+    table ``freqs_cis`` (last dim P, row p for position p; a [1, S, 1, P] or
+    [S, P] table), in fp32 -- the index -> mul regions of
+    v1/075cb40f3d5d/problem.py:8-27.  positions: [B, S], [1, S] or [S]
+    integers, default s.  conj=True multiplies by the conjugate table.
+    Returns contiguous complex64 (q_out, k_out)."""
+    _need_gpu("rope_complex q", q, torch.complex64)
+    dev = q.device
+    if q.dim() != 4:
+        raise RuntimeError(f"rope_complex: expected [B, S, H, P], got shape {tuple(q.shape)}")
+    if q.shape[3] > 1 and q.stride(3) != 1:
+        q = q.contiguous()
+    B, S, Hq, P = q.shape
+    q_out = torch.empty(q.shape, dtype=torch.complex64, device=dev)
+    k_out = None
+    k_args = [None, None, 0, None, None]
+    if k is not None:
+        _need_gpu("rope_complex k", k, torch.complex64)
+        if k.dim() != 4 or k.shape[0] != B or k.shape[1] != S or k.shape[3] != P:
+            raise RuntimeError("rope_complex: q and k must agree on B, S and P")
+        if k.shape[3] > 1 and k.stride(3) != 1:
+            k = k.contiguous()
+        k_out = torch.empty(k.shape, dtype=torch.complex64, device=dev)
+        k_args = [k.data_ptr(), k_out.data_ptr(), k.shape[2], L.i64_array(list(k.stride()[:3])),
+                  L.i64_array(list(k_out.stride()[:3]))]
+    if freqs_cis.device != dev or freqs_cis.dtype != torch.complex64 or freqs_cis.shape[-1] != P:
+        raise RuntimeError(f"rope_complex: freqs_cis must be complex64 on the same device with last dim {P}")
+    fc, frs, frows = _as_rows(freqs_cis, P)
+    pos_ptr, pos_bytes, psb, pss = _positions(positions, B, S, dev)
+    flag = _flag(dev)
+    if B * S:
+        L.call("kp_rope_c64", q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(list(q.stride()[:3])),
+               L.i64_array(list(q_out.stride()[:3])), *k_args, B, S, P, pos_ptr, pos_bytes, psb, pss,
+               torch.view_as_real(fc).data_ptr(), frows, frs, 1 if conj else 0, _ptr(flag), _stream(dev))
+    _raise_if_flagged(flag, "rope_complex")
     return q_out, k_out
 
 

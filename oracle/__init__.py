@@ -31,6 +31,9 @@ rope (theta)           ``torch.polar`` angles in fp64 (pos = 0 identity, norm
                        preservation, conj inverse), rotate-half ==
                        interleaved up to the (2i, 2i+1) <-> (i, i + D/2)
                        permutation.
+rope_c64               torch complex128 multiply (library), position 0 with
+                       a unit table is the identity, unit-modulus rows keep
+                       |x|, conj undoes the rotation.
 swiglu_fwd             torch CPU eager ``silu`` * b, fp64 ``x * expit(x)``
                        (scipy), closed forms (silu(0) = 0, silu(x) -
                        silu(-x) = x, saturation), every bf16 input value.
@@ -267,6 +270,21 @@ def rope(x: np.ndarray, pos: Optional[np.ndarray] = None, *, pairing: str = "hal
     if bad < 0:
         raise MemoryError("kpo_rope")
     return out
+
+
+def rope_c64(x: np.ndarray, table: np.ndarray, positions=None, conj: bool = False) -> np.ndarray:
+    """Complex RoPE of the v1 captures (v1/075cb40f3d5d/problem.py:14-23):
+    x complex [B, S, H, P] times table[p] (p = positions[b, s], default s),
+    conjugated on request, in complex128 (exact products of the complex64
+    inputs, one rounding per component)."""
+    x = np.asarray(x).astype(np.complex128)
+    t = np.asarray(table).astype(np.complex128).reshape(-1, x.shape[-1])
+    B, S = x.shape[:2]
+    p = np.broadcast_to(np.arange(S), (B, S)) if positions is None else np.broadcast_to(np.asarray(positions), (B, S))
+    rows = t[p]  # [B, S, P]
+    if conj:
+        rows = np.conj(rows)
+    return x * rows[:, :, None, :]
 
 
 # ---------------------------------------------------------------- SwiGLU

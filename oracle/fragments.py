@@ -207,6 +207,18 @@ def _rope_bwd_qkv(c62, c63, gq, gk, gv):  # v5/a1bb72d946b0/problem.py:16-85, v4
     return q, k, aten.t.default(v)
 
 
+def _rope_c64_qk(pos, table, *xs):      # v1/075cb40f3d5d/problem.py:14-27, v1/d7efc428b2f5:14-507
+    out = []
+    for i in range(0, len(xs), 2):
+        t = _gathered_table(pos, table)
+        out += [aten.mul.Tensor(xs[i], t), aten.mul.Tensor(xs[i + 1], t)]
+    return tuple(out)
+
+
+def _rope_c64_bwd(table, x):             # v1/9cd8f72e74ce/problem.py:12-16, v1/f23f9bb4567a:12-16
+    return aten.mul.Tensor(x, aten.clone.default(table))
+
+
 def _swiglu_fwd(mm4, mm5):               # v8/c68dae22972b/problem.py:15-28
     a = aten._unsafe_view.default(mm4, [1, *mm4.shape])
     b = aten._unsafe_view.default(mm5, [1, *mm5.shape])
@@ -336,6 +348,10 @@ _FRAGMENTS = {
     "v5/a1bb72d946b0": _rope_bwd_qkv,
     "v4/a1318bc813d2": _rope_bwd_qkv,
     "v6/c8c60d8f7015": _rope_qk_fwd,
+    "v1/075cb40f3d5d": _rope_c64_qk,
+    "v1/d7efc428b2f5": _rope_c64_qk,
+    "v1/9cd8f72e74ce": _rope_c64_bwd,
+    "v1/f23f9bb4567a": _rope_c64_bwd,
     "v5/c68dae22972b": _swiglu_fwd,
     "v8/c68dae22972b": _swiglu_fwd,
     "v8/385e1beb9bb9": _swiglu_bwd,
@@ -371,22 +387,23 @@ _FRAGMENTS = {
 _SAME_OPS = {
     "v1/1e49beb8a123": "v7/1e49beb8a123", "v1/363b7b58c971": "v4/363b7b58c971", "v1/65b4b565ed67": "v4/65b4b565ed67",
     "v1/80ad8e737b06": "v4/80ad8e737b06", "v1/9c745ea697a7": "v4/9c745ea697a7", "v1/c72358b8111e": "v4/c72358b8111e",
-    "v2/18b859c50de2": "v1/18b859c50de2", "v2/1e49beb8a123": "v7/1e49beb8a123", "v2/2a844503364a": "v1/2a844503364a",
-    "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67", "v2/680e4c57cdc8": "v1/680e4c57cdc8",
-    "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/84496d824942": "v1/84496d824942", "v2/84c0a03c4374": "v1/84c0a03c4374",
-    "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/c72358b8111e": "v4/c72358b8111e", "v2/f7ad66842c19": "v1/f7ad66842c19",
-    "v3/18b859c50de2": "v1/18b859c50de2", "v3/1e49beb8a123": "v7/1e49beb8a123", "v3/2a844503364a": "v1/2a844503364a",
-    "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67", "v3/680e4c57cdc8": "v1/680e4c57cdc8",
-    "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/84496d824942": "v1/84496d824942", "v3/84c0a03c4374": "v1/84c0a03c4374",
-    "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e", "v3/f7ad66842c19": "v1/f7ad66842c19",
-    "v4/18b859c50de2": "v1/18b859c50de2", "v4/1e49beb8a123": "v7/1e49beb8a123", "v4/2a844503364a": "v1/2a844503364a",
-    "v4/680e4c57cdc8": "v1/680e4c57cdc8", "v4/84496d824942": "v1/84496d824942", "v4/84c0a03c4374": "v1/84c0a03c4374",
-    "v4/f7ad66842c19": "v1/f7ad66842c19", "v5/1e49beb8a123": "v7/1e49beb8a123", "v6/1e49beb8a123": "v7/1e49beb8a123",
-    "v6/215dd2e6a519": "v7/215dd2e6a519", "v6/622c35f5d1c6": "v8/622c35f5d1c6", "v6/71f1d2c9f38b": "v8/71f1d2c9f38b",
-    "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968", "v6/c68dae22972b": "v5/c68dae22972b",
-    "v7/385e1beb9bb9": "v8/385e1beb9bb9", "v7/493cad38cac9": "v8/493cad38cac9", "v7/622c35f5d1c6": "v8/622c35f5d1c6",
-    "v7/8e33a91b7364": "v8/8e33a91b7364", "v7/ac3fb0b7281f": "v6/ac3fb0b7281f", "v7/f4e9e58fef73": "v8/f4e9e58fef73",
-    "v8/e29b92927600": "v7/e29b92927600",
+    "v2/075cb40f3d5d": "v1/075cb40f3d5d", "v2/18b859c50de2": "v1/18b859c50de2", "v2/1e49beb8a123": "v7/1e49beb8a123",
+    "v2/2a844503364a": "v1/2a844503364a", "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67",
+    "v2/680e4c57cdc8": "v1/680e4c57cdc8", "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/84496d824942": "v1/84496d824942",
+    "v2/84c0a03c4374": "v1/84c0a03c4374", "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/9cd8f72e74ce": "v1/9cd8f72e74ce",
+    "v2/c72358b8111e": "v4/c72358b8111e", "v2/d7efc428b2f5": "v1/d7efc428b2f5", "v2/f23f9bb4567a": "v1/f23f9bb4567a",
+    "v2/f7ad66842c19": "v1/f7ad66842c19", "v3/18b859c50de2": "v1/18b859c50de2", "v3/1e49beb8a123": "v7/1e49beb8a123",
+    "v3/2a844503364a": "v1/2a844503364a", "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67",
+    "v3/680e4c57cdc8": "v1/680e4c57cdc8", "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/84496d824942": "v1/84496d824942",
+    "v3/84c0a03c4374": "v1/84c0a03c4374", "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e",
+    "v3/f7ad66842c19": "v1/f7ad66842c19", "v4/18b859c50de2": "v1/18b859c50de2", "v4/1e49beb8a123": "v7/1e49beb8a123",
+    "v4/2a844503364a": "v1/2a844503364a", "v4/680e4c57cdc8": "v1/680e4c57cdc8", "v4/84496d824942": "v1/84496d824942",
+    "v4/84c0a03c4374": "v1/84c0a03c4374", "v4/f7ad66842c19": "v1/f7ad66842c19", "v5/1e49beb8a123": "v7/1e49beb8a123",
+    "v6/1e49beb8a123": "v7/1e49beb8a123", "v6/215dd2e6a519": "v7/215dd2e6a519", "v6/622c35f5d1c6": "v8/622c35f5d1c6",
+    "v6/71f1d2c9f38b": "v8/71f1d2c9f38b", "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968",
+    "v6/c68dae22972b": "v5/c68dae22972b", "v7/385e1beb9bb9": "v8/385e1beb9bb9", "v7/493cad38cac9": "v8/493cad38cac9",
+    "v7/622c35f5d1c6": "v8/622c35f5d1c6", "v7/8e33a91b7364": "v8/8e33a91b7364", "v7/ac3fb0b7281f": "v6/ac3fb0b7281f",
+    "v7/f4e9e58fef73": "v8/f4e9e58fef73", "v8/e29b92927600": "v7/e29b92927600",
 }
 for _alias, _canon in _SAME_OPS.items():
     _FRAGMENTS[_alias] = _FRAGMENTS[_canon]

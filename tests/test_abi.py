@@ -176,3 +176,18 @@ def test_stream_probe_validation(lib):
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, 4, None)
     _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 1, 64, 2, None)
     assert lib.kp_stream_probe(None, 0, 0, L.ptr_array([32]), 1, 0, 1, None) == L.KP_OK  # nothing to stream
+
+
+def test_rope_c64_validation(lib):
+    st = L.i64_array([0, 0, 0])
+    fn = "kp_rope_c64"
+    _expect(lib, L.KP_EINVAL, fn, 16, 32, 1, st, st, None, None, 0, None, None, 1, 1, 8, None, 0, 0, 0, None, 4, 8, 0,
+            None, None)  # no table
+    _expect(lib, L.KP_EINVAL, fn, 16, 32, 1, st, st, None, None, 0, None, None, 1, 1, 8, None, 0, 0, 0, 64, 4, 4, 0,
+            None, None)  # table row stride < P
+    _expect(lib, L.KP_EINVAL, fn, 16, 32, 1, st, st, None, None, 0, None, None, 1, 1, 8, 48, 2, 0, 0, 64, 4, 8, 0,
+            None, None)  # 2-byte positions
+    _expect(lib, L.KP_EINVAL, fn, None, 32, 1, st, st, None, None, 0, None, None, 1, 1, 8, None, 0, 0, 0, 64, 4, 8, 0,
+            None, None)  # no x
+    assert lib.kp_rope_c64(16, 32, 1, st, st, None, None, 0, None, None, 0, 1, 8, None, 0, 0, 0, 64, 4, 8, 0, None,
+                           None) == L.KP_OK  # B = 0

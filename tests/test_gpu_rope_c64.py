@@ -1,0 +1,90 @@
+"""GPU parity of the complex64 RoPE kernel (kp_rope_c64: the v1 captures
+v1/075cb40f3d5d, v1/9cd8f72e74ce, v1/d7efc428b2f5) with the complex128 CPU
+oracle -- 16-byte path (contiguous and head-strided views) and 8-byte path
+(odd P, views starting one complex value in), gathered and per-position
+tables, the conjugate table, out-of-range positions -- and with torch-ROCm's
+complex multiply at the fragments' full shape."""
+import numpy as np
+import pytest
+import torch
+
+import kernelproblems_amd as kp
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _check(out, exact, x, t_rows):
+    """Each fp32 component within 2^-22 (|ac| + |bd|) of the complex128 product."""
+    o = out.cpu().numpy().astype(np.complex128)
+    bound = 2.0**-22 * (np.abs(x.real * t_rows.real) + np.abs(x.imag * t_rows.imag) +
+                        np.abs(x.real * t_rows.imag) + np.abs(x.imag * t_rows.real)) + 1e-30
+    assert np.all(np.abs(o.real - exact.real) <= bound) and np.all(np.abs(o.imag - exact.imag) <= bound)
+
+
+def _c64(shape, g):
+    return torch.randn(shape, dtype=torch.complex64, generator=g)
+
+
+@pytest.mark.parametrize("kind", ["contig", "heads_strided", "odd_p", "offset"])
+@pytest.mark.parametrize("gather", [False, True])
+@pytest.mark.parametrize("conj", [False, True])
+def test_matches_oracle(gpu, kind, gather, conj):
+    print(f"[rope c64] {kind} gather={gather} conj={conj}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    B, S, Hq, Hk = 2, 37, 5, 3
+    P = 63 if kind == "odd_p" else 64
+    rows = 50
+    if kind == "heads_strided":       # [B, S, H, P] views of [B, S, H + 2, P]
+        q = _c64((B, S, Hq + 2, P), g).to(gpu)[:, :, 1:1 + Hq]
+        k = _c64((B, S, Hk + 2, P), g).to(gpu)[:, :, :Hk]
+    elif kind == "offset":            # starts one complex value in: the 8-byte path
+        q = _c64((B, S, Hq, P + 1), g).to(gpu)[..., 1:]
+        k = _c64((B, S, Hk, P + 1), g).to(gpu)[..., 1:]
+    else:
+        q, k = _c64((B, S, Hq, P), g).to(gpu), _c64((B, S, Hk, P), g).to(gpu)
+    table = _c64((rows, P), g).to(gpu)
+    pos = torch.randint(0, rows, (B, S), generator=g) if gather else None
+    qo, ko = kp.rope_complex(q, k, freqs_cis=table, positions=None if pos is None else pos.to(gpu), conj=conj)
+    tn = table.cpu().numpy()
+    pn = None if pos is None else pos.numpy()
+    for x, o in ((q, qo), (k, ko)):
+        xn = x.cpu().numpy()
+        exact = oracle.rope_c64(xn, tn, pn, conj=conj)
+        p_ = np.broadcast_to(np.arange(S), (B, S)) if pn is None else pn
+        rows_ = tn[p_][:, :, None, :]
+        _check(o, exact, xn.astype(np.complex128), (np.conj(rows_) if conj else rows_).astype(np.complex128))
+
+
+def test_out_of_range_positions_and_empty(gpu):
+    q = torch.randn(1, 4, 2, 8, dtype=torch.complex64, device=gpu)
+    t = torch.randn(3, 8, dtype=torch.complex64, device=gpu)
+    pos = torch.tensor([[0, 3, 1, -1]], device=gpu)
+    with pytest.raises(IndexError):
+        kp.rope_complex(q, freqs_cis=t, positions=pos)
+    kp.set_index_checking(False)
+    try:
+        qo, _ = kp.rope_complex(q, freqs_cis=t, positions=pos)
+    finally:
+        kp.set_index_checking(True)
+    assert not qo[0, 1].any() and not qo[0, 3].any()
+    exact = oracle.rope_c64(q[:, [0, 2]].cpu().numpy(), t.cpu().numpy(), np.array([[0, 1]]))
+    assert np.allclose(qo[:, [0, 2]].cpu().numpy(), exact, rtol=1e-6, atol=1e-6)
+    e = torch.empty((0, 4, 2, 8), dtype=torch.complex64, device=gpu)
+    assert kp.rope_complex(e, freqs_cis=t)[0].shape == e.shape
+
+
+def test_full_shape_against_torch(gpu):
+    """v1/075cb40f3d5d at its shape: q [1, 8192, 32, 64], k [1, 8192, 8, 64]
+    against torch-ROCm's complex64 multiply of the gathered rows."""
+    print("[rope c64 eager] full shape", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(5)
+    q = torch.randn(1, 8192, 32, 64, dtype=torch.complex64, device=gpu, generator=g)
+    k = torch.randn(1, 8192, 8, 64, dtype=torch.complex64, device=gpu, generator=g)
+    t = torch.randn(8192, 64, dtype=torch.complex64, device=gpu, generator=g)
+    pos = torch.randint(0, 100, (1, 8192), dtype=torch.int32, device=gpu, generator=g)
+    qo, ko = kp.rope_complex(q, k, freqs_cis=t, positions=pos)
+    rows = t[pos[0].long()].view(1, 8192, 1, 64)
+    for o, ref in ((qo, q * rows), (ko, k * rows)):
+        d = torch.view_as_real(o) - torch.view_as_real(ref)
+        assert float(d.abs().max()) <= 1e-5 * float(torch.view_as_real(ref).abs().max())

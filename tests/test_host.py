@@ -26,6 +26,33 @@ FLAT_LAYER = (BF, (218112000,), (1,))
 FFN = (BF, (8192, 14336), (14336, 1))
 FFN3 = (BF, (1, 8192, 14336), (117440512, 14336, 1))
 FFNW = (BF, (8, 7340032), (27264000, 1))
+CQ = (C64, (1, 8192, 32, 64), (16777216, 2048, 64, 1))
+CK = (C64, (1, 8192, 8, 64), (4194304, 512, 64, 1))
+# v1/d7efc428b2f5/problem.py:10-77: the 33 q / k complex views, q first in each pair
+D7EFC_PAIRS = (
+    "view_as_complex_62", "view_as_complex_63", "view_as_complex_62_recomputed",
+    "view_as_complex_63_recomputed", "view_as_complex_60_recomputed", "view_as_complex_61_recomputed",
+    "view_as_complex_58_recomputed", "view_as_complex_59_recomputed", "view_as_complex_56_recomputed",
+    "view_as_complex_57_recomputed", "view_as_complex_54_recomputed", "view_as_complex_55_recomputed",
+    "view_as_complex_52_recomputed", "view_as_complex_53_recomputed", "view_as_complex_50_recomputed",
+    "view_as_complex_51_recomputed", "view_as_complex_48_recomputed", "view_as_complex_49_recomputed",
+    "view_as_complex_46_recomputed", "view_as_complex_47_recomputed", "view_as_complex_44_recomputed",
+    "view_as_complex_45_recomputed", "view_as_complex_42_recomputed", "view_as_complex_43_recomputed",
+    "view_as_complex_40_recomputed", "view_as_complex_41_recomputed", "view_as_complex_38_recomputed",
+    "view_as_complex_39_recomputed", "view_as_complex_36_recomputed", "view_as_complex_37_recomputed",
+    "view_as_complex_34_recomputed", "view_as_complex_35_recomputed", "view_as_complex_32_recomputed",
+    "view_as_complex_33_recomputed", "view_as_complex_30_recomputed", "view_as_complex_31_recomputed",
+    "view_as_complex_28_recomputed", "view_as_complex_29_recomputed", "view_as_complex_26_recomputed",
+    "view_as_complex_27_recomputed", "view_as_complex_24_recomputed", "view_as_complex_25_recomputed",
+    "view_as_complex_22_recomputed", "view_as_complex_23_recomputed", "view_as_complex_20_recomputed",
+    "view_as_complex_21_recomputed", "view_as_complex_18_recomputed", "view_as_complex_19_recomputed",
+    "view_as_complex_16_recomputed", "view_as_complex_17_recomputed", "view_as_complex_14_recomputed",
+    "view_as_complex_15_recomputed", "view_as_complex_12_recomputed", "view_as_complex_13_recomputed",
+    "view_as_complex_10_recomputed", "view_as_complex_11_recomputed", "view_as_complex_8_recomputed",
+    "view_as_complex_9_recomputed", "view_as_complex_6_recomputed", "view_as_complex_7_recomputed",
+    "view_as_complex_4_recomputed", "view_as_complex_5_recomputed", "view_as_complex_2_recomputed",
+    "view_as_complex_3_recomputed", "view_as_complex_recomputed", "view_as_complex_1_recomputed",
+)
 GQ = (BF, (1, 32, 8192, 128), (33554432, 128, 4096, 1))
 GK = (BF, (1, 8, 8192, 128), (8388608, 128, 1024, 1))
 
@@ -70,6 +97,11 @@ SIGNATURES = {
                         ("getitem_643", GK)],
     "v4/a1318bc813d2": [("_conj_62", FC), ("_conj_63", FC), ("getitem_641", GQ), ("getitem_642", GK),
                         ("getitem_643", GK)],
+    "v1/075cb40f3d5d": [("arg586_1", POS), ("arg582_1", TAB), ("view_as_complex_60", CQ), ("view_as_complex_61", CK)],
+    "v1/9cd8f72e74ce": [("_conj_63", FC), ("view_as_complex_127", CQ)],
+    "v1/f23f9bb4567a": [("_conj_62", FC), ("view_as_complex_126", CK)],
+    "v1/d7efc428b2f5": [("arg586_1", POS), ("arg582_1", TAB)] + [
+        (n, CQ if i % 2 == 0 else CK) for i, n in enumerate(D7EFC_PAIRS)],
     "v8/c68dae22972b": [("mm_4", FFN), ("mm_5", FFN)],
     "v8/385e1beb9bb9": [("mm_662", FFN), ("silu_recomputed", FFN3), ("_unsafe_view_5_recomputed", FFN3),
                         ("_unsafe_view_4_recomputed", FFN3)],
@@ -119,22 +151,23 @@ SIGNATURES = {
 SAME_SIGNATURE = {
     "v1/1e49beb8a123": "v7/1e49beb8a123", "v1/363b7b58c971": "v4/363b7b58c971", "v1/65b4b565ed67": "v4/65b4b565ed67",
     "v1/80ad8e737b06": "v4/80ad8e737b06", "v1/9c745ea697a7": "v4/9c745ea697a7", "v1/c72358b8111e": "v4/c72358b8111e",
-    "v2/18b859c50de2": "v1/18b859c50de2", "v2/1e49beb8a123": "v7/1e49beb8a123", "v2/2a844503364a": "v1/2a844503364a",
-    "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67", "v2/680e4c57cdc8": "v1/680e4c57cdc8",
-    "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/84496d824942": "v1/84496d824942", "v2/84c0a03c4374": "v1/84c0a03c4374",
-    "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/c72358b8111e": "v4/c72358b8111e", "v2/f7ad66842c19": "v1/f7ad66842c19",
-    "v3/18b859c50de2": "v1/18b859c50de2", "v3/1e49beb8a123": "v7/1e49beb8a123", "v3/2a844503364a": "v1/2a844503364a",
-    "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67", "v3/680e4c57cdc8": "v1/680e4c57cdc8",
-    "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/84496d824942": "v1/84496d824942", "v3/84c0a03c4374": "v1/84c0a03c4374",
-    "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e", "v3/f7ad66842c19": "v1/f7ad66842c19",
-    "v4/18b859c50de2": "v1/18b859c50de2", "v4/1e49beb8a123": "v7/1e49beb8a123", "v4/2a844503364a": "v1/2a844503364a",
-    "v4/680e4c57cdc8": "v1/680e4c57cdc8", "v4/84496d824942": "v1/84496d824942", "v4/84c0a03c4374": "v1/84c0a03c4374",
-    "v4/f7ad66842c19": "v1/f7ad66842c19", "v5/1e49beb8a123": "v7/1e49beb8a123", "v6/1e49beb8a123": "v7/1e49beb8a123",
-    "v6/215dd2e6a519": "v7/215dd2e6a519", "v6/622c35f5d1c6": "v8/622c35f5d1c6", "v6/71f1d2c9f38b": "v8/71f1d2c9f38b",
-    "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968", "v6/c68dae22972b": "v5/c68dae22972b",
-    "v7/385e1beb9bb9": "v8/385e1beb9bb9", "v7/493cad38cac9": "v8/493cad38cac9", "v7/622c35f5d1c6": "v8/622c35f5d1c6",
-    "v7/8e33a91b7364": "v8/8e33a91b7364", "v7/ac3fb0b7281f": "v6/ac3fb0b7281f", "v7/f4e9e58fef73": "v8/f4e9e58fef73",
-    "v8/e29b92927600": "v7/e29b92927600",
+    "v2/075cb40f3d5d": "v1/075cb40f3d5d", "v2/18b859c50de2": "v1/18b859c50de2", "v2/1e49beb8a123": "v7/1e49beb8a123",
+    "v2/2a844503364a": "v1/2a844503364a", "v2/363b7b58c971": "v4/363b7b58c971", "v2/65b4b565ed67": "v4/65b4b565ed67",
+    "v2/680e4c57cdc8": "v1/680e4c57cdc8", "v2/80ad8e737b06": "v4/80ad8e737b06", "v2/84496d824942": "v1/84496d824942",
+    "v2/84c0a03c4374": "v1/84c0a03c4374", "v2/9c745ea697a7": "v4/9c745ea697a7", "v2/9cd8f72e74ce": "v1/9cd8f72e74ce",
+    "v2/c72358b8111e": "v4/c72358b8111e", "v2/d7efc428b2f5": "v1/d7efc428b2f5", "v2/f23f9bb4567a": "v1/f23f9bb4567a",
+    "v2/f7ad66842c19": "v1/f7ad66842c19", "v3/18b859c50de2": "v1/18b859c50de2", "v3/1e49beb8a123": "v7/1e49beb8a123",
+    "v3/2a844503364a": "v1/2a844503364a", "v3/363b7b58c971": "v4/363b7b58c971", "v3/65b4b565ed67": "v4/65b4b565ed67",
+    "v3/680e4c57cdc8": "v1/680e4c57cdc8", "v3/80ad8e737b06": "v4/80ad8e737b06", "v3/84496d824942": "v1/84496d824942",
+    "v3/84c0a03c4374": "v1/84c0a03c4374", "v3/9c745ea697a7": "v4/9c745ea697a7", "v3/c72358b8111e": "v4/c72358b8111e",
+    "v3/f7ad66842c19": "v1/f7ad66842c19", "v4/18b859c50de2": "v1/18b859c50de2", "v4/1e49beb8a123": "v7/1e49beb8a123",
+    "v4/2a844503364a": "v1/2a844503364a", "v4/680e4c57cdc8": "v1/680e4c57cdc8", "v4/84496d824942": "v1/84496d824942",
+    "v4/84c0a03c4374": "v1/84c0a03c4374", "v4/f7ad66842c19": "v1/f7ad66842c19", "v5/1e49beb8a123": "v7/1e49beb8a123",
+    "v6/1e49beb8a123": "v7/1e49beb8a123", "v6/215dd2e6a519": "v7/215dd2e6a519", "v6/622c35f5d1c6": "v8/622c35f5d1c6",
+    "v6/71f1d2c9f38b": "v8/71f1d2c9f38b", "v6/8e33a91b7364": "v8/8e33a91b7364", "v6/97032595d968": "v8/97032595d968",
+    "v6/c68dae22972b": "v5/c68dae22972b", "v7/385e1beb9bb9": "v8/385e1beb9bb9", "v7/493cad38cac9": "v8/493cad38cac9",
+    "v7/622c35f5d1c6": "v8/622c35f5d1c6", "v7/8e33a91b7364": "v8/8e33a91b7364", "v7/ac3fb0b7281f": "v6/ac3fb0b7281f",
+    "v7/f4e9e58fef73": "v8/f4e9e58fef73", "v8/e29b92927600": "v7/e29b92927600",
 }
 for _a, _c in SAME_SIGNATURE.items():
     SIGNATURES[_a] = SIGNATURES[_c]

@@ -90,3 +90,33 @@ def test_out_of_table_positions():
     freqs = np.ones((4, 4), np.complex64)
     out = oracle.rope(to_u16(x), np.array([[0, 4, -1]]), pairing="interleaved", freqs=freqs)
     assert np.array_equal(out[0, 0], to_u16(x[0, 0])) and not out[0, 1:].any()
+
+
+def test_c64_matches_torch_complex128_multiply_with_gather():
+    """oracle.rope_c64 (v1/075cb40f3d5d): x * table[pos] against torch's
+    complex128 multiply of the gathered rows, positions repeated and out of
+    order; a transposed or conjugated table would fail it."""
+    g = torch.Generator().manual_seed(31)
+    B, S, H, P = 2, 6, 3, 8
+    x = torch.randn(B, S, H, P, dtype=torch.complex64, generator=g)
+    t = torch.randn(10, P, dtype=torch.complex64, generator=g)
+    pos = torch.tensor([[3, 3, 0, 9, 1, 5], [9, 8, 7, 6, 5, 4]])
+    out = oracle.rope_c64(x.numpy(), t.numpy(), pos.numpy())
+    ref = x.to(torch.complex128) * t.to(torch.complex128)[pos][:, :, None, :]
+    np.testing.assert_array_equal(out, ref.numpy())
+    # default positions: row s for position s
+    out2 = oracle.rope_c64(x.numpy(), t.numpy())
+    np.testing.assert_array_equal(out2, (x.to(torch.complex128) * t.to(torch.complex128)[:S][None, :, None, :]).numpy())
+
+
+def test_c64_unit_rows_identity_norm_and_conj():
+    g = torch.Generator().manual_seed(32)
+    x = torch.randn(1, 5, 2, 16, dtype=torch.complex64, generator=g).numpy()
+    ang = torch.rand(5, 16, generator=g).double().numpy() * 6.283
+    t = np.exp(1j * ang)
+    t[0] = 1.0
+    out = oracle.rope_c64(x, t)
+    np.testing.assert_array_equal(out[:, 0], x[:, 0].astype(np.complex128))  # position 0, unit row: identity
+    np.testing.assert_allclose(np.abs(out), np.abs(x), rtol=1e-6)              # unit modulus keeps |x|
+    back = oracle.rope_c64(out, t, conj=True)                                  # conj undoes the rotation
+    np.testing.assert_allclose(back, x, rtol=0, atol=1e-6 * np.abs(x).max())
