@@ -12,6 +12,7 @@ BASELINE.json configurations:
   c3f  embedding forward      table [128256, 4096], ids [8, 2048] Zipf(1.1) -> [8, 2048, 4096]
   c3b  embedding backward     grad [8, 2048, 4096]        -> dense fp32 [128256, 4096]
   c4   RoPE rotate-half       q [4, 4096, 32, 128], k [4, 4096, 8, 128], pos 0..4095, theta 5e5
+  c64r RoPE on complex64      q [1, 8192, 32, 64], k [1, 8192, 8, 64] c64, gathered table rows (v1/075cb40f3d5d)
   c5f  add + RMSNorm forward  x, res [16384, 8192]        -> h, y bf16
   c5b  add + RMSNorm backward x, res, dy [16384, 8192]    -> dx bf16, dw fp32
   swf  SwiGLU gate forward    a, b [8192, 14336]          -> bf16(silu(a)) * b        (v8/c68dae22972b)
@@ -358,6 +359,48 @@ class Rope(Workload):
         torch_ref.rope_half(self.q, self.k, self.pos, self.theta)
 
 
+class RopeComplex(Workload):
+    """The complex64 RoPE of the v1 captures (v1/075cb40f3d5d): q and k
+    already viewed as complex, times the table rows gathered by position ids,
+    complex64 out."""
+
+    def __init__(self, dev, S=8192, Hq=32, Hk=8, P=64, name="c64r"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        g = _gen(0)
+        self.q = torch.randn((1, S, Hq, P), dtype=torch.complex64, generator=g)
+        self.k = torch.randn((1, S, Hk, P), dtype=torch.complex64, generator=g)
+        self.table = torch.randn((S, P), dtype=torch.complex64, generator=g)
+        self.pos = torch.randint(0, 100, (1, S), dtype=torch.int32, generator=g)
+        nq, nk = S * Hq * P, S * Hk * P
+        # q and k read and written (8 B per complex), the gathered table row once per position, the id
+        self.bytes_per_call = 2 * (nq + nk) * 8 + S * P * 8 + S * 4
+        self.dominant_bytes = self.bytes_per_call
+        self.dominant_kernel = "rope_c64_kernel"
+        self.probe_mix = (1, 1, (nq + nk) * 8, (nq + nk) * 8, f"copy of {(nq + nk) * 8 / 1e6:.1f} MB (q and k)")
+        self.description = (f"RoPE on complex64 q [1,{S},{Hq},{P}], k [1,{S},{Hk},{P}] (v1/075cb40f3d5d): times "
+                            f"table rows gathered by int32 positions, complex64 out")
+        R = self.rotations(self.bytes_per_call)
+        qd, kd, td, pd = self.q.to(dev), self.k.to(dev), self.table.to(dev), self.pos.to(dev)
+        fn = L.lib().kp_rope_c64
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        for r in range(R):
+            qs, ks = qd.clone(), kd.clone()
+            qo, ko = torch.empty_like(qs), torch.empty_like(ks)
+            sq = L.i64_array(list(qs.stride()[:3]))
+            sk = L.i64_array(list(ks.stride()[:3]))
+            args = (qs.data_ptr(), qo.data_ptr(), Hq, sq, sq, ks.data_ptr(), ko.data_ptr(), Hk, sk, sk, 1, S, P,
+                    pd.data_ptr(), 4, S, 1, torch.view_as_real(td).data_ptr(), S, P, 0, None, stream)
+            self.sets.append((fn, args, (qs, ks, qo, ko, sq, sk, pd, td)))
+        self.cpu_sample = f"full [1,{S}] q and k"
+
+    def cpu_run(self):
+        rows = self.table[self.pos[0].long()].view(1, -1, 1, self.table.shape[-1])
+        _ = self.q * rows, self.k * rows  # torch CPU complex multiply: the fragment's eager ops
+
+
 # ------------------------------------------------------------------ SwiGLU
 class SwiGlu(Workload):
     """The feed-forward gate region at its reference shape: forward reads the
@@ -536,6 +579,8 @@ def make_workload(name, dev):
         return EmbNorm(dev)
     if name == "c4":
         return Rope(dev)
+    if name == "c64r":
+        return RopeComplex(dev)
     if name == "c5f":
         return RmsFwd(dev, 16384, 8192, 1e-5, "c5f", residual=True, rstd=False)
     if name == "c5b":
@@ -557,7 +602,8 @@ def make_workload(name, dev):
     raise SystemExit(f"unknown workload {name!r}")
 
 
-ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb", "cefb"]
+ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c64r", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb",
+       "cefb"]
 
 
 # ------------------------------------------------------------------ measure
