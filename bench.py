@@ -774,7 +774,8 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU; --gpus {args.gpus} is not supported "
-              "(the hot path is single-GPU; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(every kernel runs on one GPU's rows; sharding would split tokens across ranks with the "
+              "weight-gradient sum as the only collective)", file=sys.stderr)
         return 2
 
     import torch
