@@ -724,7 +724,7 @@ def measure_cpu(wl, seconds):
         t0 = time.perf_counter()
         wl.cpu_run()
         times.append(time.perf_counter() - t0)
-        if time.perf_counter() - t_all >= seconds or len(times) >= 50:
+        if time.perf_counter() - t_all >= seconds or len(times) >= 500:
             break
     times.sort()
     med = times[len(times) // 2]
