@@ -36,8 +36,20 @@ constexpr int64_t kBlockChunks = (int64_t)kThreads * kPer;  // 16-byte chunks pe
 // kernels do (expf, IEEE division, this operation order).
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 
+// sig = fl(1 / fl(1 + expf(-x))) as eager computes it.  For |x| < 16 the
+// IEEE division is replaced by rcp and one Newton step, which gives the same
+// fp32 value for every bf16 x in that range (all 33536 of them, checked on
+// gfx950; the exhaustive test of silu_backward over every bf16 input is in
+// tests/test_gpu_swiglu.py): ~3 VALU instructions instead of ~10.
+__device__ __forceinline__ float sigmoid_f(float x) {
+  const float d = 1.0f + expf(-x);
+  if (!(__builtin_fabsf(x) < 16.0f)) return 1.0f / d;
+  const float r = __builtin_amdgcn_rcpf(d);
+  return __builtin_fmaf(__builtin_fmaf(-d, r, 1.0f), r, r);
+}
+
 __device__ __forceinline__ float silu_bwd_f(float t, float x) {
-  const float sig = 1.0f / (1.0f + expf(-x));
+  const float sig = sigmoid_f(x);
   return t * sig * (1.0f + x * (1.0f - sig));
 }
 

@@ -192,3 +192,24 @@ def test_fwd_bwd_empty_and_errors(gpu):
     a = torch.randn(4, 16, dtype=torch.bfloat16, device=gpu)
     with pytest.raises(RuntimeError):
         kp.swiglu_forward_backward(a, a, a[:, :8])
+
+
+@pytest.mark.parametrize("op", ["backward", "forward_backward"])
+def test_silu_backward_every_bf16_input_bitwise(gpu, op):
+    """da = silu_backward(t, a) over all 65536 bf16 patterns of a, with t
+    spanning random magnitudes and signs, against torch's eager
+    silu_backward bit for bit: the sigmoid's division replaced by rcp and a
+    Newton step for |a| < 16 must give eager's value for every input."""
+    a = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).to(gpu).view(64, 1024)
+    gen = torch.Generator(device=gpu).manual_seed(11)
+    g = (torch.randn(a.shape, device=gpu, generator=gen) * 4).to(torch.bfloat16)
+    b = torch.randn(a.shape, device=gpu, generator=gen).to(torch.bfloat16)
+    ref = torch.ops.aten.silu_backward(g * b, a)
+    if op == "backward":
+        s = torch.nn.functional.silu(a)
+        _, da = kp.swiglu_backward(g, s, b, a)
+    else:
+        _, _, da = kp.swiglu_forward_backward(a, b, g)
+    same = (da.view(torch.int16) == ref.view(torch.int16)) | (torch.isnan(da) & torch.isnan(ref))
+    bad = (~same).flatten().nonzero().flatten().tolist()
+    assert not bad, f"{len(bad)} inputs differ, e.g. a={a.flatten()[bad[:5]].tolist()}"
