@@ -229,3 +229,17 @@ def test_aten_drop_ins_refuse_cpu_tensors():
 def test_equivalent_fragments_reexport_their_canonical():
     for alias, canon in {**fr.SAME_AS, **fr.EQUIVALENT}.items():
         assert fr.load(alias).kernel_function is fr.load(canon).kernel_function, alias
+
+
+def test_bench_rejects_more_than_one_gpu():
+    """bench.py measures one GPU: --gpus 2 exits with status 2 and says why,
+    before touching torch or the GPU."""
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120, cwd=root)
+    assert r.returncode == 2
+    assert "measures one GPU" in r.stderr and "--gpus 2" in r.stderr
+    assert r.stdout == ""
