@@ -1,7 +1,13 @@
 #!/usr/bin/env python3
 """Throughput of the fused fragment kernels on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--all] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c2] [--solo] [--all] [--no-cpu]
+
+The default run measures every BASELINE configuration (c1, c2, c3f, c3b, c4,
+c5f, c5b) and prints one JSON line: the headline workload (c2, configs[1])
+in the top-level fields and one block per configuration under "configs",
+each with its whole-call rate, roofline (dominant kernel), traffic, CPU
+baseline and the tensor-level drop-in's time per call.
 
 A step is one call of the fragment (one pass of the hot path over one batch
 of synthetic input, already resident in HBM).  Workloads are the
@@ -77,9 +83,13 @@ class Workload:
     # input array, bytes per output array, description)
     probe_mix = None
 
+    dropin_entry = ""        # the tensor-level drop-in timed beside the C call
+    cpu_bytes = None         # bytes of the CPU sample when it is a part of the call
+
     def __init__(self, dev):
         self.dev = dev
-        self.sets = []  # per rotation set: (fn, args, keepalive)
+        self.sets = []     # per rotation set: (fn, args, keepalive)
+        self.dropins = []  # per rotation set: (callable, args) of the tensor-level drop-in
 
     def rotations(self, per_set_bytes):
         return max(2, math.ceil(MIN_ROTATION_BYTES / max(per_set_bytes, 1)))
@@ -90,6 +100,10 @@ class Workload:
         if st != 0:
             from kernelproblems_amd import _lib as L
             raise L.KPError(fn.__name__, st, L.lib().kp_last_error_message().decode())
+
+    def dropin(self, i):
+        fn, args = self.dropins[i % len(self.dropins)]
+        return fn(*args)
 
     def cpu_run(self):
         raise NotImplementedError
@@ -115,10 +129,11 @@ def _zipf(n, vocab, s, g):
 
 # ------------------------------------------------------------------ RMSNorm
 class RmsFwd(Workload):
-    def __init__(self, dev, M=4096, N=4096, eps=1e-6, name="c1", residual=False, rstd=True):
+    def __init__(self, dev, M=4096, N=4096, eps=1e-6, name="c1", residual=False, rstd=True, cpu_rows=None):
         super().__init__(dev)
         import torch
         from kernelproblems_amd import _lib as L
+        from kernelproblems_amd import fused as F
         self.name = name
         g = _gen(0)
         self.x = _randn((M, N), g)
@@ -152,21 +167,32 @@ class RmsFwd(Workload):
             args = (pa, sa, len(terms), wd.data_ptr(), N, N, None if h is None else h.data_ptr(), N, y.data_ptr(),
                     N, None if rstd_t is None else rstd_t.data_ptr(), M, N, eps, stream)
             self.sets.append((fn, args, (xs, rs, y, h, rstd_t, pa, sa, wd)))
-        self.cpu_sample = f"full [{M},{N}] call"
+            self.dropins.append((F.rms_norm, (terms, wd, eps, N)) if not residual else
+                                (lambda t, w: F.rms_norm(t, w, eps, N, return_h=True, return_rstd=False), (terms, wd)))
+        self.dropin_entry = ("fused.rms_norm([x, res], w, eps, N, return_h=True, return_rstd=False)" if residual
+                             else "fused.rms_norm([x], w, eps, N)")
+        self.cpu_rows = min(cpu_rows or M, M)
+        if self.cpu_rows < M:
+            self.cpu_bytes = self.bytes_per_call * self.cpu_rows // M
+            self.cpu_sample = f"{self.cpu_rows} of the {M} rows (rate scaled by the sample's own bytes)"
+        else:
+            self.cpu_sample = f"full [{M},{N}] call"
 
     def cpu_run(self):
         from oracle import torch_ref
+        k = self.cpu_rows
         if self.res is not None:
-            torch_ref.add_rms_norm_fwd(self.x, self.res, self.w, self.eps)
+            torch_ref.add_rms_norm_fwd(self.x[:k], self.res[:k], self.w, self.eps)
         else:
-            torch_ref.rms_norm_fwd(self.x, self.w, self.eps)
+            torch_ref.rms_norm_fwd(self.x[:k], self.w, self.eps)
 
 
 class RmsBwd(Workload):
-    def __init__(self, dev, M=8192, N=4096, eps=1e-6, name="c2", residual=False):
+    def __init__(self, dev, M=8192, N=4096, eps=1e-6, name="c2", residual=False, cpu_rows=None):
         super().__init__(dev)
         import torch
         from kernelproblems_amd import _lib as L
+        from kernelproblems_amd import fused as F
         self.name = name
         g = _gen(0)
         self.x = _randn((M, N), g)
@@ -203,14 +229,24 @@ class RmsBwd(Workload):
             args = (dpa, dsa, 1, xpa, xsa, len(xterms), None, wd.data_ptr(), N, N, None, N, dx.data_ptr(), N,
                     dw.data_ptr(), None, 0, M, N, eps, ws.data_ptr(), ws_bytes, stream)
             self.sets.append((fn, args, (xs, dys, rs, dx, dw, ws, dpa, dsa, xpa, xsa, wd)))
-        self.cpu_sample = f"full [{M},{N}] call"
+            self.dropins.append((lambda d, xt, w: F.rms_norm_backward([d], xt, None, w, eps, N, dw="f32"),
+                                 (dys, xterms, wd)))
+        self.dropin_entry = (f"fused.rms_norm_backward([dy], [x{', res' if residual else ''}], None, w, eps, N, "
+                             f"dw='f32')")
+        self.cpu_rows = min(cpu_rows or M, M)
+        if self.cpu_rows < M:
+            self.cpu_bytes = self.bytes_per_call * self.cpu_rows // M
+            self.cpu_sample = f"{self.cpu_rows} of the {M} rows (rate scaled by the sample's own bytes)"
+        else:
+            self.cpu_sample = f"full [{M},{N}] call"
 
     def cpu_run(self):
         from oracle import torch_ref
+        k = self.cpu_rows
         if self.res is not None:
-            torch_ref.add_rms_norm_bwd(self.x, self.res, self.dy, self.w, self.eps)
+            torch_ref.add_rms_norm_bwd(self.x[:k], self.res[:k], self.dy[:k], self.w, self.eps)
         else:
-            torch_ref.rms_norm_bwd(self.x, self.dy, self.w, self.eps)
+            torch_ref.rms_norm_bwd(self.x[:k], self.dy[:k], self.w, self.eps)
 
 
 # ---------------------------------------------------------------- embedding
@@ -219,6 +255,7 @@ class EmbFwd(Workload):
         super().__init__(dev)
         import torch
         from kernelproblems_amd import _lib as L
+        from kernelproblems_amd import fused as F
         self.name = name
         self.ids = _zipf(B * S, V, 1.1, _gen(0)).view(B, S)
         self.table = _randn((V, D), _gen(1), 0.0, 0.02)
@@ -240,6 +277,8 @@ class EmbFwd(Workload):
             out = torch.empty((B, S, D), dtype=torch.bfloat16, device=dev)
             args = (tab.data_ptr(), V, D, D, ids_d.data_ptr(), 8, T, out.data_ptr(), D, None, stream)
             self.sets.append((fn, args, (tab, out)))
+            self.dropins.append((F.embedding, (tab, ids_d)))
+        self.dropin_entry = "fused.embedding(table, ids)"
         self.cpu_sample = f"full [{B},{S}] gather"
 
     def cpu_run(self):
@@ -289,6 +328,7 @@ class EmbBwd(Workload):
         super().__init__(dev)
         import torch
         from kernelproblems_amd import _lib as L
+        from kernelproblems_amd import fused as F
         self.name = name
         self.ids = _zipf(B * S, V, 1.1, _gen(0)).view(B, S)  # the same ids as the forward
         self.grad = _randn((B, S, D), _gen(2))
@@ -314,6 +354,8 @@ class EmbBwd(Workload):
             args = (gs.data_ptr(), D, idd.data_ptr(), 8, T, V, D, -1, 0, out.data_ptr(), 0, 0, ws.data_ptr(),
                     ws_bytes, None, stream)
             self.sets.append((fn, args, (gs, out, ws)))
+            self.dropins.append((F.embedding_dense_backward, (gs, idd, V)))
+        self.dropin_entry = "fused.embedding_dense_backward(grad, ids, V)"
         self.cpu_sample = f"full [{B},{S}] x {D} scatter into [{V},{D}]"
 
     def cpu_run(self):
@@ -327,6 +369,7 @@ class Rope(Workload):
         super().__init__(dev)
         import torch
         from kernelproblems_amd import _lib as L
+        from kernelproblems_amd import fused as F
         self.name = name
         g = _gen(0)
         self.q = _randn((B, S, Hq, D), g)
@@ -352,6 +395,8 @@ class Rope(Workload):
             args = (qs.data_ptr(), qo.data_ptr(), Hq, sq, sq, ks.data_ptr(), ko.data_ptr(), Hk, sk, sk, B, S, D,
                     pd.data_ptr(), 8, S, 1, 0, theta, None, 0, 0, 0, 0, None, stream)
             self.sets.append((fn, args, (qs, ks, qo, ko, sq, sk, pd)))
+            self.dropins.append((lambda q, k, p: F.rope(q, k, positions=p, theta=theta, pairing="half"), (qs, ks, pd)))
+        self.dropin_entry = "fused.rope(q, k, positions=pos, theta=theta, pairing='half')"
         self.cpu_sample = f"full [{B},{S}] q and k"
 
     def cpu_run(self):
@@ -582,9 +627,9 @@ def make_workload(name, dev):
     if name == "c64r":
         return RopeComplex(dev)
     if name == "c5f":
-        return RmsFwd(dev, 16384, 8192, 1e-5, "c5f", residual=True, rstd=False)
+        return RmsFwd(dev, 16384, 8192, 1e-5, "c5f", residual=True, rstd=False, cpu_rows=4096)
     if name == "c5b":
-        return RmsBwd(dev, 16384, 8192, 1e-5, "c5b", residual=True)
+        return RmsBwd(dev, 16384, 8192, 1e-5, "c5b", residual=True, cpu_rows=4096)
     if name == "swf":
         return SwiGlu(dev, name="swf")
     if name == "swb":
@@ -604,6 +649,8 @@ def make_workload(name, dev):
 
 ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c64r", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb",
        "cefb"]
+# The BASELINE.json configurations: every default run measures each of them.
+CONFIGS = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
 
 
 # ------------------------------------------------------------------ measure
@@ -652,6 +699,33 @@ def measure_gpu(wl, steps, warmup):
         "dominant_ms_min": min(dom),
         "achieved": achieved,
     }
+
+
+def measure_dropin(wl, steps, warmup):
+    """The tensor-level drop-in (fused.*) on the same rotating inputs: what a
+    caller of the reference's boundary pays per call, with outputs and
+    workspace allocated by torch's caching allocator on every call, shape
+    checks and the ctypes marshalling included.  us_per_call is the sustained
+    wall time over K calls (synchronised on both sides); host_us_per_call is
+    the Python time until each call returns (no synchronisation: launches are
+    asynchronous), i.e. the host cost the GPU hides while it is longer than
+    the kernels."""
+    import torch
+    if not wl.dropins:
+        return None
+    for i in range(warmup):
+        wl.dropin(i)
+    torch.cuda.synchronize()
+    host = 0.0
+    w0 = time.perf_counter()
+    for i in range(steps):
+        t = time.perf_counter()
+        wl.dropin(warmup + i)
+        host += time.perf_counter() - t
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    return {"entry": wl.dropin_entry, "us_per_call": round(wall * 1e6 / steps, 3),
+            "host_us_per_call": round(host * 1e6 / steps, 3)}
 
 
 def measure_probe(wl, steps, warmup):
@@ -729,7 +803,7 @@ def measure_cpu(wl, seconds):
     times.sort()
     med = times[len(times) // 2]
     return {
-        "value": getattr(wl, "cpu_bytes", wl.bytes_per_call) / med / 1e9,
+        "value": (wl.cpu_bytes or wl.bytes_per_call) / med / 1e9,
         "unit": "GB/s",
         "ms_per_call": med * 1e3,
         "cores": torch.get_num_threads(),
@@ -763,11 +837,15 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
     ap.add_argument("--warmup", type=int, default=10)
-    ap.add_argument("--workload", default="c2", choices=ALL)
-    ap.add_argument("--all", action="store_true", help="also measure every other workload (GPU only)")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--workload", default="c2", choices=ALL, help="the headline workload (top-level fields)")
+    ap.add_argument("--solo", action="store_true",
+                    help="measure the headline workload only (profiling runs); by default every BASELINE "
+                         "configuration (c1, c2, c3f, c3b, c4, c5f, c5b) gets a block under 'configs'")
+    ap.add_argument("--all", action="store_true", help="also measure every other workload (no CPU baseline)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-probe", action="store_true", help="skip the streaming-ceiling probe")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-dropin", action="store_true", help="skip timing the tensor-level drop-ins")
+    ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU baseline budget per configuration")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the workload, run 5 plain device copies of this many MiB (a known-size "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -779,7 +857,7 @@ def main():
         return 2
 
     import torch
-    import kernelproblems_amd as kp
+    import kernelproblems_amd as kp  # noqa: F401  (loads libkp_hip.so; raises if it is missing)
 
     if not torch.cuda.is_available():
         print("bench.py: no HIP device visible", file=sys.stderr)
@@ -793,20 +871,62 @@ def main():
         r = measure_gpu(wl, args.steps, args.warmup)
         print(f"[bench] {name}: {r['ms_per_step'] * 1e3:.1f} us/call, {r['value']:.0f} GB/s, dominant kernel "
               f"{r['dominant_ms'] * 1e3:.1f} us -> {r['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+        r["dropin"] = None if args.no_dropin else measure_dropin(wl, args.steps, args.warmup)
+        if r["dropin"]:
+            d = r["dropin"]
+            print(f"[bench] {name}: drop-in {d['us_per_call']:.1f} us/call (host {d['host_us_per_call']:.1f} us)",
+                  file=sys.stderr, flush=True)
         r["ceiling"] = None if args.no_probe else measure_probe(wl, args.steps, args.warmup)
         if r["ceiling"]:
             c = r["ceiling"]
-            print(f"[bench] {name}: streaming ceiling of its mix ({c['mix']}): {c['us']:.1f} us at {c['chunks_per_thread']} chunk(s)/thread -> {c['GBps']:.0f} GB/s; "
+            print(f"[bench] {name}: streaming ceiling of its mix ({c['mix']}): {c['us']:.1f} us at "
+                  f"{c['chunks_per_thread']} chunk(s)/thread -> {c['GBps']:.0f} GB/s; "
                   f"dominant kernel at {r['achieved'] / c['GBps']:.1%} of it", file=sys.stderr, flush=True)
         cpu = None
         if with_cpu:
             print(f"[bench] cpu baseline {name}", file=sys.stderr, flush=True)
             cpu = measure_cpu(wl, args.cpu_seconds)
+            print(f"[bench] {name}: cpu {cpu['ms_per_call']:.1f} ms/call ({cpu['cores']} threads)",
+                  file=sys.stderr, flush=True)
         wl.sets.clear()
+        wl.dropins.clear()
         torch.cuda.empty_cache()
         return wl, r, cpu
 
-    wl, r, cpu = run(args.workload, not args.no_cpu)
+    def roofline(name, wl, r):
+        return {
+            "bound": "hbm",
+            "achieved": round(r["achieved"], 2),
+            "peak": PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(r["achieved"] / PEAK_GBS, 4),
+            "traffic": load_traffic(name),
+            "kernel": wl.dominant_kernel,
+            "kernel_us": round(r["dominant_ms"] * 1e3, 3),
+            "kernel_bytes": wl.dominant_bytes,
+            "ceiling": _ceiling_json(r),
+        }
+
+    def block(name, wl, r, cpu):
+        return {
+            "workload": wl.description,
+            "us_per_call": round(r["ms_per_step"] * 1e3, 3),
+            "GBps": round(r["value"], 1),
+            "pct_of_peak": round(100 * r["value"] / PEAK_GBS, 2),
+            "bytes_per_call": wl.bytes_per_call,
+            "roofline": roofline(name, wl, r),
+            "dropin": r["dropin"],
+            "cpu_baseline": cpu,
+        }
+
+    names = [args.workload] if args.solo else [args.workload] + [c for c in CONFIGS if c != args.workload]
+    configs = {}
+    head = None
+    for name in names:
+        wl, r, cpu = run(name, not args.no_cpu)
+        configs[name] = block(name, wl, r, cpu)
+        if head is None:
+            head = (wl, r, cpu)
     if args.copy_calibration_mib > 0:
         n = args.copy_calibration_mib << 20
         src = torch.empty(n, dtype=torch.uint8, device=dev)
@@ -815,6 +935,7 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         print(f"[bench] copy calibration: 5 x {args.copy_calibration_mib} MiB device copies", file=sys.stderr, flush=True)
+    wl, r, cpu = head
     line = {
         "metric": "achieved HBM GB/s and % of 8 TB/s peak per fragment; us/call vs CPU eager",
         "value": round(r["value"], 2),
@@ -826,34 +947,26 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "bf16",
         "data": "synthetic",
         "config": {
             "workload": wl.description,
             "io_dtype": "bf16",
+            "accumulate": "fp32",
             "algorithmic_bytes_per_call": wl.bytes_per_call,
             "gpu_ms_per_step": round(r["gpu_ms_per_step"], 6),
             "pct_of_hbm_peak": round(100 * r["value"] / PEAK_GBS, 2),
             "device": torch.cuda.get_device_name(dev),
         },
-        "roofline": {
-            "bound": "hbm",
-            "achieved": round(r["achieved"], 2),
-            "peak": PEAK_GBS,
-            "unit": "GB/s",
-            "frac": round(r["achieved"] / PEAK_GBS, 4),
-            "traffic": load_traffic(args.workload),
-            "kernel": wl.dominant_kernel,
-            "kernel_us": round(r["dominant_ms"] * 1e3, 3),
-            "kernel_bytes": wl.dominant_bytes,
-            "ceiling": _ceiling_json(r),
-        },
+        "roofline": roofline(args.workload, wl, r),
         "cpu_baseline": cpu,
+        "dropin": r["dropin"],
+        "configs": configs,
     }
     if args.all:
         frags = {}
         for name in ALL:
-            if name == args.workload:
+            if name in configs:
                 continue
             w2, r2, _ = run(name, False)
             frags[name] = {
