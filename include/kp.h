@@ -126,6 +126,39 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * RMSNorm forward and backward of the same rows in one row pass.
+ *
+ * Replaces the _fused_rms_norm -> _fused_rms_norm_backward region (plus the
+ * gradient adds in front of the backward and the residual add after it) of
+ *   v6/0b493aad68f0/problem.py:16-47   (y returned as 3 views; dy = (mm_670 + mm_672) + mm_674;
+ *                                       out = add_220 + dx feeds embedding_dense_backward)
+ *   v5/118d525f44e0/problem.py:16-50   (the same chain over a flat-buffer weight view)
+ *   v6/822931829090/problem.py:10-66   (y as 3 views, 3-term dy, residual)
+ *   v6/408ac0979ac5/problem.py:10-63   (x = embedding + mm_3 recomputed, 2-term dy, residual)
+ *   v6/e9198b707240/problem.py          (2-term dy, residual)
+ * where the forward's rstd is used only by the backward.  Every argument has
+ * its kp_rmsnorm_bwd_bf16 meaning (there is no rstd input: it is recomputed
+ * from x with eps); in addition the same pass writes
+ *   y (bf16 [M, N], row stride y_stride) = bf16(fp32(x) * rstd * fp32(w)),
+ *   h_out (bf16 [M, N], may be NULL) = the summed x terms when n_x > 1,
+ *   rstd_out (fp32 [M], may be NULL) = the rstd both halves used,
+ * reading x once where the two-operator sequence reads it twice.
+ * workspace: at least kp_rmsnorm_fwd_bwd_workspace_size(M, N) bytes, 16-byte aligned.
+ */
+size_t kp_rmsnorm_fwd_bwd_workspace_size(int64_t M, int64_t N);
+int kp_rmsnorm_fwd_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
+                            const void* const* x_terms, const int64_t* x_strides, int n_x,
+                            const void* weight, int64_t w_seg_len, int64_t w_seg_stride,
+                            void* h_out, int64_t h_stride,
+                            void* y, int64_t y_stride,
+                            float* rstd_out,
+                            const void* dx_residual, int64_t dxr_stride,
+                            void* dx, int64_t dx_stride,
+                            float* dw_f32, void* dw_bf16, int dw_f32_round_bf16,
+                            int64_t M, int64_t N, float eps,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * Token embedding fused into the RMSNorm forward that consumes it:
  *   h[t, :] = table[indices[t], :]   (bit copy; written only when h_out != NULL)
  *   y[t, :] = bf16(fp32(h) * rstd_t * fp32(w)),  rstd_t = 1 / sqrt(sum(h^2) / N + eps)

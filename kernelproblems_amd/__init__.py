@@ -24,6 +24,7 @@ from .fused import (
     index_checking,
     rms_norm,
     rms_norm_backward,
+    rms_norm_forward_backward,
     rope,
     rope_complex,
     set_index_checking,
@@ -48,6 +49,7 @@ __all__ = [
     "index_checking",
     "rms_norm",
     "rms_norm_backward",
+    "rms_norm_forward_backward",
     "rope",
     "rope_complex",
     "set_index_checking",

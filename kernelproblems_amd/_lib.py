@@ -72,6 +72,12 @@ SIGNATURES = {
         [pvp, pi64, i32, pvp, pi64, i32, vp, vp, i64, i64, vp, i64, vp, i64, vp, vp, i32,
          i64, i64, f32, vp, sz, vp],
     ),
+    "kp_rmsnorm_fwd_bwd_workspace_size": (sz, [i64, i64]),
+    "kp_rmsnorm_fwd_bwd_bf16": (
+        i32,
+        [pvp, pi64, i32, pvp, pi64, i32, vp, i64, i64, vp, i64, vp, i64, vp, vp, i64, vp, i64, vp, vp, i32,
+         i64, i64, f32, vp, sz, vp],
+    ),
     "kp_embedding_fwd_bf16": (i32, [vp, i64, i64, i64, vp, i32, i64, vp, i64, vp, vp]),
     "kp_embedding_bwd_workspace_size": (sz, [i64, i64, i64]),
     "kp_embedding_bwd_bf16": (

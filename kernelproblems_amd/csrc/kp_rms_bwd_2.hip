@@ -4,11 +4,11 @@
 namespace kp {
 namespace rms {
 
-BwdKernel bwd_kernel_vpl2(int wpr, int nx, int ndy, bool res) {
+BwdKernel bwd_kernel_vpl2(int wpr, int nx, int ndy, bool res, bool fwd) {
   switch (wpr) {
-    case 1: return bwd_for_terms<2, 1>(nx, ndy, res);
-    case 2: return bwd_for_terms<2, 2>(nx, ndy, res);
-    case 4: return bwd_for_terms<2, 4>(nx, ndy, res);
+    case 1: return bwd_for_terms<2, 1>(nx, ndy, res, fwd);
+    case 2: return bwd_for_terms<2, 2>(nx, ndy, res, fwd);
+    case 4: return bwd_for_terms<2, 4>(nx, ndy, res, fwd);
   }
   return nullptr;
 }

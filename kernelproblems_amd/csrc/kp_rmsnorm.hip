@@ -215,16 +215,17 @@ bool pick_vec(int64_t N, bool forward, int* vpl, int* wpr) {
   return false;
 }
 
-// Backward kernel for a fast-path shape, from its instantiation unit.
-BwdKernel bwd_kernel(int vpl, int wpr, int nx, int ndy, bool res) {
+// Backward kernel for a fast-path shape, from its instantiation unit (fwd:
+// the fused forward + backward variant).
+BwdKernel bwd_kernel(int vpl, int wpr, int nx, int ndy, bool res, bool fwd) {
   switch (vpl) {
-    case 1: return bwd_kernel_vpl1(wpr, nx, ndy, res);
-    case 2: return bwd_kernel_vpl2(wpr, nx, ndy, res);
-    case 3: return bwd_kernel_vpl3(wpr, nx, ndy, res);
-    case 4: return bwd_kernel_vpl4(wpr, nx, ndy, res);
-    case 5: return bwd_kernel_vpl5(wpr, nx, ndy, res);
+    case 1: return bwd_kernel_vpl1(wpr, nx, ndy, res, fwd);
+    case 2: return bwd_kernel_vpl2(wpr, nx, ndy, res, fwd);
+    case 3: return bwd_kernel_vpl3(wpr, nx, ndy, res, fwd);
+    case 4: return bwd_kernel_vpl4(wpr, nx, ndy, res, fwd);
+    case 5: return bwd_kernel_vpl5(wpr, nx, ndy, res, fwd);
     case 6:
-    case 8: return bwd_kernel_vpl68(vpl, wpr, nx, ndy, res);
+    case 8: return bwd_kernel_vpl68(vpl, wpr, nx, ndy, res, fwd);
   }
   return nullptr;
 }
@@ -251,6 +252,170 @@ int bwd_blocks(int64_t M, int rows_per_block_step, int bpc) {
   const int64_t groups = ceil_div(M, rows_per_block_step);
   const int64_t want = (int64_t)cu_count() * bpc;
   return (int)(groups < want ? (groups > 0 ? groups : 1) : want);
+}
+
+
+// Forward outputs of the fused forward + backward (kp_rmsnorm_fwd_bwd_bf16).
+struct FwdOut {
+  uint16_t* y;
+  int64_t ys;
+  uint16_t* h;
+  int64_t hs;
+  float* rstd;
+};
+
+size_t bwd_workspace_size(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return 16;
+  // Partial rows: at most one per row block; the block count never exceeds 4 per
+  // CU.  Rows are padded to whole 32-column chunks.
+  const int64_t blocks = (int64_t)cu_count() * 4;
+  const int64_t rows = M < blocks ? M : blocks;
+  return (size_t)(rows * ceil_div(N, kPartChunk) * kPartChunk * (int64_t)sizeof(float));
+}
+// The fused forward + backward also keeps room for an fp32 rstd per row after
+// the partial rows (used only by its two-launch fallback).
+size_t fwd_bwd_workspace_size(int64_t M, int64_t N) {
+  if (M <= 0 || N <= 0) return 16;
+  return ((bwd_workspace_size(M, N) + 255) & ~(size_t)255) + (size_t)M * sizeof(float);
+}
+
+// Launch plan of a backward row pass: the kernel and its block count (each
+// block writes one weight-gradient partial row).
+struct BwdPlan {
+  BwdKernel vec;   // vectorized kernel, or nullptr for rms_bwd_generic
+  int wpr;         // waves per row of the vectorized kernel
+  int blocks;      // row blocks = partial rows
+  size_t lds;      // dynamic LDS of the vectorized kernel
+};
+
+BwdPlan plan_bwd(const void* const* dy_terms, const int64_t* dy_strides, int n_dy, const void* const* x_terms,
+                 const int64_t* x_strides, int n_x, const void* weight, int64_t w_seg_len, int64_t w_seg_stride,
+                 const void* dx_residual, int64_t dxr_stride, const void* dx, int64_t dx_stride, bool want_dw,
+                 const FwdOut* fo, int64_t M, int64_t N) {
+  BwdPlan p{nullptr, 1, 0, 0};
+  if (M <= 0) return p;
+  int vpl = 0, wpr = 0;
+  bool vec = pick_vec(N, false, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) &&
+             rows_vec_ok(dy_terms, dy_strides, n_dy) && aligned16(dx) && (dx_stride & 7) == 0;
+  if (vec && dx_residual) vec = aligned16(dx_residual) && (dxr_stride & 7) == 0;
+  if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
+  if (vec && fo)
+    vec = aligned16(fo->y) && (fo->ys & 7) == 0 && (fo->h == nullptr || (aligned16(fo->h) && (fo->hs & 7) == 0));
+  const int nw = kThreads / 64;
+  p.vec = vec ? bwd_kernel(vpl, wpr, n_x, n_dy, dx_residual != nullptr, fo != nullptr) : nullptr;
+  if (p.vec != nullptr) {
+    const int rb = nw / wpr;
+    p.wpr = wpr;
+    p.blocks = bwd_blocks(M, rb, bwd_bpc((int64_t)(n_x + n_dy + (dx_residual ? 1 : 0)) * vpl * 1024));
+    p.lds = (want_dw && rb >= 2) ? (size_t)(rb / 2) * wpr * 512 * vpl * sizeof(float) : 0;
+  } else {
+    p.blocks = bwd_blocks(M, 1, 2);  // generic kernel: one row per block step, 2 blocks per CU
+  }
+  return p;
+}
+
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Bytes of the partial rows a plan writes.
+size_t partial_bytes(const BwdPlan& p, int64_t N) {
+  return (size_t)p.blocks * (size_t)(ceil_div(N, kPartChunk) * kPartChunk) * sizeof(float);
+}
+
+// The RMSNorm backward (fo == nullptr) and the fused forward + backward
+// (fo != nullptr: rstd is recomputed and y / h / rstd are written by the same
+// row pass).  Shapes or term combinations without a fused kernel run the
+// forward kernel and then the backward with the rstd it wrote (workspace
+// bytes past the partial rows hold it when the caller wants no rstd).  The
+// workspace must hold the partial rows the launch plan writes (the *_size
+// functions return an upper bound of that).
+int rms_bwd_impl(const char* who, const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
+                 const void* const* x_terms, const int64_t* x_strides, int n_x, const float* rstd, const void* weight,
+                 int64_t w_seg_len, int64_t w_seg_stride, const void* dx_residual, int64_t dxr_stride, void* dx,
+                 int64_t dx_stride, float* dw_f32, void* dw_bf16, int dw_f32_round_bf16, int64_t M, int64_t N,
+                 float eps, void* workspace, size_t workspace_bytes, const FwdOut* fo, void* stream) {
+  int st = check_terms(who, "dy", dy_terms, dy_strides, n_dy, M);
+  if (st != KP_OK) return st;
+  st = check_terms(who, "x", x_terms, x_strides, n_x, M);
+  if (st != KP_OK) return st;
+  if (M < 0 || N <= 0) return fail(KP_EINVAL, "%s: need M >= 0 and N > 0 (M=%lld N=%lld)", who, (long long)M, (long long)N);
+  if ((dx == nullptr && M > 0) || dx_stride < 0) return fail(KP_EINVAL, "%s: dx is NULL or has a negative stride", who);
+  if (dx_residual != nullptr && dxr_stride < 0) return fail(KP_EINVAL, "%s: negative dx_residual stride", who);
+  const bool want_dw = dw_f32 != nullptr || dw_bf16 != nullptr;
+  if (want_dw && weight == nullptr) return fail(KP_EINVAL, "%s: a weight gradient needs a weight", who);
+  if (weight != nullptr && (w_seg_len <= 0 || w_seg_stride < 0))
+    return fail(KP_EINVAL, "%s: weight segment length must be > 0", who);
+
+  // The pass: the fused kernel when there is one, else (fo only) the forward
+  // kernel followed by the plain backward.
+  BwdPlan plan = plan_bwd(dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, weight, w_seg_len, w_seg_stride,
+                          dx_residual, dxr_stride, dx, dx_stride, want_dw, fo, M, N);
+  const bool two_launch = fo != nullptr && M > 0 && plan.vec == nullptr;
+  if (two_launch)
+    plan = plan_bwd(dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, weight, w_seg_len, w_seg_stride,
+                    dx_residual, dxr_stride, dx, dx_stride, want_dw, nullptr, M, N);
+  const size_t part = want_dw ? partial_bytes(plan, N) : 0;
+  const bool rstd_in_ws = two_launch && fo->rstd == nullptr;
+  const size_t need = rstd_in_ws ? align256(part) + (size_t)M * sizeof(float) : part;
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
+    return fail(KP_EWORKSPACE, "%s: workspace needs %zu bytes, 16-byte aligned (got %zu)", who, need, workspace_bytes);
+
+  hipStream_t s = as_stream(stream);
+  RmsBwdArgs a{};
+  for (int i = 0; i < n_dy; ++i) {
+    a.dy[i] = static_cast<const uint16_t*>(dy_terms[i]);
+    a.dys[i] = dy_strides[i];
+  }
+  a.n_dy = n_dy;
+  for (int i = 0; i < n_x; ++i) {
+    a.x[i] = static_cast<const uint16_t*>(x_terms[i]);
+    a.xs[i] = x_strides[i];
+  }
+  a.n_x = n_x;
+  a.rstd = rstd;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.w_seg_len = weight ? w_seg_len : N;
+  a.w_seg_stride = weight ? w_seg_stride : N;
+  a.dxr = static_cast<const uint16_t*>(dx_residual);
+  a.dxrs = dxr_stride;
+  a.dx = static_cast<uint16_t*>(dx);
+  a.dxs = dx_stride;
+  a.partial = want_dw ? static_cast<float*>(workspace) : nullptr;
+  a.M = M;
+  a.N = N;
+  a.eps = eps;
+
+  if (M > 0) {
+    if (two_launch) {
+      float* r = rstd_in_ws ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + align256(part)) : fo->rstd;
+      st = kp_rmsnorm_fwd_bf16(x_terms, x_strides, n_x, weight, w_seg_len, w_seg_stride, n_x > 1 ? fo->h : nullptr,
+                               fo->hs, fo->y, fo->ys, r, M, N, eps, stream);
+      if (st != KP_OK) return st;
+      a.rstd = r;
+    } else if (fo != nullptr) {
+      a.y = fo->y;
+      a.ys = fo->ys;
+      a.h = n_x > 1 ? fo->h : nullptr;
+      a.hs = fo->hs;
+      a.rstd_out = fo->rstd;
+      a.rstd = nullptr;
+    }
+    if (plan.vec != nullptr) {
+      void* args[] = {&a};
+      launch_dominant_raw(reinterpret_cast<const void*>(plan.vec), dim3(plan.blocks), dim3(kThreads), args, plan.lds,
+                          s);
+    } else {
+      KP_LAUNCH_DOMINANT(rms_bwd_generic, dim3(plan.blocks), dim3(kThreads), 0, s, a);
+    }
+    st = check_launch(who);
+    if (st != KP_OK) return st;
+  }
+  if (want_dw) {
+    hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, kPartChunk)), dim3(kThreads), 0, s,
+                       static_cast<const float*>(workspace), plan.blocks, N, dw_f32, static_cast<uint16_t*>(dw_bf16),
+                       dw_f32_round_bf16);
+    st = check_launch(who);
+  }
+  return st;
 }
 
 }  // namespace
@@ -364,91 +529,33 @@ int kp_embedding_rmsnorm_fwd_bf16(const void* table, int64_t V, int64_t table_ro
   return check_launch(who);
 }
 
-size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N) {
-  if (M <= 0 || N <= 0) return 16;
-  // Partial rows: at most one per row block; the block count never exceeds 4 per
-  // CU.  Rows are padded to whole 32-column chunks.
-  const int64_t blocks = (int64_t)cu_count() * 4;
-  const int64_t rows = M < blocks ? M : blocks;
-  return (size_t)(rows * ceil_div(N, kPartChunk) * kPartChunk * (int64_t)sizeof(float));
-}
+size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N) { return bwd_workspace_size(M, N); }
+
+size_t kp_rmsnorm_fwd_bwd_workspace_size(int64_t M, int64_t N) { return fwd_bwd_workspace_size(M, N); }
 
 int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy, const void* const* x_terms,
                         const int64_t* x_strides, int n_x, const float* rstd, const void* weight, int64_t w_seg_len,
                         int64_t w_seg_stride, const void* dx_residual, int64_t dxr_stride, void* dx,
                         int64_t dx_stride, float* dw_f32, void* dw_bf16, int dw_f32_round_bf16, int64_t M, int64_t N,
                         float eps, void* workspace, size_t workspace_bytes, void* stream) {
-  static const char* who = "kp_rmsnorm_bwd_bf16";
-  int st = check_terms(who, "dy", dy_terms, dy_strides, n_dy, M);
-  if (st != KP_OK) return st;
-  st = check_terms(who, "x", x_terms, x_strides, n_x, M);
-  if (st != KP_OK) return st;
-  if (M < 0 || N <= 0) return fail(KP_EINVAL, "%s: need M >= 0 and N > 0 (M=%lld N=%lld)", who, (long long)M, (long long)N);
-  if ((dx == nullptr && M > 0) || dx_stride < 0) return fail(KP_EINVAL, "%s: dx is NULL or has a negative stride", who);
-  if (dx_residual != nullptr && dxr_stride < 0) return fail(KP_EINVAL, "%s: negative dx_residual stride", who);
-  const bool want_dw = dw_f32 != nullptr || dw_bf16 != nullptr;
-  if (want_dw && weight == nullptr) return fail(KP_EINVAL, "%s: a weight gradient needs a weight", who);
-  if (weight != nullptr && (w_seg_len <= 0 || w_seg_stride < 0))
-    return fail(KP_EINVAL, "%s: weight segment length must be > 0", who);
-  const size_t need = kp_rmsnorm_bwd_workspace_size(M, N);
-  if (want_dw && M > 0 && (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)))
-    return fail(KP_EWORKSPACE, "%s: workspace needs %zu bytes, 16-byte aligned (got %zu)", who, need, workspace_bytes);
+  return rms_bwd_impl("kp_rmsnorm_bwd_bf16", dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, rstd, weight,
+                      w_seg_len, w_seg_stride, dx_residual, dxr_stride, dx, dx_stride, dw_f32, dw_bf16,
+                      dw_f32_round_bf16, M, N, eps, workspace, workspace_bytes, nullptr, stream);
+}
 
-  hipStream_t s = as_stream(stream);
-  RmsBwdArgs a{};
-  for (int i = 0; i < n_dy; ++i) {
-    a.dy[i] = static_cast<const uint16_t*>(dy_terms[i]);
-    a.dys[i] = dy_strides[i];
-  }
-  a.n_dy = n_dy;
-  for (int i = 0; i < n_x; ++i) {
-    a.x[i] = static_cast<const uint16_t*>(x_terms[i]);
-    a.xs[i] = x_strides[i];
-  }
-  a.n_x = n_x;
-  a.rstd = rstd;
-  a.w = static_cast<const uint16_t*>(weight);
-  a.w_seg_len = weight ? w_seg_len : N;
-  a.w_seg_stride = weight ? w_seg_stride : N;
-  a.dxr = static_cast<const uint16_t*>(dx_residual);
-  a.dxrs = dxr_stride;
-  a.dx = static_cast<uint16_t*>(dx);
-  a.dxs = dx_stride;
-  a.partial = want_dw ? static_cast<float*>(workspace) : nullptr;
-  a.M = M;
-  a.N = N;
-  a.eps = eps;
-
-  int blocks = 0;
-  if (M > 0) {
-    int vpl = 0, wpr = 0;
-    bool vec = pick_vec(N, false, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) &&
-               rows_vec_ok(dy_terms, dy_strides, n_dy) && aligned16(dx) && (dx_stride & 7) == 0;
-    if (vec && dx_residual) vec = aligned16(dx_residual) && (dxr_stride & 7) == 0;
-    if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
-    const int nw = kThreads / 64;
-    const BwdKernel bk = vec ? bwd_kernel(vpl, wpr, n_x, n_dy, dx_residual != nullptr) : nullptr;
-    vec = vec && bk != nullptr;
-    if (vec) {
-      const int rb = nw / wpr;
-      blocks = bwd_blocks(M, rb, bwd_bpc((int64_t)(n_x + n_dy + (dx_residual ? 1 : 0)) * vpl * 1024));
-      const size_t lds = (want_dw && rb >= 2) ? (size_t)(rb / 2) * wpr * 512 * vpl * sizeof(float) : 0;
-      void* args[] = {&a};
-      launch_dominant_raw(reinterpret_cast<const void*>(bk), dim3(blocks), dim3(nw * 64), args, lds, s);
-    } else {
-      blocks = bwd_blocks(M, 1, 2);  // generic kernel: one row per block step, 2 blocks per CU
-      KP_LAUNCH_DOMINANT(rms_bwd_generic, dim3(blocks), dim3(kThreads), 0, s, a);
-    }
-    st = check_launch(who);
-    if (st != KP_OK) return st;
-  }
-  if (want_dw) {
-    hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, kPartChunk)), dim3(kThreads), 0, s,
-                       static_cast<const float*>(workspace), blocks, N, dw_f32, static_cast<uint16_t*>(dw_bf16),
-                       dw_f32_round_bf16);
-    st = check_launch(who);
-  }
-  return st;
+int kp_rmsnorm_fwd_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
+                            const void* const* x_terms, const int64_t* x_strides, int n_x, const void* weight,
+                            int64_t w_seg_len, int64_t w_seg_stride, void* h_out, int64_t h_stride, void* y,
+                            int64_t y_stride, float* rstd_out, const void* dx_residual, int64_t dxr_stride, void* dx,
+                            int64_t dx_stride, float* dw_f32, void* dw_bf16, int dw_f32_round_bf16, int64_t M,
+                            int64_t N, float eps, void* workspace, size_t workspace_bytes, void* stream) {
+  static const char* who = "kp_rmsnorm_fwd_bwd_bf16";
+  if ((y == nullptr && M > 0) || y_stride < 0 || (h_out != nullptr && h_stride < 0))
+    return fail(KP_EINVAL, "%s: y is NULL or a forward output has a negative stride", who);
+  FwdOut fo{static_cast<uint16_t*>(y), y_stride, static_cast<uint16_t*>(h_out), h_stride, rstd_out};
+  return rms_bwd_impl(who, dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, nullptr, weight, w_seg_len,
+                      w_seg_stride, dx_residual, dxr_stride, dx, dx_stride, dw_f32, dw_bf16, dw_f32_round_bf16, M, N,
+                      eps, workspace, workspace_bytes, &fo, stream);
 }
 
 }  // extern "C"

@@ -60,6 +60,14 @@ struct RmsBwdArgs {
   uint16_t* dx;
   int64_t dxs;
   float* partial;  // [gridDim.x, N] fp32, or nullptr when no weight gradient is wanted
+  // Forward outputs of the fused forward + backward kernels (FWD): the
+  // normalised row y = bf16(x * rstd * w), the summed x terms h (n_x > 1;
+  // may be NULL) and rstd (may be NULL), all from the rstd the backward uses.
+  uint16_t* y;
+  int64_t ys;
+  uint16_t* h;
+  int64_t hs;
+  float* rstd_out;
   int64_t M, N;
   float eps;
 };
@@ -284,7 +292,7 @@ __device__ __forceinline__ void add_acc(const float* buf, int lane, float (&acc)
 // gradient (RES) and the given rstd.  `row` is already clamped to M - 1 and
 // nothing is predicated (see load_raw); without a given rstd the 4-byte load
 // reads the row's own first x word instead (an L1 hit, never used).
-template <int VPL, int NX, int NDY, bool RES>
+template <int VPL, int NX, int NDY, bool RES, bool FWD>
 __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& dr, RawRow<VPL, 1>& rr, float& rq,
                                          const RmsBwdArgs& a, int64_t row, int64_t col) {
   load_raw<VPL, NX>(xr, a.x, a.xs, row, col);
@@ -294,7 +302,7 @@ __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& 
 #pragma unroll
     for (int i = 0; i < VPL; ++i) rr.v[0][i] = ld16_stream(rrow + i * 512);
   }
-  const float* rp = a.rstd != nullptr ? a.rstd + row : reinterpret_cast<const float*>(a.x[0] + row * a.xs[0]);
+  const float* rp = (!FWD && a.rstd != nullptr) ? a.rstd + row : reinterpret_cast<const float*>(a.x[0] + row * a.xs[0]);
   rq = *rp;
 }
 
@@ -305,16 +313,23 @@ __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& 
 // them again in the second pass (to save registers) made the loop ~16 VALU
 // instructions per element against ~10 now, and the backward grids run one
 // wave per SIMD, so the registers are free.
-template <int VPL, int WPR, int NX, int NDY, bool RES, int NW>
+//
+// FWD (fused forward + backward): rstd is recomputed from x here (never
+// loaded), and the forward's outputs are stored from it as well -- y =
+// bf16(xhat * w), the same expression as the forward kernel, h when there are
+// several x terms, rstd -- so the chain's x is read once for both passes.
+template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD>
 __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, NX>& xr, const RawRow<VPL, NDY>& dr,
                                         const RawRow<VPL, 1>& rr, float rq, const float (&wf)[VPL * 8],
                                         float (&acc)[VPL * 8], float (&red)[2][NW][2], int64_t row, int64_t col,
                                         int lane, int wave, int rloc, int it) {
   const bool valid = row < a.M;
   const float inv_n = 1.0f / (float)a.N;
+  const bool have_rstd = !FWD && a.rstd != nullptr;
   float xf[VPL * 8], df[VPL * 8];
+  u32x4 xv[VPL];
   {
-    u32x4 xv[VPL], dv[VPL];
+    u32x4 dv[VPL];
     sum_raw<VPL, NX>(xv, xr);
     sum_raw<VPL, NDY>(dv, dr);
 #pragma unroll
@@ -331,7 +346,7 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
     ss = fmaf(xf[j], xf[j], ss);
   }
   sxg = wave_sum(sxg);
-  if (a.rstd == nullptr) ss = wave_sum(ss);
+  if (!have_rstd) ss = wave_sum(ss);
   if constexpr (WPR > 1) {
     if (lane == 0) {
       red[it & 1][wave][0] = sxg;
@@ -347,10 +362,28 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
     sxg = t0;
     ss = t1;
   }
-  const float r = (a.rstd != nullptr) ? rq : 1.0f / sqrtf(ss / (float)a.N + a.eps);
+  const float r = have_rstd ? rq : 1.0f / sqrtf(ss / (float)a.N + a.eps);
   // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
   const float cN = (r * sxg) * inv_n;
   if (valid) {
+    if constexpr (FWD) {
+      uint16_t* yrow = a.y + row * a.ys + col;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (xf[i * 8 + e] * r) * wf[i * 8 + e];
+        st16_stream(yrow + i * 512, pack8(o));
+      }
+      if constexpr (NX > 1) {
+        if (a.h != nullptr) {
+          uint16_t* hrow = a.h + row * a.hs + col;
+#pragma unroll
+          for (int i = 0; i < VPL; ++i) st16_stream(hrow + i * 512, xv[i]);
+        }
+      }
+      if (a.rstd_out != nullptr && wave % WPR == 0 && lane == 0) a.rstd_out[row] = r;
+    }
     uint16_t* dxrow = a.dx + row * a.dxs + col;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
@@ -373,7 +406,7 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
 // Grid-stride over row groups with one group of loads in flight, in two named
 // register slots (see rms_fwd_vec).  NW waves per block (4 or 8): RB = NW / WPR
 // rows per block step; every block owns one weight-gradient partial row.
-template <int VPL, int WPR, int NX, int NDY, bool RES, int NW>
+template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD>
 __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   constexpr int RB = NW / WPR;
   constexpr int SEG = 512 * VPL;
@@ -404,10 +437,11 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   int it = 0;
 #define KP_ROW(g) ((g) * RB + rloc)
 #define KP_LOAD(S, g)                                                                       \
-  bwd_load<VPL, NX, NDY, RES>(x##S, d##S, r##S, q##S, a, clamp_row(KP_ROW(g), a.M), col); \
+  bwd_load<VPL, NX, NDY, RES, FWD>(x##S, d##S, r##S, q##S, a, clamp_row(KP_ROW(g), a.M), col); \
   __builtin_amdgcn_sched_barrier(0)
 #define KP_PROC(S, g)                                                                                               \
-  bwd_row<VPL, WPR, NX, NDY, RES, NW>(a, x##S, d##S, r##S, q##S, wf, acc, red, KP_ROW(g), col, lane, wave, rloc, it); \
+  bwd_row<VPL, WPR, NX, NDY, RES, NW, FWD>(a, x##S, d##S, r##S, q##S, wf, acc, red, KP_ROW(g), col, lane, wave, rloc, \
+                                          it);                                                                         \
   ++it
   // Exact trip count (see rms_fwd_vec): nb >= 1 groups per block.
   const int64_t nb = (ngroups - 1 - blockIdx.x) / G + 1;
@@ -463,12 +497,13 @@ typedef void (*BwdKernel)(RmsBwdArgs);
 FwdKernel fwd_kernel(int vpl, int wpr, int nx);
 // Gather variants (one term, row ids): kp_rms_fwd_gather.hip.
 FwdKernel fwd_gather_kernel(int vpl, int wpr);
-BwdKernel bwd_kernel_vpl1(int wpr, int nx, int ndy, bool res);
-BwdKernel bwd_kernel_vpl2(int wpr, int nx, int ndy, bool res);
-BwdKernel bwd_kernel_vpl3(int wpr, int nx, int ndy, bool res);
-BwdKernel bwd_kernel_vpl4(int wpr, int nx, int ndy, bool res);
-BwdKernel bwd_kernel_vpl5(int wpr, int nx, int ndy, bool res);
-BwdKernel bwd_kernel_vpl68(int vpl, int wpr, int nx, int ndy, bool res);
+// fwd = true selects the fused forward + backward variant (FWD).
+BwdKernel bwd_kernel_vpl1(int wpr, int nx, int ndy, bool res, bool fwd);
+BwdKernel bwd_kernel_vpl2(int wpr, int nx, int ndy, bool res, bool fwd);
+BwdKernel bwd_kernel_vpl3(int wpr, int nx, int ndy, bool res, bool fwd);
+BwdKernel bwd_kernel_vpl4(int wpr, int nx, int ndy, bool res, bool fwd);
+BwdKernel bwd_kernel_vpl5(int wpr, int nx, int ndy, bool res, bool fwd);
+BwdKernel bwd_kernel_vpl68(int vpl, int wpr, int nx, int ndy, bool res, bool fwd);
 
 template <int VPL, int WPR>
 FwdKernel fwd_for_terms(int nx) {
@@ -482,20 +517,34 @@ FwdKernel fwd_for_terms(int nx) {
 // Term combinations of the backward fast path (x terms, dy terms, residual
 // epilogue) -- the ones the configurations and reference fragments use;
 // others run the generic kernel.
+// The fused forward + backward variants cover the chain fragments' terms:
+// (1 x, 1..3 dy, +- residual) and (2 x, 2 dy, residual).
 template <int VPL, int WPR>
-BwdKernel bwd_for_terms(int nx, int ndy, bool res) {
+BwdKernel bwd_for_terms(int nx, int ndy, bool res, bool fwd) {
   constexpr int NW = kThreads / 64;
+  if (fwd) {
+    if (!res) {
+      if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, false, NW, true>;
+    } else {
+      if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, true, NW, true>;
+      if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, true, NW, true>;
+      if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, true, NW, true>;
+      if (nx == 2 && ndy == 2) return rms_bwd_vec<VPL, WPR, 2, 2, true, NW, true>;
+    }
+    return nullptr;
+  }
   if (!res) {
-    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, false, NW>;
-    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, false, NW>;
-    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, false, NW>;
-    if (nx == 2 && ndy == 1) return rms_bwd_vec<VPL, WPR, 2, 1, false, NW>;
-    if (nx == 3 && ndy == 1) return rms_bwd_vec<VPL, WPR, 3, 1, false, NW>;
-    if (nx == 2 && ndy == 2) return rms_bwd_vec<VPL, WPR, 2, 2, false, NW>;
+    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, false, NW, false>;
+    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, false, NW, false>;
+    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, false, NW, false>;
+    if (nx == 2 && ndy == 1) return rms_bwd_vec<VPL, WPR, 2, 1, false, NW, false>;
+    if (nx == 3 && ndy == 1) return rms_bwd_vec<VPL, WPR, 3, 1, false, NW, false>;
+    if (nx == 2 && ndy == 2) return rms_bwd_vec<VPL, WPR, 2, 2, false, NW, false>;
   } else {
-    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, true, NW>;
-    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, true, NW>;
-    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, true, NW>;
+    if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, true, NW, false>;
+    if (nx == 1 && ndy == 2) return rms_bwd_vec<VPL, WPR, 1, 2, true, NW, false>;
+    if (nx == 1 && ndy == 3) return rms_bwd_vec<VPL, WPR, 1, 3, true, NW, false>;
+    if (nx == 2 && ndy == 2) return rms_bwd_vec<VPL, WPR, 2, 2, true, NW, false>;
   }
   return nullptr;
 }

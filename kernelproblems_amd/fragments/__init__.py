@@ -19,12 +19,13 @@ _CANONICAL = (
     "v5/013a3088b488",
     # RMSNorm backward (+ gradient adds, + residual add recompute)
     "v7/45990c83cfd6", "v8/d8f596b3df34", "v7/7f544ceb2120", "v7/ed20955ec34b", "v8/3c6c589cdf81",
+    "v8/43f0c930291e",
     # embedding forward / backward
     "v7/1e49beb8a123", "v8/12545c1e9b06", "v7/a12a160cb11b",
     # RoPE (interleaved complex, table) forward / backward
     "v7/e29b92927600", "v8/493cad38cac9", "v8/c8c60d8f7015", "v8/97032595d968", "v7/0f38bc55457c",
     "v7/5c65f62b0422", "v7/bfe872e373e4", "v5/ca76bd89ec38", "v4/6b92d6e665ab", "v6/03d64c25b654",
-    "v6/dc55b25cdcb2", "v5/a1bb72d946b0", "v4/a1318bc813d2", "v6/c8c60d8f7015",
+    "v6/dc55b25cdcb2", "v5/a1bb72d946b0", "v4/a1318bc813d2", "v6/c8c60d8f7015", "v8/7e38211c7f1c",
     # RoPE on complex64 q / k (the v1 captures)
     "v1/075cb40f3d5d", "v1/9cd8f72e74ce", "v1/f23f9bb4567a", "v1/d7efc428b2f5",
     # SwiGLU gate forward / backward (+ silu alone, forward recomputed with the backward)
@@ -33,7 +34,7 @@ _CANONICAL = (
     # token cross-entropy forward / backward
     "v8/71f1d2c9f38b", "v8/622c35f5d1c6", "v7/e59c6b1b5156", "v5/fb5b36393cbd", "v4/80ad8e737b06",
     # chain: RMSNorm forward -> backward (+ gradient adds, residual) -> embedding backward
-    "v6/0b493aad68f0", "v5/118d525f44e0",
+    "v6/0b493aad68f0", "v5/118d525f44e0", "v8/f6251e84e3fa",
     # chain: (residual add +) RMSNorm forward -> backward (+ gradient adds, residual epilogue)
     "v6/822931829090", "v6/e9198b707240", "v5/92ce4a0c7b2c", "v5/401b52261ef5", "v4/363b7b58c971",
     "v6/408ac0979ac5", "v4/9c745ea697a7", "v6/28b45679fca1", "v1/f7ad66842c19", "v5/ac7d64b3c769",

@@ -45,3 +45,14 @@ def layer_norm_weight(flat: torch.Tensor, index: int = 0) -> torch.Tensor:
     rows = flat.view(SHARDS, -1)
     off = sum(LAYER_SPLITS[:index])
     return rows[:, off:off + LAYER_SPLITS[index]]
+
+
+def norm_saved(x: torch.Tensor, w: torch.Tensor, eps: float = EPS):
+    """The (y, rstd) tuple _fused_rms_norm returns for x, w, eps -- the saved
+    forward a backward-only fragment receives as its first input (e.g.
+    v8/43f0c930291e/problem.py:12,21: only element [1], rstd [..., 1] fp32, is
+    read).  Input synthesis only: plain torch fp32 ops, not this package's
+    kernels."""
+    xf = x.float()
+    rstd = torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (xf * rstd * w.float()).to(torch.bfloat16), rstd

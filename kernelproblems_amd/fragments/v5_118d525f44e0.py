@@ -1,6 +1,6 @@
 """The chain of v6/0b493aad68f0 with the norm weight taken from an FSDP flat
 buffer: v5/118d525f44e0/problem.py:10-59 (inputs :62-70).  The [8, 512] view
-(row stride 27264000) is read in place by both norm kernels; the reference
+(row stride 27264000) is read in place by the norm's row pass; the reference
 clones it to a contiguous [4096] first (:17-19)."""
 from ._common import randint, randn, strided_randn
 from .v6_0b493aad68f0 import chain

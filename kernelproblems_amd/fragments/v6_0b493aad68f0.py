@@ -2,13 +2,14 @@
 gradient and residual epilogue, and the token-embedding backward of the
 result: v6/0b493aad68f0/problem.py:10-56 (inputs :59-67).
 
-Three launches of the fused kernels: the norm forward (y, returned as three
-views, and the rstd the backward uses); the backward with
-dy = bf16(bf16(mm_670 + mm_672) + mm_674), g = bf16(add_220 + dx) and the
-fp32-widened bf16 weight gradient; the dense embedding backward of g
-(fp32 accumulation, rounded once to bf16 like the eager bf16 table, stored
-fp32).  g is the one intermediate that reaches HBM: the embedding backward
-reads its rows in sorted-id order, not in the token order they are made in."""
+One row pass for the norm forward and backward: x is read once, rstd is
+computed once in registers, and the pass writes y (returned as three views),
+g = bf16(add_220 + dx) with dy = bf16(bf16(mm_670 + mm_672) + mm_674), and
+the weight-gradient partials (then the fixed-order finalize, widened from the
+bf16 rounding to fp32).  Then the dense embedding backward of g (fp32
+accumulation, rounded once to bf16 like the eager bf16 table, stored fp32).
+g is the one intermediate that reaches HBM: the embedding backward reads its
+rows in sorted-id order, not in the token order they are made in."""
 from .. import fused as F
 from ._common import EPS, randint, randn, rows2d
 
@@ -30,8 +31,7 @@ def chain(x, w, dy_terms, residual, ids):
     import torch
 
     n = x.shape[-1]
-    _, y, rstd = F.rms_norm([x], w, EPS, n)
-    g, dw = F.rms_norm_backward(dy_terms, [x], rstd, w, EPS, n, dx_residual=residual, dw="f32_bf16")
+    y, g, dw, _, _ = F.rms_norm_forward_backward(dy_terms, [x], w, EPS, n, dx_residual=residual, dw="f32_bf16")
     table = F.embedding_dense_backward(g, ids, NUM_WEIGHTS, -1, False, out_dtype=torch.float32, round_to_bf16=True)
     v = rows2d(y)
     return v, v.view(v.shape), v.view(v.shape), dw.view(-1), table  # dw: f32[N] whatever the weight view

@@ -148,6 +148,54 @@ def rms_norm(
     return h, y, rstd
 
 
+def _bwd_operands(who, dy_terms, x_terms, weight, n, dx_residual):
+    """Row views of the backward's operands: (dev, x shape, M, dy rows,
+    dy strides, x rows, x strides, weight segments, residual rows, stride)."""
+    dy0 = dy_terms[0]
+    _need_gpu(f"{who} grad_out", dy0)
+    dev, shape = dy0.device, x_terms[0].shape
+    dyr, dys = [], []
+    m = None
+    for i, t in enumerate(dy_terms):
+        _need_gpu(f"{who} grad term {i}", t)
+        if t.numel() != dy0.numel():
+            raise RuntimeError(f"{who}: grad terms must have the same number of elements")
+        tt, rs, m = _as_rows(t, n)
+        dyr.append(tt)
+        dys.append(rs)
+    xr, xs = [], []
+    for i, t in enumerate(x_terms):
+        _need_gpu(f"{who} input term {i}", t)
+        if t.numel() != dy0.numel():
+            raise RuntimeError(f"{who}: input and grad must have the same number of elements")
+        tt, rs, _ = _as_rows(t, n)
+        xr.append(tt)
+        xs.append(rs)
+    w_seg = (None, n, n)
+    if weight is not None:
+        _need_gpu(f"{who} weight", weight)
+        w_seg = _weight_segments(weight, n)
+    res_t, res_s = None, n
+    if dx_residual is not None:
+        _need_gpu(f"{who} residual", dx_residual)
+        res_t, res_s, _ = _as_rows(dx_residual, n)
+    return dev, shape, m, dyr, dys, xr, xs, w_seg, res_t, res_s
+
+
+def _dw_outputs(who, dw, weight, n, dev):
+    dw_f32 = dw_bf16 = None
+    if dw is not None:
+        if weight is None:
+            raise RuntimeError(f"{who}: no weight, no weight gradient")
+        if dw in ("f32", "f32_bf16"):
+            dw_f32 = torch.empty(n, dtype=torch.float32, device=dev)
+        elif dw == "bf16":
+            dw_bf16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
+        else:
+            raise ValueError(f"{who}: unknown dw mode {dw!r}")
+    return dw_f32, dw_bf16
+
+
 def rms_norm_backward(
     dy_terms: Sequence[torch.Tensor],
     x_terms: Sequence[torch.Tensor],
@@ -168,51 +216,17 @@ def rms_norm_backward(
     (fp32 sum), "f32_bf16" (the reference's bf16 rounding widened to fp32),
     "bf16", or None.  Returns (dx, dw).
     """
-    dy0 = dy_terms[0]
-    _need_gpu("rms_norm_backward grad_out", dy0)
-    dev, shape = dy0.device, x_terms[0].shape
-    dyr, dys = [], []
-    m = None
-    for i, t in enumerate(dy_terms):
-        _need_gpu(f"rms_norm_backward grad term {i}", t)
-        if t.numel() != dy0.numel():
-            raise RuntimeError("rms_norm_backward: grad terms must have the same number of elements")
-        tt, rs, m = _as_rows(t, n)
-        dyr.append(tt)
-        dys.append(rs)
-    xr, xs = [], []
-    for i, t in enumerate(x_terms):
-        _need_gpu(f"rms_norm_backward input term {i}", t)
-        if t.numel() != dy0.numel():
-            raise RuntimeError("rms_norm_backward: input and grad must have the same number of elements")
-        tt, rs, _ = _as_rows(t, n)
-        xr.append(tt)
-        xs.append(rs)
+    who = "rms_norm_backward"
+    dev, shape, m, dyr, dys, xr, xs, (w_t, seg_len, seg_stride), res_t, res_s = _bwd_operands(
+        who, dy_terms, x_terms, weight, n, dx_residual)
     rstd_t = None
     if rstd is not None:
-        _need_gpu("rms_norm_backward rstd", rstd, torch.float32)
+        _need_gpu(f"{who} rstd", rstd, torch.float32)
         if rstd.numel() != m:
-            raise RuntimeError(f"rms_norm_backward: rstd has {rstd.numel()} values, expected {m}")
+            raise RuntimeError(f"{who}: rstd has {rstd.numel()} values, expected {m}")
         rstd_t = rstd.contiguous()
-    w_t, seg_len, seg_stride = (None, n, n)
-    if weight is not None:
-        _need_gpu("rms_norm_backward weight", weight)
-        w_t, seg_len, seg_stride = _weight_segments(weight, n)
-    res_t, res_s = None, n
-    if dx_residual is not None:
-        _need_gpu("rms_norm_backward residual", dx_residual)
-        res_t, res_s, _ = _as_rows(dx_residual, n)
     dx = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-    dw_f32 = dw_bf16 = None
-    if dw is not None:
-        if weight is None:
-            raise RuntimeError("rms_norm_backward: no weight, no weight gradient")
-        if dw in ("f32", "f32_bf16"):
-            dw_f32 = torch.empty(n, dtype=torch.float32, device=dev)
-        elif dw == "bf16":
-            dw_bf16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
-        else:
-            raise ValueError(f"rms_norm_backward: unknown dw mode {dw!r}")
+    dw_f32, dw_bf16 = _dw_outputs(who, dw, weight, n, dev)
     ws_bytes = int(L.lib().kp_rmsnorm_bwd_workspace_size(m, n)) if dw is not None else 0
     ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev) if dw is not None else None
     L.call(
@@ -228,6 +242,54 @@ def rms_norm_backward(
     if weight is not None and out_dw is not None:
         out_dw = out_dw.view(weight.shape)
     return (dx if want_dx else None), out_dw
+
+
+def rms_norm_forward_backward(
+    dy_terms: Sequence[torch.Tensor],
+    x_terms: Sequence[torch.Tensor],
+    weight: Optional[torch.Tensor],
+    eps: float,
+    n: int,
+    *,
+    dx_residual: Optional[torch.Tensor] = None,
+    dw: Optional[str] = "f32",
+    return_h: bool = False,
+    return_rstd: bool = False,
+):
+    """RMSNorm forward and backward of the same rows in one row pass: the
+    _fused_rms_norm -> _fused_rms_norm_backward regions whose forward rstd
+    only feeds the backward (v6/0b493aad68f0/problem.py:16-47,
+    v6/822931829090/problem.py:10-66).  x = bf16 running sum of x_terms,
+    dy = that of dy_terms; rstd is computed once from x and eps and used for
+    both y = bf16(x * rstd * w) and the backward (as rms_norm_backward with
+    rstd=None).  Returns (y, dx, dw, h or None, rstd or None); y and dx have
+    x_terms[0]'s shape, h is only produced for several x terms."""
+    who = "rms_norm_forward_backward"
+    dev, shape, m, dyr, dys, xr, xs, (w_t, seg_len, seg_stride), res_t, res_s = _bwd_operands(
+        who, dy_terms, x_terms, weight, n, dx_residual)
+    y = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    dx = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+    h = torch.empty(shape, dtype=torch.bfloat16, device=dev) if (return_h and len(x_terms) > 1) else None
+    rstd = torch.empty(m, dtype=torch.float32, device=dev) if return_rstd else None
+    dw_f32, dw_bf16 = _dw_outputs(who, dw, weight, n, dev)
+    ws_bytes = int(L.lib().kp_rmsnorm_fwd_bwd_workspace_size(m, n))
+    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
+    L.call(
+        "kp_rmsnorm_fwd_bwd_bf16",
+        L.ptr_array([t.data_ptr() for t in dyr]), L.i64_array(dys), len(dyr),
+        L.ptr_array([t.data_ptr() for t in xr]), L.i64_array(xs), len(xr),
+        _ptr(w_t), seg_len, seg_stride,
+        _ptr(h), n, y.data_ptr(), n, _ptr(rstd),
+        _ptr(res_t), res_s, dx.data_ptr(), n,
+        _ptr(dw_f32), _ptr(dw_bf16), 1 if dw == "f32_bf16" else 0,
+        m, n, float(eps), ws.data_ptr(), ws_bytes, _stream(dev),
+    )
+    out_dw = dw_f32 if dw_f32 is not None else dw_bf16
+    if weight is not None and out_dw is not None:
+        out_dw = out_dw.view(weight.shape)
+    if return_h and h is None:
+        h = x_terms[0]
+    return y, dx, out_dw, h, rstd
 
 
 # ---------------------------------------------------------------- embedding

@@ -289,6 +289,21 @@ def _norm_emb_bwd_chain(x, w, mm_a, mm_b, mm_c, res, ids):  # v6/0b493aad68f0/pr
             aten._to_copy.default(table, dtype=torch.float32))
 
 
+def _norm_bwd_emb_bwd(saved, mm_a, mm_b, mm_c, x, w, res, ids):  # v8/f6251e84e3fa/problem.py:21-57
+    r = saved[1]
+    dy = aten.add.Tensor(aten.add.Tensor(aten.view.default(mm_a, list(x.shape)), aten.view.default(mm_b, list(x.shape))),
+                         aten.view.default(mm_c, list(x.shape)))
+    dx, dw = _norm_bwd(dy, x, r, w)
+    g = aten.add.Tensor(res, dx)
+    table = aten.embedding_dense_backward.default(g, ids, 128256, -1, False)
+    return aten._to_copy.default(dw, dtype=torch.float32), aten._to_copy.default(table, dtype=torch.float32)
+
+
+def _norm_bwd_saved(saved, mm_a, mm_b, mm_c, x, w, res):  # v8/43f0c930291e/problem.py:21-52
+    out, dw = _rms_bwd_epilogue([aten.view.default(mm_a, list(x.shape)), mm_b, mm_c], x, saved[1], w, res, True)
+    return out, dw
+
+
 def _norm_emb_bwd_chain_fsdp(wv, x, mm_a, mm_b, mm_c, res, ids):  # v5/118d525f44e0/problem.py:16-59
     return _norm_emb_bwd_chain(x, _clone_weight(wv), mm_a, mm_b, mm_c, res, ids)
 
@@ -340,6 +355,9 @@ _FRAGMENTS = {
     "v8/97032595d968": _rope_qk(False),
     "v7/0f38bc55457c": _rope_qk(True),
     "v7/5c65f62b0422": _rope_bwd,
+    "v8/7e38211c7f1c": lambda saved, table: _rope_bwd(saved[1], table),  # v8/7e38211c7f1c/problem.py:16-43
+    "v8/43f0c930291e": _norm_bwd_saved,
+    "v8/f6251e84e3fa": _norm_bwd_emb_bwd,
     "v7/bfe872e373e4": _rope_bwd,
     "v5/ca76bd89ec38": _rope_qk_fwd_twice,
     "v4/6b92d6e665ab": _rope_qk_fwd_twice,

@@ -145,6 +145,13 @@ SIGNATURES = {
     "v6/28b45679fca1": [("mm_223", MM), ("add_62_recomputed", X), ("mm_226", MM), ("view_3253", W)],
     "v8/622c35f5d1c6": [("div", (F32, (), ())), ("_log_softmax", (F32, (8192, 128256), (128256, 1))),
                         ("view_805", (I64, (8192,), (1,))), ("getitem_419", (F32, (), ()))],
+    # a tuple input (a list of specs): the saved forward / attention-backward
+    # outputs a captured graph passes, of which the fragment reads element [1]
+    "v8/43f0c930291e": [("_fused_rms_norm_2_recomputed", [X, RSTD]), ("mm_656", MM), ("mm_658", MM),
+                        ("mm_660", MM), ("add_1", X), ("_unsafe_view_450", W), ("add_215", X)],
+    "v8/f6251e84e3fa": [("_fused_rms_norm_recomputed", [X, RSTD]), ("mm_670", MM), ("mm_672", MM), ("mm_674", MM),
+                        ("embedding", X), ("_unsafe_view_432", W), ("add_220", X), ("arg583_1", IDS)],
+    "v8/7e38211c7f1c": [("_scaled_dot_product_flash_attention_backward_31", [GQ, GK, GK]), ("clone_62", FC)],
 }
 
 # Fragments whose problem.py repeats a listed one's signature.
@@ -184,11 +191,21 @@ def test_fragment_signature_and_inputs(fid):
     assert params == [n for n, _ in SIGNATURES[fid]]
     inputs = mod.get_inputs(device="meta")
     assert len(inputs) == len(params)
-    for t, (name, (dt, shape, stride)) in zip(inputs, SIGNATURES[fid]):
+
+    def check(t, spec, name):
+        dt, shape, stride = spec
         assert (t.dtype, tuple(t.shape), t.stride()) == (dt, shape, stride), name
         # meta tensors skip as_strided's bounds check: every view fits its storage
         last = t.storage_offset() + sum((n - 1) * st for n, st in zip(t.shape, t.stride()))
         assert t.numel() == 0 or (last + 1) * t.element_size() <= t.untyped_storage().nbytes(), name
+
+    for t, (name, spec) in zip(inputs, SIGNATURES[fid]):
+        if isinstance(spec, list):
+            assert isinstance(t, tuple) and len(t) == len(spec), name
+            for k, (tk, sk) in enumerate(zip(t, spec)):
+                check(tk, sk, f"{name}[{k}]")
+        else:
+            check(t, spec, name)
     with pytest.raises(RuntimeError, match="GPU|device"):
         mod.kernel_function(*inputs)
 
