@@ -126,6 +126,31 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------------------
+ * RMSNorm backward that allocates nothing and takes no workspace.
+ *
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): the same computation and arguments as
+ * kp_rmsnorm_bwd_bf16, with the weight-gradient partial rows kept in a static
+ * device array of kp_rmsnorm_bwd_noalloc_max_bytes() bytes (8 MiB: 256 row
+ * blocks of up to 8192 fp32 columns, enough for every configuration here) that
+ * each GPU holds until the process ends.  A shape whose partial rows do not
+ * fit returns KP_EUNSUPPORTED before launching anything.  Every call on one
+ * GPU shares that GPU's array, so calls that overlap on one GPU (different
+ * streams, no ordering) race; calls ordered on one stream do not.  No
+ * hipMalloc, hipFree or hipMemset is made.
+ */
+size_t kp_rmsnorm_bwd_noalloc_max_bytes(void);
+int kp_rmsnorm_bwd_bf16_noalloc(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
+                                const void* const* x_terms, const int64_t* x_strides, int n_x,
+                                const float* rstd,
+                                const void* weight, int64_t w_seg_len, int64_t w_seg_stride,
+                                const void* dx_residual, int64_t dxr_stride,
+                                void* dx, int64_t dx_stride,
+                                float* dw_f32, void* dw_bf16, int dw_f32_round_bf16,
+                                int64_t M, int64_t N, float eps, void* stream);
+
+/* ------------------------------------------------------------------------
  * RMSNorm forward and backward of the same rows in one row pass.
  *
  * Replaces the _fused_rms_norm -> _fused_rms_norm_backward region (plus the

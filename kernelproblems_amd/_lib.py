@@ -72,6 +72,12 @@ SIGNATURES = {
         [pvp, pi64, i32, pvp, pi64, i32, vp, vp, i64, i64, vp, i64, vp, i64, vp, vp, i32,
          i64, i64, f32, vp, sz, vp],
     ),
+    "kp_rmsnorm_bwd_noalloc_max_bytes": (sz, []),
+    "kp_rmsnorm_bwd_bf16_noalloc": (
+        i32,
+        [pvp, pi64, i32, pvp, pi64, i32, vp, vp, i64, i64, vp, i64, vp, i64, vp, vp, i32,
+         i64, i64, f32, vp],
+    ),
     "kp_rmsnorm_fwd_bwd_workspace_size": (sz, [i64, i64]),
     "kp_rmsnorm_fwd_bwd_bf16": (
         i32,

@@ -3,6 +3,8 @@
 // vectorized row kernels are in kp_rmsnorm_kernels.hpp.
 #include <stdlib.h>
 
+#include <mutex>
+
 #include "kp_internal.hpp"
 #include "kp_rmsnorm_kernels.hpp"
 
@@ -418,6 +420,37 @@ int rms_bwd_impl(const char* who, const void* const* dy_terms, const int64_t* dy
   return st;
 }
 
+// ------------------------------------------------------------ allocation-free
+// kp_rmsnorm_bwd_bf16_noalloc keeps the weight-gradient partial rows in a
+// fixed device array instead of a caller workspace: one copy per GPU, held
+// until the process ends, shared by every call on that GPU (calls that overlap
+// on one GPU race on it).  Nothing in it needs clearing: each call's row
+// blocks write their whole partial rows before the finalize reads them.  The
+// array's name is a host-side stand-in in host code, never a device address:
+// scratch_ptr() looks the address up once per device (that device current)
+// with hipGetSymbolAddress, and launches take that pointer.
+constexpr size_t kScratchBytes = (size_t)8 << 20;  // 256 row blocks x 8192 fp32 columns
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxScratchDevices];
+
+int scratch_ptr(const char* who, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
+    return fail(KP_EHIP, "%s: no current HIP device (or device %d beyond %d)", who, dev, kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch[dev] == nullptr) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return fail(KP_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev, hipGetErrorString(e));
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return KP_OK;
+}
 }  // namespace
 }  // namespace kp
 
@@ -541,6 +574,30 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
   return rms_bwd_impl("kp_rmsnorm_bwd_bf16", dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, rstd, weight,
                       w_seg_len, w_seg_stride, dx_residual, dxr_stride, dx, dx_stride, dw_f32, dw_bf16,
                       dw_f32_round_bf16, M, N, eps, workspace, workspace_bytes, nullptr, stream);
+}
+
+size_t kp_rmsnorm_bwd_noalloc_max_bytes(void) { return kScratchBytes; }
+
+int kp_rmsnorm_bwd_bf16_noalloc(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
+                                const void* const* x_terms, const int64_t* x_strides, int n_x, const float* rstd,
+                                const void* weight, int64_t w_seg_len, int64_t w_seg_stride, const void* dx_residual,
+                                int64_t dxr_stride, void* dx, int64_t dx_stride, float* dw_f32, void* dw_bf16,
+                                int dw_f32_round_bf16, int64_t M, int64_t N, float eps, void* stream) {
+  static const char* who = "kp_rmsnorm_bwd_bf16_noalloc";
+  void* ws = nullptr;
+  if ((dw_f32 != nullptr || dw_bf16 != nullptr) && M > 0) {
+    const int st = scratch_ptr(who, &ws);
+    if (st != KP_OK) return st;
+  }
+  const int st = rms_bwd_impl(who, dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, rstd, weight, w_seg_len,
+                              w_seg_stride, dx_residual, dxr_stride, dx, dx_stride, dw_f32, dw_bf16,
+                              dw_f32_round_bf16, M, N, eps, ws, kScratchBytes, nullptr, stream);
+  if (st == KP_EWORKSPACE)  // rejected before any launch
+    return fail(KP_EUNSUPPORTED,
+                "%s: M=%lld, N=%lld needs more weight-gradient partial rows than its %zu bytes of static scratch "
+                "hold (one fp32 row of N per row block); use kp_rmsnorm_bwd_bf16 with a workspace",
+                who, (long long)M, (long long)N, kScratchBytes);
+  return st;
 }
 
 int kp_rmsnorm_fwd_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
