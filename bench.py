@@ -335,8 +335,11 @@ class EmbBwd(Workload):
         self.V = V
         T = B * S
         self.bytes_per_call = T * D * 2 + T * 8 + V * D * 4
+        # the zero fill is spread over the sort, rank, window and combine
+        # launches: the timed span is the whole pipeline (first kernel's start
+        # to last kernel's end) and carries every byte of the call
         self.dominant_bytes = self.bytes_per_call
-        self.dominant_kernel = "emb_dense"
+        self.dominant_kernel = "emb_sort_chunks .. emb_combine (4-launch pipeline span)"
         self.probe_mix = (1, 1, T * D * 2, V * D * 4,
                           f"read {T * D * 2 / 1e6:.1f} MB + write {V * D * 4 / 1e6:.1f} MB")
         uniq = int(torch.unique(self.ids).numel())

@@ -56,7 +56,8 @@ const char* kp_last_error_message(void);
  * stop_event (hipEvent_t, timing enabled) at that kernel's own start and
  * completion: the row kernel of the RMSNorm entry points (and of
  * kp_embedding_rmsnorm_fwd_bf16), the gather kernel
- * of kp_embedding_fwd_bf16, the dense-write kernel of kp_embedding_bwd_bf16,
+ * of kp_embedding_fwd_bf16, the whole four-launch pipeline of kp_embedding_bwd_bf16
+ * (start event at its first kernel's start, stop event at its last kernel's end),
  * the kernel of kp_rope_bf16 (and of kp_rope_c64), the copy kernel of kp_unshard_bf16, the
  * kernels of kp_swiglu_fwd_bf16 / kp_swiglu_bwd_bf16 / kp_silu_bf16 / kp_swiglu_fwd_bwd_bf16, the row kernel of
  * kp_cross_entropy_fwd_bf16, the kernel of kp_cross_entropy_bwd_bf16, the row

@@ -5,27 +5,42 @@
 // Zipf-distributed ids hit the same rows repeatedly; output rows are written
 // with non-temporal stores.
 //
-// Backward pipeline (four launches on one stream, no float atomics):
-//   K1 emb_sort_chunks : keys (id << tbits | t) of each 2048-token chunk are
-//                        bitonic-sorted (registers, lane shuffles, LDS only for
+// Backward pipeline (four launches on one stream, no float atomics).  The
+// token ids are sorted by (id, token) in 2048-token chunks and ranked
+// globally; the dense [V, D] result is then written by window blocks (summed
+// runs) and zero blocks (untouched rows).  The first three launches are
+// latency chains over a few hundred KB; each carries, behind its own blocks
+// in the grid, a share of the zero fill, so that the HBM streams while they
+// wait:
+//   K1 emb_sort_chunks : keys (id << 11 | t mod 2048) of each 2048-token chunk
+//                        are bitonic-sorted (registers, lane shuffles, LDS for
 //                        the cross-wave stages); padding / out-of-range ids get
 //                        the sentinel key and sort last.  K1 also clears the
-//                        touched-row bitmap.
-//   K2 emb_rank        : one thread per key.  Binary searches in every sorted
-//                        chunk give the key's global rank (keys are unique, so
-//                        the order is fully determined) and the bounds [lo, hi)
-//                        of its id's run in the global order; the key and its
-//                        bounds are scattered to that rank and the first key of
-//                        a run sets the id's bit in the bitmap.
-//   K3 emb_dense       : one-shot grid.  A window block covers kWin
-//                        consecutive sorted positions x 1024 columns: each run
-//                        piece inside it is summed in ascending t (fp32) and
-//                        written as the output row when the run lies inside the
-//                        window, else as an fp32 piece row.  Every other block
-//                        writes 1024 zero columns of one untouched vocab row.
+//                        touched-row bitmap.  Zero blocks: rows at the top of
+//                        the vocabulary, written unconditionally (the bitmap is
+//                        not known yet; a touched row there is written again
+//                        by K3 / K4).
+//   K2 emb_rank        : one thread per key.  Two binary searches per sorted
+//                        chunk count the keys of smaller ids and of ids up to
+//                        its own; with ties ordered by chunk (= token order)
+//                        these give the key's global rank and the bounds
+//                        [lo, hi) of its id's run.  Sorted ids and token
+//                        indices are scattered to the rank and the first key
+//                        of a run sets the id's bit in the bitmap.  Zero
+//                        blocks: the next rows down, unconditionally.
+//   K3 emb_dense       : window blocks cover kWin consecutive sorted positions
+//                        x 1024 columns: each run piece inside a window is
+//                        summed in ascending token order (fp32) and written as
+//                        the output row when the run lies inside the window,
+//                        else as an fp32 piece row.  Zero blocks: 1024 zero
+//                        columns of each untouched row of the rest.
 //   K4 emb_combine     : runs that span windows: the window holding the run's
-//                        start adds the pieces in window order and writes the row.
-// Every output row is written exactly once.
+//                        start adds the pieces in window order and writes the
+//                        row.  Zero blocks: the untouched rows of the last share.
+// Results are bitwise reproducible; rows outside the unconditional shares are
+// written exactly once.
+#include <stdlib.h>
+
 #include "kp_common.hpp"
 #include "kp_internal.hpp"
 
@@ -34,8 +49,11 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kChunk = 2048;   // keys per K1 block (256 threads x 8)
+constexpr int kChunkBits = 11;
 constexpr int kWin = 32;       // sorted positions per K3 window item
 constexpr uint32_t kSentinel = 0xffffffffu;
+// ids fit 21 bits so that (id << 11 | 2047) stays below the sentinel.
+constexpr int64_t kMaxVocab = ((int64_t)1 << (32 - kChunkBits)) - 1;
 
 __device__ __forceinline__ int64_t load_index(const void* idx, int ib, int64_t t) {
   return ib == 8 ? static_cast<const int64_t*>(idx)[t] : (int64_t) static_cast<const int32_t*>(idx)[t];
@@ -101,45 +119,104 @@ struct EmbBwdArgs {
   void* out;
   int out_bf16;
   int round_bf16;
-  int tbits;
   int nchunks;
   int32_t* err;
   // workspace views
   EmbHeader* hdr;
   uint32_t* keys_chunk;  // [nchunks * kChunk] chunk-sorted keys
   int32_t* chunk_valid;  // [nchunks]
-  uint32_t* keys;        // [T] globally sorted valid keys
-  int32_t* run_lo;       // [T] start of the key's id run in the sorted order
+  uint32_t* sid;         // [T] ids in (id, token) order
+  uint32_t* stok;        // [T] token indices in (id, token) order
+  int32_t* run_lo;       // [T] start of the position's id run in the sorted order
   int32_t* run_hi;       // [T] end of the run
   uint32_t* bitmap;      // [ceil(V / 32)] touched rows
-  float* pieces;         // [2 * nwin, D] piece rows of runs that span windows
+  float* pieces;         // [2 * nwin + 1, D] piece rows of runs that span windows
 };
+
+// Rows [lo, hi) of the zero fill carried by one launch; `cond` skips rows
+// whose bit is set in the touched-row bitmap.
+struct ZeroShare {
+  int64_t lo, hi;
+  int cond;
+};
+
+// Column ownership in the dense writer: a block handles one 1024-column chunk
+// q of a row and thread t the 4 columns [q*1024 + 4t, q*1024 + 4t + 4); every
+// wave load of grad (8 B per lane) and every fp32 store (16 B per lane) then
+// covers one contiguous span of the row.
+constexpr int kColStep = kThreads * 4;
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ u32x2 ld8_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+}
+
+// Stores 4 consecutive output values (fp32 or bf16) at column c of row r.
+__device__ __forceinline__ void store_out4(const EmbBwdArgs& a, int64_t r, int64_t c, f32x4 v) {
+  if (a.out_bf16) {
+    const u32x2 pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
+    __builtin_nontemporal_store(pk, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + r * a.D + c));
+  } else {
+    if (a.round_bf16) v = f32x4{round_bf(v[0]), round_bf(v[1]), round_bf(v[2]), round_bf(v[3])};
+    st16f_stream(static_cast<float*>(a.out) + r * a.D + c, v);
+  }
+}
+__device__ __forceinline__ void store_out1(const EmbBwdArgs& a, int64_t r, int64_t c, float v) {
+  if (a.out_bf16) {
+    static_cast<uint16_t*>(a.out)[r * a.D + c] = f_to_bf(v);
+  } else {
+    static_cast<float*>(a.out)[r * a.D + c] = a.round_bf16 ? round_bf(v) : v;
+  }
+}
+
+// Zero block zb of a share: 1024 columns of one row (skipped when the share
+// is conditional and the row is touched).  The block's threads store one
+// 16-byte (or 8-byte bf16) vector each.
+template <bool VEC>
+__device__ __forceinline__ void zero_block(const EmbBwdArgs& a, const ZeroShare& z, int64_t zb) {
+  const int64_t nq = (a.D + kColStep - 1) / kColStep;
+  const int64_t r = z.lo + zb / nq, q = zb % nq;
+  if (r >= z.hi || r >= a.V) return;
+  if (z.cond && ((a.bitmap[r >> 5] >> (r & 31)) & 1u)) return;
+  if constexpr (VEC) {
+    const int64_t c = q * kColStep + (int64_t)threadIdx.x * 4;
+    if (c < a.D) store_out4(a, r, c, f32x4{0.f, 0.f, 0.f, 0.f});
+  } else {
+    for (int64_t c = q * kColStep + threadIdx.x; c < min(a.D, (q + 1) * kColStep); c += kThreads) store_out1(a, r, c, 0.f);
+  }
+}
 
 // ---- K1: sort each chunk of keys (bitonic, ascending) --------------------
 // Thread t holds positions 8t..8t+7.  Stages with partner distance j < 8 are
 // register min/max, 8 <= j < 512 exchange within the wave (lane t ^ j/8),
-// j >= 512 go through LDS with block barriers.
-__global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a) {
+// j >= 512 go through LDS with block barriers.  Blocks past nchunks are the
+// launch's zero share.
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a, ZeroShare z) {
+  if ((int64_t)blockIdx.x >= a.nchunks) {
+    zero_block<VEC>(a, z, (int64_t)blockIdx.x - a.nchunks);
+    return;
+  }
   __shared__ uint32_t s[kChunk];
   const int tid = threadIdx.x;
   const int64_t base = (int64_t)blockIdx.x * kChunk;
 
   // clear this block's share of the bitmap (K2 sets bits after this kernel)
   const int64_t nwords = (a.V + 31) / 32;
-  const int64_t per = (nwords + gridDim.x - 1) / gridDim.x;
+  const int64_t per = (nwords + a.nchunks - 1) / a.nchunks;
   for (int64_t w = blockIdx.x * per + tid; w < min(nwords, (int64_t)(blockIdx.x + 1) * per); w += kThreads)
     a.bitmap[w] = 0u;
 
-  // The keys are unique, so their initial placement does not change the
-  // sorted result: load them coalesced (element e of thread tid is token
-  // base + e * 256 + tid) and sort positions 8 * tid + e.
-  // All 8 index loads go out before any of them is used: the error-flag
-  // store below may alias the index buffer as far as the compiler knows, so
-  // loading and checking one index at a time serializes 8 memory round trips.
-  // Slots past the end re-read the last index (never used); with no tokens
-  // at all (the index buffer may be NULL) nothing is read.
-  // The index width is tested once for the whole batch (a per-load branch
-  // makes the compiler wait after every int32 load).
+  // Element e of thread tid is token base + e * 256 + tid (coalesced index
+  // loads); the keys are unique within the chunk, so their placement does
+  // not change the sorted result.  All 8 index loads go out before any of
+  // them is used: the error-flag store below may alias the index buffer as
+  // far as the compiler knows, so loading and checking one index at a time
+  // serializes 8 memory round trips.  Slots past the end re-read the last
+  // index (never used); with no tokens at all (the index buffer may be NULL)
+  // nothing is read.  The index width is tested once for the whole batch (a
+  // per-load branch makes the compiler wait after every int32 load).
   int64_t id8[8];
   if (a.T > 0 && a.ib == 8) {
     const int64_t* ix = static_cast<const int64_t*>(a.idx);
@@ -171,7 +248,7 @@ __global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a) {
       const bool in_range = id >= 0 && id < a.V;
       bad |= !in_range;
       if (in_range && id != a.padding_idx) {
-        key = ((uint32_t)id << a.tbits) | (uint32_t)t;
+        key = ((uint32_t)id << kChunkBits) | (uint32_t)(e * kThreads + tid);
         ++nvalid;
       }
     }
@@ -229,140 +306,85 @@ __global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a) {
 }
 
 // ---- K2: global rank and run bounds of every valid key -------------------
-// For each key, three counts over every sorted chunk: keys < key (rank),
-// keys < (id << tbits) (run start) and keys < ((id + 1) << tbits) (run end).
-// The 3 * nchunks binary searches advance in lockstep so their LDS reads
-// overlap.  The sorted chunks are staged in LDS when they fit (<= 64 KiB,
-// i.e. up to kMaxLdsChunks chunks), else read from global memory.
-constexpr int kMaxLdsChunks = 8;
+// Position i of the chunk-sorted keys (chunk c, place p in it) holds id v.
+// Per chunk o: lo_o = #keys of ids < v, hi_o = #keys of ids <= v (two
+// branch-free binary searches; the 11-step searches of a batch of chunks
+// advance in lockstep so their loads overlap).  Run bounds: lo = sum lo_o,
+// hi = sum hi_o.  Rank in (id, token) order: p + sum_{o < c} hi_o +
+// sum_{o > c} lo_o -- equal ids of earlier chunks are earlier tokens.  The
+// sorted chunks (a few hundred KB at most) are read through the caches.
+constexpr int kRankBatch = 8;
 
-template <bool IN_LDS>
-__global__ __launch_bounds__(kThreads) void emb_rank(EmbBwdArgs a) {
-  extern __shared__ uint32_t lds_keys[];
-  const int total = a.nchunks * kChunk;
-  if constexpr (IN_LDS) {
-    // up to kMaxLdsChunks * kChunk keys = 16 vectors per thread, all loads
-    // issued before the LDS writes (a load-write loop waits per iteration)
-    constexpr int kPer = kMaxLdsChunks * kChunk / (kThreads * 4);
-    u32x4 v[kPer];
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = (k * kThreads + threadIdx.x) * 4;
-      v[k] = *reinterpret_cast<const u32x4*>(a.keys_chunk + (i < total ? i : 0));
-    }
-#pragma unroll
-    for (int k = 0; k < kPer; ++k) {
-      const int i = (k * kThreads + threadIdx.x) * 4;
-      if (i < total) *reinterpret_cast<u32x4*>(lds_keys + i) = v[k];
-    }
-    __syncthreads();
+template <bool VEC>
+__global__ __launch_bounds__(kThreads) void emb_rank(EmbBwdArgs a, int rank_blocks, ZeroShare z) {
+  if ((int)blockIdx.x >= rank_blocks) {
+    zero_block<VEC>(a, z, (int64_t)blockIdx.x - rank_blocks);
+    return;
   }
   if (blockIdx.x == 0 && threadIdx.x == 0) {
     int n = 0;
     for (int c = 0; c < a.nchunks; ++c) n += a.chunk_valid[c];
     a.hdr->n_valid = n;
   }
-  const int i = blockIdx.x * kThreads + threadIdx.x;
+  const int64_t total = (int64_t)a.nchunks * kChunk;
+  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
   if (i >= total) return;
-  const uint32_t key = IN_LDS ? lds_keys[i] : a.keys_chunk[i];
+  const uint32_t key = a.keys_chunk[i];
   if (key == kSentinel) return;
-  const int c = i / kChunk;
-  const uint32_t id = key >> a.tbits;
-  const uint32_t q[3] = {key, id << a.tbits, (id + 1) << a.tbits};  // (id + 1) << tbits <= 2^31
-  int rank = i - c * kChunk, lo = 0, hi = 0;
-  if constexpr (IN_LDS) {
-    int pos[kMaxLdsChunks][3];
+  const int c = (int)(i / kChunk);
+  const int p = (int)(i - (int64_t)c * kChunk);
+  const uint32_t id = key >> kChunkBits;
+  const uint32_t q_lo = id << kChunkBits, q_hi = (id + 1) << kChunkBits;  // id < 2^21 - 1: no overflow
+  int64_t lo = 0, hi = 0, rank = p;
+  for (int o0 = 0; o0 < a.nchunks; o0 += kRankBatch) {
+    int pl[kRankBatch], ph[kRankBatch];
 #pragma unroll
-    for (int o = 0; o < kMaxLdsChunks; ++o)
-#pragma unroll
-      for (int k = 0; k < 3; ++k) pos[o][k] = 0;
+    for (int b = 0; b < kRankBatch; ++b) pl[b] = ph[b] = 0;
 #pragma unroll
     for (int step = kChunk >> 1; step > 0; step >>= 1) {
 #pragma unroll
-      for (int o = 0; o < kMaxLdsChunks; ++o) {
-        if (o >= a.nchunks) break;
-#pragma unroll
-        for (int k = 0; k < 3; ++k)
-          if (lds_keys[o * kChunk + pos[o][k] + step - 1] < q[k]) pos[o][k] += step;
+      for (int b = 0; b < kRankBatch; ++b) {
+        const int o = o0 + b < a.nchunks ? o0 + b : a.nchunks - 1;  // clamped: results of o >= nchunks unused
+        const uint32_t* v = a.keys_chunk + (int64_t)o * kChunk;
+        if (v[pl[b] + step - 1] < q_lo) pl[b] += step;
+        if (v[ph[b] + step - 1] < q_hi) ph[b] += step;
       }
     }
 #pragma unroll
-    for (int o = 0; o < kMaxLdsChunks; ++o) {
+    for (int b = 0; b < kRankBatch; ++b) {
+      const int o = o0 + b;
       if (o >= a.nchunks) break;
-      int cnt[3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) cnt[k] = pos[o][k] + (lds_keys[o * kChunk + pos[o][k]] < q[k] ? 1 : 0);
-      if (o != c) rank += cnt[0];
-      lo += cnt[1];
-      hi += cnt[2];
-    }
-  } else {
-    for (int o = 0; o < a.nchunks; ++o) {
       const uint32_t* v = a.keys_chunk + (int64_t)o * kChunk;
-      int pos[3] = {0, 0, 0};
-#pragma unroll
-      for (int step = kChunk >> 1; step > 0; step >>= 1)
-#pragma unroll
-        for (int k = 0; k < 3; ++k)
-          if (v[pos[k] + step - 1] < q[k]) pos[k] += step;
-      int cnt[3];
-#pragma unroll
-      for (int k = 0; k < 3; ++k) cnt[k] = pos[k] + (v[pos[k]] < q[k] ? 1 : 0);
-      if (o != c) rank += cnt[0];
-      lo += cnt[1];
-      hi += cnt[2];
+      const int cl = pl[b] + (v[pl[b]] < q_lo ? 1 : 0);
+      const int ch = ph[b] + (v[ph[b]] < q_hi ? 1 : 0);
+      lo += cl;
+      hi += ch;
+      if (o < c) rank += ch;
+      else if (o > c) rank += cl;
     }
   }
-  if (rank >= a.T) return;  // impossible for unique keys; bounds the stores regardless
-  a.keys[rank] = key;
-  a.run_lo[rank] = lo;
-  a.run_hi[rank] = hi;
+  if (rank >= a.T) return;  // impossible (ranks are a permutation); bounds the stores regardless
+  a.sid[rank] = id;
+  a.stok[rank] = (uint32_t)((int64_t)c * kChunk + (key & (kChunk - 1)));
+  a.run_lo[rank] = (int32_t)lo;
+  a.run_hi[rank] = (int32_t)hi;
   if (rank == lo) atomicOr(a.bitmap + (id >> 5), 1u << (id & 31));
-}
-
-// Column ownership in K3/K4: a block handles one 1024-column chunk q of a
-// row and thread t the 4 columns [q*1024 + 4t, q*1024 + 4t + 4); every wave
-// load of grad (8 B per lane) and every fp32 store (16 B per lane) then covers
-// one contiguous span of the row.
-constexpr int kColStep = kThreads * 4;
-
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ u32x2 ld8_stream(const void* p) {
-  return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
-}
-
-// Stores 4 consecutive output values (fp32 or bf16) at column c of row r.
-__device__ __forceinline__ void store_out4(const EmbBwdArgs& a, int64_t r, int64_t c, f32x4 v) {
-  if (a.out_bf16) {
-    const u32x2 pk = {pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3])};
-    __builtin_nontemporal_store(pk, reinterpret_cast<u32x2*>(static_cast<uint16_t*>(a.out) + r * a.D + c));
-  } else {
-    if (a.round_bf16) v = f32x4{round_bf(v[0]), round_bf(v[1]), round_bf(v[2]), round_bf(v[3])};
-    st16f_stream(static_cast<float*>(a.out) + r * a.D + c, v);
-  }
-}
-__device__ __forceinline__ void store_out1(const EmbBwdArgs& a, int64_t r, int64_t c, float v) {
-  if (a.out_bf16) {
-    static_cast<uint16_t*>(a.out)[r * a.D + c] = f_to_bf(v);
-  } else {
-    static_cast<float*>(a.out)[r * a.D + c] = a.round_bf16 ? round_bf(v) : v;
-  }
 }
 
 // Workspace reads in K3/K4 are clamped to their valid ranges, so even a
 // corrupted workspace cannot steer a load or store out of bounds.
 __device__ __forceinline__ int64_t token_of(const EmbBwdArgs& a, int64_t r) {
-  const int64_t t = (int64_t)(a.keys[r] & ((1u << a.tbits) - 1u));
+  const int64_t t = (int64_t)a.stok[r];
   return t < a.T ? t : 0;
 }
+__device__ __forceinline__ int64_t row_of(const EmbBwdArgs& a, int64_t r) { return (int64_t)a.sid[r]; }
 __device__ __forceinline__ int clamp_pos(int v, int n_valid) { return v < 0 ? 0 : (v > n_valid ? n_valid : v); }
 
 // Where a finished piece [p0, p1) of the run [lo, hi) inside window [w0, w1) goes.
 __device__ __forceinline__ void emit_piece(const EmbBwdArgs& a, int64_t w, int64_t w0, int64_t w1, int lo, int hi,
                                            int64_t c, const f32x4& acc) {
   if (lo >= w0 && hi <= w1) {
-    const int64_t row = (int64_t)(a.keys[lo] >> a.tbits);
+    const int64_t row = row_of(a, lo);
     if (row < a.V) store_out4(a, row, c, acc);
   } else {
     const int slot = lo < w0 ? 0 : 1;  // 0: continues from an earlier window; 1: run starts here
@@ -372,7 +394,7 @@ __device__ __forceinline__ void emit_piece(const EmbBwdArgs& a, int64_t w, int64
 __device__ __forceinline__ void emit_piece1(const EmbBwdArgs& a, int64_t w, int64_t w0, int64_t w1, int lo, int hi,
                                             int64_t c, float acc) {
   if (lo >= w0 && hi <= w1) {
-    const int64_t row = (int64_t)(a.keys[lo] >> a.tbits);
+    const int64_t row = row_of(a, lo);
     if (row < a.V) store_out1(a, row, c, acc);
   } else {
     const int slot = lo < w0 ? 0 : 1;
@@ -441,13 +463,11 @@ __device__ void emb_do_window(const EmbBwdArgs& a, int64_t w, int64_t q, int n_v
   }
 }
 
-// One-shot dense writer.  Blocks [0, n_win_blocks) are window blocks, one per
-// (window, 1024-column chunk); they come first in the grid so the heavy runs
-// start early.  Every later block writes one 1024-column chunk of one vocab
-// row as zeros, unless the row is touched (its window block writes it): one
-// 16-byte store per thread, the launch shape that streams fastest on gfx950.
+// Blocks [0, n_win_blocks) are window blocks, one per (window, 1024-column
+// chunk); they come first in the grid so the heavy runs start early.  Every
+// later block is one zero block of the launch's (conditional) share.
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void emb_dense(EmbBwdArgs a, int64_t n_win_blocks) {
+__global__ __launch_bounds__(kThreads) void emb_dense(EmbBwdArgs a, int64_t n_win_blocks, ZeroShare z) {
   const int64_t nq = (a.D + kColStep - 1) / kColStep;
   const int64_t b = blockIdx.x;
   if (b < n_win_blocks) {
@@ -457,32 +477,29 @@ __global__ __launch_bounds__(kThreads) void emb_dense(EmbBwdArgs a, int64_t n_wi
     emb_do_window<VEC>(a, w, q, n_valid);
     return;
   }
-  const int64_t zb = b - n_win_blocks;
-  const int64_t r = zb / nq, q = zb % nq;
-  if (r >= a.V) return;
-  if ((a.bitmap[r >> 5] >> (r & 31)) & 1u) return;
-  if constexpr (VEC) {
-    const int64_t c = q * kColStep + (int64_t)threadIdx.x * 4;
-    if (c < a.D) store_out4(a, r, c, f32x4{0.f, 0.f, 0.f, 0.f});
-  } else {
-    for (int64_t c = q * kColStep + threadIdx.x; c < min(a.D, (q + 1) * kColStep); c += kThreads) store_out1(a, r, c, 0.f);
-  }
+  zero_block<VEC>(a, z, b - n_win_blocks);
 }
 
 // ---- K4: runs spanning windows, pieces added in window order ---------------
+// Blocks [0, comb_blocks) walk the windows grid-stride; later blocks are the
+// launch's (conditional) zero share.
 template <bool VEC>
-__global__ __launch_bounds__(kThreads) void emb_combine(EmbBwdArgs a) {
+__global__ __launch_bounds__(kThreads) void emb_combine(EmbBwdArgs a, int comb_blocks, ZeroShare z) {
+  if ((int)blockIdx.x >= comb_blocks) {
+    zero_block<VEC>(a, z, (int64_t)blockIdx.x - comb_blocks);
+    return;
+  }
   const int n_valid = (int)min((int64_t)max(a.hdr->n_valid, 0), a.T);
   const int64_t n_win = (n_valid + kWin - 1) / kWin;
   const int64_t nq = (a.D + kColStep - 1) / kColStep;
-  for (int64_t it = blockIdx.x; it < n_win * nq; it += gridDim.x) {
+  for (int64_t it = blockIdx.x; it < n_win * nq; it += comb_blocks) {
     const int64_t w = it / nq, q = it % nq;
     const int64_t w0 = w * kWin, w1 = w0 + kWin;
     if (w1 >= n_valid) continue;  // the last window cannot hold a run that spans past it
     const int lo = clamp_pos(a.run_lo[w1 - 1], n_valid), hi = clamp_pos(a.run_hi[w1 - 1], n_valid);
     if (!(lo >= w0 && hi > w1)) continue;  // only the window where a spanning run starts combines it
     const int64_t wl = (hi - 1) / kWin;   // window holding the run's last position
-    const int64_t row = a.keys[lo] >> a.tbits;
+    const int64_t row = row_of(a, lo);
     if (row >= a.V) continue;
     if constexpr (VEC) {
       const int64_t c = q * kColStep + (int64_t)threadIdx.x * 4;
@@ -511,15 +528,9 @@ __global__ __launch_bounds__(kThreads) void emb_combine(EmbBwdArgs a) {
 }
 
 // ------------------------------------------------------------- workspace
-int bits_for(int64_t n) {  // bits needed to represent values 0..n-1
-  int b = 0;
-  while (b < 63 && ((int64_t)1 << b) < n) ++b;
-  return b;
-}
-
 struct Layout {
-  size_t hdr, keys_chunk, chunk_valid, keys, run_lo, run_hi, bitmap, pieces, total;
-  int nchunks;
+  size_t hdr, keys_chunk, chunk_valid, sid, stok, run_lo, run_hi, bitmap, pieces, total;
+  int64_t nchunks;
   int64_t nwin;
 };
 
@@ -527,7 +538,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 Layout make_layout(int64_t T, int64_t V, int64_t D) {
   Layout L{};
-  L.nchunks = (int)ceil_div(T > 0 ? T : 1, kChunk);
+  L.nchunks = ceil_div(T > 0 ? T : 1, kChunk);
   L.nwin = ceil_div(T, kWin);
   size_t o = 0;
   L.hdr = o;
@@ -536,7 +547,9 @@ Layout make_layout(int64_t T, int64_t V, int64_t D) {
   o = align256(o + (size_t)L.nchunks * kChunk * 4);
   L.chunk_valid = o;
   o = align256(o + (size_t)L.nchunks * 4);
-  L.keys = o;
+  L.sid = o;
+  o = align256(o + (size_t)T * 4);
+  L.stok = o;
   o = align256(o + (size_t)T * 4);
   L.run_lo = o;
   o = align256(o + (size_t)T * 4);
@@ -548,6 +561,21 @@ Layout make_layout(int64_t T, int64_t V, int64_t D) {
   o = align256(o + (size_t)(2 * L.nwin + 1) * (size_t)D * 4);
   L.total = o;
   return L;
+}
+
+// Zero-fill share of each latency-chain launch, in MiB of output rows (K1,
+// K2: unconditional; K4: conditional), at least as long to stream as the
+// launch's own chain (~13-17 us each at the C3 configuration).  Measured on
+// MI355X at C3 (whole call): 96/96/64 MiB 357.1 us, 128/128/96 356.1 us,
+// 160/160/128 357.6 us, 256/256/192 360.9 us -- once the chains are hidden
+// the pipeline is bound by HBM alone.  Tuning knobs: KP_EMB_ZERO_MB_SORT /
+// _RANK / _COMBINE.
+int64_t share_rows(const char* env, int64_t dflt_mb, int64_t row_bytes, int64_t cap_rows) {
+  static_assert(sizeof(long long) == 8, "");
+  const char* e = getenv(env);
+  const int64_t mb = e ? atoll(e) : dflt_mb;
+  const int64_t rows = mb <= 0 ? 0 : ((mb << 20) + row_bytes - 1) / row_bytes;
+  return rows < cap_rows ? rows : cap_rows;
 }
 
 }  // namespace
@@ -596,11 +624,9 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   if (index_bytes != 4 && index_bytes != 8) return fail(KP_EINVAL, "%s: index_bytes must be 4 or 8", who);
   if (out_dtype != KP_DTYPE_F32 && out_dtype != KP_DTYPE_BF16) return fail(KP_EINVAL, "%s: bad out_dtype", who);
   if (T > 0 && grad_row_stride < D) return fail(KP_EINVAL, "%s: grad row stride must be >= D", who);
-  const int tbits = bits_for(T > 0 ? T : 1);
-  const int vbits = bits_for(V);
-  if (T > 32768 || vbits + tbits > 31)
-    return fail(KP_EUNSUPPORTED, "%s: T=%lld, V=%lld exceed this build's sort (T <= 32768, log2 V + log2 T <= 31)", who,
-                (long long)T, (long long)V);
+  if (V > kMaxVocab || T > 0x7fffffffLL)
+    return fail(KP_EUNSUPPORTED, "%s: V=%lld, T=%lld outside this build's sort (V < 2^21, T < 2^31)", who,
+                (long long)V, (long long)T);
   const Layout L = make_layout(T, V, D);
   if (workspace == nullptr || workspace_bytes < L.total || !aligned16(workspace))
     return fail(KP_EWORKSPACE, "%s: workspace needs %zu bytes, 16-byte aligned (got %zu)", who, L.total,
@@ -620,13 +646,13 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   a.out = grad_table;
   a.out_bf16 = out_dtype == KP_DTYPE_BF16;
   a.round_bf16 = out_round_bf16 ? 1 : 0;
-  a.tbits = tbits;
-  a.nchunks = L.nchunks;
+  a.nchunks = (int)L.nchunks;
   a.err = error_flag;
   a.hdr = reinterpret_cast<EmbHeader*>(ws + L.hdr);
   a.keys_chunk = reinterpret_cast<uint32_t*>(ws + L.keys_chunk);
   a.chunk_valid = reinterpret_cast<int32_t*>(ws + L.chunk_valid);
-  a.keys = reinterpret_cast<uint32_t*>(ws + L.keys);
+  a.sid = reinterpret_cast<uint32_t*>(ws + L.sid);
+  a.stok = reinterpret_cast<uint32_t*>(ws + L.stok);
   a.run_lo = reinterpret_cast<int32_t*>(ws + L.run_lo);
   a.run_hi = reinterpret_cast<int32_t*>(ws + L.run_hi);
   a.bitmap = reinterpret_cast<uint32_t*>(ws + L.bitmap);
@@ -635,25 +661,40 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   const bool vec = (D % 4) == 0 && aligned16(grad_table) &&
                    (T == 0 || ((reinterpret_cast<uintptr_t>(grad) & 7u) == 0 && grad_row_stride % 4 == 0));
   hipStream_t s = as_stream(stream);
-  int st;
-  hipLaunchKernelGGL(emb_sort_chunks, dim3(L.nchunks), dim3(kThreads), 0, s, a);
-  if ((st = check_launch(who)) != KP_OK) return st;
-  const int total_keys = L.nchunks * kChunk;
-  const size_t keys_bytes = (size_t)total_keys * 4;
-  const dim3 rgrid((unsigned)ceil_div(total_keys, kThreads));
-  if (keys_bytes <= 64 * 1024) hipLaunchKernelGGL(emb_rank<true>, rgrid, dim3(kThreads), keys_bytes, s, a);
-  else hipLaunchKernelGGL(emb_rank<false>, rgrid, dim3(kThreads), 0, s, a);
-  if ((st = check_launch(who)) != KP_OK) return st;
   const int64_t nq = ceil_div(D, kColStep);
-  const int64_t n_win_blocks = L.nwin * nq;
-  const int64_t dense_blocks = n_win_blocks + V * nq;
-  if (dense_blocks > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: V * D too large for one launch", who);
-  if (vec) KP_LAUNCH_DOMINANT(emb_dense<true>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
-  else KP_LAUNCH_DOMINANT(emb_dense<false>, dim3((unsigned)dense_blocks), dim3(kThreads), 0, s, a, n_win_blocks);
-  const int grid = cu_count() * 4;
+  const int64_t row_bytes = D * (out_dtype == KP_DTYPE_BF16 ? 2 : 4);
+  // Zero-fill shares, taken from the top of the vocabulary down (high ids are
+  // the rarely touched ones under the usual frequency-ordered vocabularies):
+  // K1 [V - z1, V), K2 [V - z1 - z2, V - z1), K4 [r3, V - z1 - z2), K3 [0, r3).
+  const int64_t z1 = share_rows("KP_EMB_ZERO_MB_SORT", 128, row_bytes, V / 4);
+  const int64_t z2 = share_rows("KP_EMB_ZERO_MB_RANK", 128, row_bytes, V / 4);
+  const int64_t z4 = share_rows("KP_EMB_ZERO_MB_COMBINE", 96, row_bytes, V / 4);
+  const ZeroShare zs1{V - z1, V, 0};
+  const ZeroShare zs2{V - z1 - z2, V - z1, 0};
+  const ZeroShare zs4{V - z1 - z2 - z4, V - z1 - z2, 1};
+  const ZeroShare zs3{0, V - z1 - z2 - z4, 1};
+  const int64_t nwin_blocks = L.nwin * nq;
+  const int64_t total_keys = L.nchunks * kChunk;
+  const int64_t rank_blocks = ceil_div(total_keys, kThreads);
+  const int comb_blocks = cu_count() * 4;
+  const int64_t g1 = L.nchunks + z1 * nq, g2 = rank_blocks + z2 * nq, g3 = nwin_blocks + zs3.hi * nq,
+                g4 = comb_blocks + z4 * nq;
+  if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL || g3 > 0x7fffffffLL || g4 > 0x7fffffffLL)
+    return fail(KP_EUNSUPPORTED, "%s: V * D too large for one launch", who);
+  // With the timing hook set, the events span the whole pipeline (K1 start
+  // to K4 end): its zero fill is spread over all four launches.
+  int st;
+  if (vec) KP_LAUNCH_SPAN(true, false, emb_sort_chunks<true>, dim3((unsigned)g1), dim3(kThreads), 0, s, a, zs1);
+  else KP_LAUNCH_SPAN(true, false, emb_sort_chunks<false>, dim3((unsigned)g1), dim3(kThreads), 0, s, a, zs1);
   if ((st = check_launch(who)) != KP_OK) return st;
-  if (vec) hipLaunchKernelGGL(emb_combine<true>, dim3(grid), dim3(kThreads), 0, s, a);
-  else hipLaunchKernelGGL(emb_combine<false>, dim3(grid), dim3(kThreads), 0, s, a);
+  if (vec) hipLaunchKernelGGL(emb_rank<true>, dim3((unsigned)g2), dim3(kThreads), 0, s, a, (int)rank_blocks, zs2);
+  else hipLaunchKernelGGL(emb_rank<false>, dim3((unsigned)g2), dim3(kThreads), 0, s, a, (int)rank_blocks, zs2);
+  if ((st = check_launch(who)) != KP_OK) return st;
+  if (vec) hipLaunchKernelGGL(emb_dense<true>, dim3((unsigned)g3), dim3(kThreads), 0, s, a, nwin_blocks, zs3);
+  else hipLaunchKernelGGL(emb_dense<false>, dim3((unsigned)g3), dim3(kThreads), 0, s, a, nwin_blocks, zs3);
+  if ((st = check_launch(who)) != KP_OK) return st;
+  if (vec) KP_LAUNCH_SPAN(false, true, emb_combine<true>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
+  else KP_LAUNCH_SPAN(false, true, emb_combine<false>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
   return check_launch(who);
 }
 

@@ -32,6 +32,19 @@ inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s);
 
 }  // namespace kp
 
+// The first / last launch of a multi-launch pipeline whose whole span is
+// timed: the start event is stamped at the first kernel's start, the stop
+// event at the last kernel's completion (kp_profile_dominant_kernel).
+#define KP_LAUNCH_SPAN(first, last, kernel, grid, block, shmem, stream, ...)                            \
+  do {                                                                                                  \
+    hipEvent_t kp_ev_a_ = ::kp::prof_start_event(), kp_ev_b_ = ::kp::prof_stop_event();               \
+    if (kp_ev_a_ && kp_ev_b_)                                                                           \
+      hipExtLaunchKernelGGL(kernel, grid, block, shmem, stream, (first) ? kp_ev_a_ : nullptr,          \
+                            (last) ? kp_ev_b_ : nullptr, 0, __VA_ARGS__);                               \
+    else                                                                                                \
+      hipLaunchKernelGGL(kernel, grid, block, shmem, stream, __VA_ARGS__);                              \
+  } while (0)
+
 #define KP_LAUNCH_DOMINANT(kernel, grid, block, shmem, stream, ...)                                       \
   do {                                                                                                  \
     hipEvent_t kp_ev_a_ = ::kp::prof_start_event(), kp_ev_b_ = ::kp::prof_stop_event();               \

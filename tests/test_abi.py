@@ -74,9 +74,12 @@ def test_rmsnorm_validation(lib):
 
 def test_embedding_validation(lib):
     _expect(lib, L.KP_EINVAL, "kp_embedding_fwd_bf16", 16, 10, 8, 8, 32, 3, 4, 48, 8, None, None)  # 3-byte ids
-    ws = lib.kp_embedding_bwd_workspace_size(40000, 1000, 64)
-    _expect(lib, L.KP_EUNSUPPORTED, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 40000, 1000, 64, -1, 0, 48,
-            L.KP_DTYPE_F32, 0, 64, max(ws, 1), None, None)  # more tokens than one sort handles
+    ws = lib.kp_embedding_bwd_workspace_size(100, 1 << 21, 64)
+    _expect(lib, L.KP_EUNSUPPORTED, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 100, 1 << 21, 64, -1, 0, 48,
+            L.KP_DTYPE_F32, 0, 64, max(ws, 1), None, None)  # a vocabulary past the sort key's 21 id bits
+    ws = lib.kp_embedding_bwd_workspace_size(65536, 128256, 64)
+    _expect(lib, L.KP_EWORKSPACE, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 65536, 128256, 64, -1, 0, 48,
+            L.KP_DTYPE_F32, 0, 64, ws - 1, None, None)  # any token count: only the workspace bounds it
     _expect(lib, L.KP_EINVAL, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 100, 1000, 64, -1, 0, 48, 7, 0, 64,
             1 << 20, None, None)  # unknown output dtype
 
