@@ -427,6 +427,37 @@ for _alias, _canon in _SAME_OPS.items():
     _FRAGMENTS[_alias] = _FRAGMENTS[_canon]
 
 
+class CpuDecompositions:
+    """Context manager under which every fragment's op sequence runs on the
+    CPU: the CUDA-only _fused_rms_norm_backward goes through torch's own
+    decomposition (torch/_decomp/decompositions.py:1815-1887), and the
+    device=cuda argument the captures pin on _to_copy (e.g.
+    v7/e29b92927600/problem.py:22) becomes the CPU.  Used to check this file
+    against the reference's own forward (tests/test_fragment_structure.py)."""
+
+    def __enter__(self):
+        from torch._decomp import decomposition_table
+        from torch.utils._python_dispatch import TorchDispatchMode
+
+        table = decomposition_table
+
+        class _Mode(TorchDispatchMode):
+            def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+                kwargs = kwargs or {}
+                if func is aten._fused_rms_norm_backward.default:
+                    return table[func](*args, **kwargs)
+                if func is aten._to_copy.default and kwargs.get("device") is not None:
+                    kwargs = {**kwargs, "device": torch.device("cpu")}
+                return func(*args, **kwargs)
+
+        self._mode = _Mode()
+        self._mode.__enter__()
+        return self
+
+    def __exit__(self, *exc):
+        return self._mode.__exit__(*exc)
+
+
 def run(fragment_id: str, inputs):
     """Outputs of the fragment's eager op sequence (a tuple, or one tensor
     where the fragment returns a single output)."""

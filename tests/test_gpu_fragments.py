@@ -4,6 +4,10 @@ at the reference's full shapes: same output arity, shapes, strides, dtypes,
 the same aliasing between outputs, untouched inputs, and values within the
 tolerance of each output's kind.
 """
+import json
+import os
+from pathlib import Path
+
 import pytest
 import torch
 
@@ -39,6 +43,38 @@ RESIDUAL_SUM = {
 # fp32 outputs that carry no bf16 rounding (complex-multiply result):
 # fp32 reassociation / contraction differences only.
 F32_TOL = {"v7/0f38bc55457c": {0}}
+
+
+# The reference harness's pass criterion (tests/golden/make_tol_tiers.py):
+# max |out - ref| / (atol_eff + rtol |ref|) <= 1 with the fragment's tier.
+# Fragments without a result record use their family's tier at its base atol
+# (the RoPE captures: complex; the rest here: reduction).
+TOL_TIERS = json.loads((Path(__file__).resolve().parent / "golden" / "tol_tiers.json").read_text())
+BASE_TIERS = {"bitwise": (0.08, 1e-3), "reduction": (0.05, 1e-2), "complex": (0.05, 1e-2)}
+COMPLEX_WITHOUT_RECORD = {"v8/7e38211c7f1c", "v1/075cb40f3d5d", "v1/9cd8f72e74ce", "v1/f23f9bb4567a",
+                          "v1/d7efc428b2f5"}
+
+
+def _tier(fid):
+    for f in (fid, fr.SAME_AS.get(fid), fr.EQUIVALENT.get(fid), fr.EQUIVALENT.get(fr.SAME_AS.get(fid, ""))):
+        if f in TOL_TIERS:
+            t = TOL_TIERS[f]
+            return t["tier"], t["atol_eff"], t["rtol"]
+    canon = fr.EQUIVALENT.get(fr.SAME_AS.get(fid, fid), fr.SAME_AS.get(fid, fid))
+    tier = "complex" if canon in COMPLEX_WITHOUT_RECORD else "reduction"
+    return (tier, *BASE_TIERS[tier])
+
+
+def max_tol_units(ours, ref, atol, rtol):
+    worst = 0.0
+    for a, e in zip(ours, ref):
+        if a.is_complex():
+            a, e = torch.view_as_real(a), torch.view_as_real(e)
+        if a.numel() == 0:
+            continue
+        d = (a.double() - e.double()).abs() / (atol + rtol * e.double().abs())
+        worst = max(worst, float(d.max()))
+    return worst
 
 
 def _tuple(o):
@@ -116,3 +152,11 @@ def test_fragment_matches_eager(fid, gpu):
             same_ref = _storage(ref[i]) == _storage(ref[j])
             same_ours = _storage(ours[i]) == _storage(ours[j])
             assert same_ref == same_ours, f"{fid}: aliasing of outputs {i} and {j} differs from the fragment's"
+    tier, atol, rtol = _tier(fid)
+    units = max_tol_units(ours, ref, atol, rtol)
+    print(f"[fragment] {fid}: max_tol_units {units:.4f} ({tier}, atol_eff {atol:g}, rtol {rtol:g})", flush=True)
+    if os.environ.get("KP_TOL_REPORT"):
+        with open(os.environ["KP_TOL_REPORT"], "a") as f:
+            f.write(json.dumps({"fragment": fid, "tier": tier, "atol_eff": atol, "rtol": rtol,
+                                "max_tol_units": units}) + "\n")
+    assert units <= 1.0, f"{fid}: max_tol_units {units:.4f} > 1 (the reference harness's {tier} tier)"
