@@ -95,29 +95,33 @@ __global__ __launch_bounds__(kThreads) void rms_bwd_generic(RmsBwdArgs a) {
   }
 }
 
-// dw[c] = sum_{p < P} partial[p, c].  A block owns one 32-column chunk, whose
-// P partial rows are contiguous ([P][32] fp32).  Thread (r, q) sums columns
-// 4q..4q+3 over rows r, r + 32, r + 64, ... in row order; the 32 row-group
-// sums are then added in group order.  Loads go out in batches of 8 rows.
-constexpr int kFinGroups = kThreads / (kPartChunk / 4);  // 32
+// dw[c] = sum_{p < P} partial[p, c].  A block owns one 16-column chunk, whose
+// P partial rows are contiguous ([P][16] fp32).  Thread (r, q) sums columns
+// 4q..4q+3 over rows r, r + 64, r + 128, ... in row order (loads in batches
+// of 4 rows: P = 256 is one batch); the 64 row-group sums of a column are
+// then added as 16 sums of 4 consecutive groups, and those 16 in order.  The
+// order is fixed, so the result is bitwise reproducible.
+constexpr int kFinGroups = kThreads / (kPartChunk / 4);  // 64
+constexpr int kFinPairs = kThreads / kPartChunk;         // 16
 
 __global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restrict__ partial, int P, int64_t N,
                                                             float* dw_f32, uint16_t* dw_bf16, int round_f32) {
   __shared__ float s[kFinGroups][kPartChunk + 1];
-  const int q = threadIdx.x & 7, r = threadIdx.x >> 3;
+  __shared__ float s2[kFinPairs][kPartChunk + 1];
+  const int q = threadIdx.x & 3, r = threadIdx.x >> 2;
   const int64_t c0 = (int64_t)blockIdx.x * kPartChunk;
   const float* base = partial + (int64_t)blockIdx.x * P * kPartChunk;
   const int ncol = (int)(N - c0 < kPartChunk ? N - c0 : kPartChunk);
   f32x4 acc = {0.f, 0.f, 0.f, 0.f};
   if (ncol == kPartChunk) {
     int p = r;
-    for (; p + 7 * kFinGroups < P; p += 8 * kFinGroups) {
-      f32x4 v[8];
+    for (; p + 3 * kFinGroups < P; p += 4 * kFinGroups) {
+      f32x4 v[4];
 #pragma unroll
-      for (int k = 0; k < 8; ++k)
+      for (int k = 0; k < 4; ++k)
         v[k] = *reinterpret_cast<const f32x4*>(base + (int64_t)(p + k * kFinGroups) * kPartChunk + q * 4);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) acc += v[k];
+      for (int k = 0; k < 4; ++k) acc += v[k];
     }
     for (; p < P; p += kFinGroups) acc += *reinterpret_cast<const f32x4*>(base + (int64_t)p * kPartChunk + q * 4);
   } else {
@@ -132,9 +136,15 @@ __global__ __launch_bounds__(kThreads) void rms_dw_finalize(const float* __restr
 #pragma unroll
   for (int k = 0; k < 4; ++k) s[r][q * 4 + k] = acc[k];
   __syncthreads();
+  {
+    const int c = threadIdx.x & (kPartChunk - 1), g = threadIdx.x / kPartChunk;  // g < 16
+    s2[g][c] = ((s[4 * g][c] + s[4 * g + 1][c]) + s[4 * g + 2][c]) + s[4 * g + 3][c];
+  }
+  __syncthreads();
   if (threadIdx.x < ncol) {
-    float t = s[0][threadIdx.x];
-    for (int g = 1; g < kFinGroups; ++g) t += s[g][threadIdx.x];
+    float t = s2[0][threadIdx.x];
+#pragma unroll
+    for (int g = 1; g < kFinPairs; ++g) t += s2[g][threadIdx.x];
     const int64_t c = c0 + threadIdx.x;
     if (dw_bf16) dw_bf16[c] = f_to_bf(t);
     if (dw_f32) dw_f32[c] = round_f32 ? round_bf(t) : t;

@@ -72,10 +72,11 @@ struct RmsBwdArgs {
   float eps;
 };
 
-// Weight-gradient partials are stored column-chunk-major, [ceil(N/32)][P][32]
-// fp32 (P = row blocks): a block's partial row lands as full 128-byte lines
-// and the finalize reads each 32-column chunk of all P rows contiguously.
-constexpr int kPartChunk = 32;
+// Weight-gradient partials are stored column-chunk-major, [ceil(N/16)][P][16]
+// fp32 (P = row blocks): a lane's 8 columns land as 32 contiguous bytes, and
+// the finalize -- one block per 16-column chunk, N / 16 blocks, at least one
+// per CU for N >= 4096 -- reads each chunk of all P rows contiguously.
+constexpr int kPartChunk = 16;
 __host__ __device__ __forceinline__ int64_t part_index(int64_t c, int64_t p, int64_t P) {
   return ((c / kPartChunk) * P + p) * kPartChunk + (c % kPartChunk);
 }
