@@ -29,6 +29,8 @@ BASELINE.json configurations:
   cef  cross-entropy forward  logits [8192, 128256] bf16, targets -> loss, total_weight (v8/71f1d2c9f38b)
   ceb  cross-entropy backward log-softmax [8192, 128256] fp32, targets -> bf16 grad   (v8/622c35f5d1c6)
   cefb cross-entropy fwd+bwd  logits [8192, 128256] bf16, targets -> bf16 grad, one pass (v5/fb5b36393cbd)
+  nfb  RMSNorm fwd + bwd      x, 3 dy, res [8192, 4096] -> y, g, dw in one row pass (v6/0b493aad68f0)
+  nfb2 the same as the forward kernel then the backward kernel (the composition nfb replaces)
 
 Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 ~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
@@ -614,7 +616,80 @@ class CrossEntropyFwdBwd(Workload):
         torch_ref.cross_entropy_fwd_bwd(self.logits[:self.cpu_rows], self.targets[:self.cpu_rows], 1.0 / 8192.0)
 
 
+# ------------------------------------------------------------ norm fwd + bwd
+class NormFwdBwd(Workload):
+    """The RMSNorm forward -> backward region of the chain fragments
+    (v6/0b493aad68f0/problem.py:16-47) at their shape: x [8192, 4096], dy =
+    three gradient terms, g = add_220 + dx.  one_pass=True: one row pass
+    (kp_rmsnorm_fwd_bwd_bf16, x read once: 5 arrays read, y and g written);
+    one_pass=False: the forward kernel then the backward kernel with its rstd
+    (x read twice, rstd written and read) -- the composition it replaces."""
+
+    def __init__(self, dev, M=8192, N=4096, one_pass=True, name="nfb"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        g = _gen(0)
+        self.x = _randn((M, N), g)
+        self.dys = [_randn((M, N), g) for _ in range(3)]
+        self.res = _randn((M, N), g)
+        self.w = _randn(N, g, 1.0, 0.02)
+        eps = 1e-5
+        nb = M * N * 2
+        self.bytes_per_call = 7 * nb + N * 2 + N * 4 if one_pass else 9 * nb + N * 2 + N * 4 + 2 * M * 4
+        self.dominant_bytes = 7 * nb + N * 2 if one_pass else 6 * nb + N * 2 + M * 4
+        self.dominant_kernel = "rms_bwd_vec<.., FWD>" if one_pass else "rms_bwd_vec (after rms_fwd_vec)"
+        self.probe_mix = None  # 5 reads + 2 writes: past what kp_stream_probe streams (<= 4 reads)
+        self.description = (f"RMSNorm forward + backward of the chain fragments (v6/0b493aad68f0): x, 3 dy terms, "
+                            f"residual [{M},{N}] bf16 -> y, g = res + dx bf16, dw fp32; "
+                            + ("one row pass" if one_pass else "forward kernel then backward kernel"))
+        lib = L.lib()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        R = self.rotations(self.bytes_per_call)
+        xd, wd, rd = self.x.to(dev), self.w.to(dev), self.res.to(dev)
+        dyd = [d.to(dev) for d in self.dys]
+        ws_bytes = int(lib.kp_rmsnorm_fwd_bwd_workspace_size(M, N))
+        for r in range(R):
+            xs, rs = xd.clone(), rd.clone()
+            dys = [d.clone() for d in dyd]
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            gout = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            dw = torch.empty(N, dtype=torch.float32, device=dev)
+            rstd = torch.empty(M, dtype=torch.float32, device=dev)
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            dpa, dsa = L.ptr_array([d.data_ptr() for d in dys]), L.i64_array([N] * 3)
+            xpa, xsa = L.ptr_array([xs.data_ptr()]), L.i64_array([N])
+            keep = (xs, rs, dys, y, gout, dw, rstd, ws, dpa, dsa, xpa, xsa, wd)
+            if one_pass:
+                args = (dpa, dsa, 3, xpa, xsa, 1, wd.data_ptr(), N, N, None, N, y.data_ptr(), N, None,
+                        rs.data_ptr(), N, gout.data_ptr(), N, dw.data_ptr(), None, 1, M, N, eps, ws.data_ptr(),
+                        ws_bytes, stream)
+                self.sets.append((lib.kp_rmsnorm_fwd_bwd_bf16, args, keep))
+            else:
+                fa = (xpa, xsa, 1, wd.data_ptr(), N, N, None, N, y.data_ptr(), N, rstd.data_ptr(), M, N, eps, stream)
+                ba = (dpa, dsa, 3, xpa, xsa, 1, rstd.data_ptr(), wd.data_ptr(), N, N, rs.data_ptr(), N,
+                      gout.data_ptr(), N, dw.data_ptr(), None, 1, M, N, eps, ws.data_ptr(), ws_bytes, stream)
+
+                def both(fa=fa, ba=ba):
+                    st = lib.kp_rmsnorm_fwd_bf16(*fa)
+                    return st if st != 0 else lib.kp_rmsnorm_bwd_bf16(*ba)
+                both.__name__ = "kp_rmsnorm_fwd_bf16 + kp_rmsnorm_bwd_bf16"
+                self.sets.append((both, (), keep))
+        self.cpu_sample = f"full [{M},{N}] call"
+
+    def cpu_run(self):
+        from oracle import torch_ref
+        torch_ref.rms_norm_fwd(self.x, self.w, 1e-5)
+        dy = self.dys[0] + self.dys[1] + self.dys[2]
+        torch_ref.rms_norm_bwd(self.x, dy, self.w, 1e-5)
+
+
 def make_workload(name, dev):
+    if name == "nfb":
+        return NormFwdBwd(dev, one_pass=True, name="nfb")
+    if name == "nfb2":
+        return NormFwdBwd(dev, one_pass=False, name="nfb2")
     if name == "c1":
         return RmsFwd(dev, 4096, 4096, 1e-6, "c1")
     if name == "c2":
@@ -651,7 +726,7 @@ def make_workload(name, dev):
 
 
 ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c64r", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb",
-       "cefb"]
+       "cefb", "nfb", "nfb2"]
 # The BASELINE.json configurations: every default run measures each of them.
 CONFIGS = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
 

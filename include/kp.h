@@ -472,6 +472,14 @@ int kp_cross_entropy_fwd_bwd_bf16(const void* logits, int64_t row_stride, int64_
                                   float scale, float* loss, float* total_weight, int32_t* error_flag,
                                   void* workspace, size_t workspace_bytes, void* stream);
 
+/* Self-test of the SwiGLU arithmetic (no counterpart in the reference): for
+ * every bf16 bit pattern i (65536 of each, uint32 device arrays) writes the
+ * fp32 bits of the fast sigmoid used by the backward kernels and of the IEEE
+ * quotient 1 / (1 + expf(-x)) it stands for, and of the fast bf16 silu used by
+ * the forward kernels and of bf16(x / (1 + expf(-x))).  tests/ compare them. */
+int kp_swiglu_math_selftest(uint32_t* sig_fast, uint32_t* sig_ieee, uint32_t* silu_fast, uint32_t* silu_ref,
+                            void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -15,6 +15,7 @@ Layers:
 from . import aten, fused
 from ._lib import KPError, LIB_PATH, version
 from .fused import (
+    check_indices,
     cross_entropy_backward,
     cross_entropy_forward_backward,
     cross_entropy_loss,
@@ -39,6 +40,7 @@ __all__ = [
     "KPError",
     "LIB_PATH",
     "aten",
+    "check_indices",
     "cross_entropy_backward",
     "cross_entropy_forward_backward",
     "cross_entropy_loss",

@@ -105,6 +105,7 @@ SIGNATURES = {
     "kp_swiglu_bwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, vp]),
     "kp_silu_bf16": (i32, [vp, i64, vp, i64, i64, i64, vp]),
     "kp_swiglu_fwd_bwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, vp, i64, i64, i64, vp]),
+    "kp_swiglu_math_selftest": (i32, [vp, vp, vp, vp, vp]),
     "kp_cross_entropy_fwd_workspace_size": (sz, [i64]),
     "kp_cross_entropy_fwd_bf16": (i32, [vp, i64, i64, i64, vp, i32, i64, f32, vp, vp, vp, vp, vp, sz, vp]),
     "kp_cross_entropy_bwd_bf16": (i32, [vp, i64, vp, i32, i64, f32, vp, i64, i64, i64, vp, vp]),
@@ -132,12 +133,17 @@ def lib() -> C.CDLL:
     return _lib
 
 
+_fns = {}
+
+
 def call(name: str, *args) -> None:
     """Calls an entry point and raises KPError on a non-zero status."""
-    l = lib()
-    st = getattr(l, name)(*args)
+    fn = _fns.get(name)
+    if fn is None:
+        fn = _fns[name] = getattr(lib(), name)
+    st = fn(*args)
     if st != KP_OK:
-        msg = l.kp_last_error_message().decode(errors="replace")
+        msg = lib().kp_last_error_message().decode(errors="replace")
         raise KPError(name, st, msg)
 
 

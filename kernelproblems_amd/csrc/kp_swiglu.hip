@@ -38,9 +38,9 @@ __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x));
 
 // sig = fl(1 / fl(1 + expf(-x))) as eager computes it.  For |x| < 16 the
 // IEEE division is replaced by rcp and one Newton step, which gives the same
-// fp32 value for every bf16 x in that range (all 33536 of them, checked on
-// gfx950; the exhaustive test of silu_backward over every bf16 input is in
-// tests/test_gpu_swiglu.py): ~3 VALU instructions instead of ~10.
+// fp32 value for every bf16 x in that range (all 33536 of them: compared bit
+// for bit on the device by kp_swiglu_math_selftest in tests/test_gpu_swiglu.py):
+// ~3 VALU instructions instead of ~10.
 __device__ __forceinline__ float sigmoid_f(float x) {
   const float d = 1.0f + expf(-x);
   if (!(__builtin_fabsf(x) < 16.0f)) return 1.0f / d;
@@ -311,12 +311,35 @@ int launch_pointwise(const char* who, int op, const void* const* in, const int64
   return check_launch(who);
 }
 
+// Self-test of the arithmetic above over every bf16 input (x = bit pattern
+// i): the fast sigmoid against the IEEE quotient it replaces, and the fast
+// bf16 silu against the bf16 rounding of silu_f, as fp32 bit patterns.
+__global__ __launch_bounds__(kThreads) void swiglu_math_bits(uint32_t* sig_fast, uint32_t* sig_ieee,
+                                                             uint32_t* silu_fast, uint32_t* silu_ref) {
+  const int i = blockIdx.x * kThreads + threadIdx.x;
+  if (i >= 65536) return;
+  const float x = bf_to_f((uint16_t)i);
+  sig_fast[i] = __float_as_uint(sigmoid_f(x));
+  sig_ieee[i] = __float_as_uint(1.0f / (1.0f + expf(-x)));
+  silu_fast[i] = __float_as_uint(silu_bf16(x));
+  silu_ref[i] = __float_as_uint(round_bf(silu_f(x)));
+}
+
 }  // namespace
 }  // namespace kp
 
 using namespace kp;
 
 extern "C" {
+
+int kp_swiglu_math_selftest(uint32_t* sig_fast, uint32_t* sig_ieee, uint32_t* silu_fast, uint32_t* silu_ref,
+                            void* stream) {
+  static const char* who = "kp_swiglu_math_selftest";
+  if (!sig_fast || !sig_ieee || !silu_fast || !silu_ref) return fail(KP_EINVAL, "%s: NULL output", who);
+  hipLaunchKernelGGL(swiglu_math_bits, dim3(65536 / kThreads), dim3(kThreads), 0, as_stream(stream), sig_fast,
+                     sig_ieee, silu_fast, silu_ref);
+  return check_launch(who);
+}
 
 int kp_swiglu_fwd_bf16(const void* a, int64_t a_rs, const void* b, int64_t b_rs, void* out, int64_t out_rs, int64_t M,
                        int64_t N, void* stream) {

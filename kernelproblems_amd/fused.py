@@ -25,19 +25,43 @@ _index_checking = os.environ.get("KP_CHECK_INDICES", "0") not in ("", "0")
 
 def set_index_checking(enabled: bool) -> None:
     """When enabled, index-taking ops synchronise after the launch and raise
-    IndexError if an id/position was out of range (the kernels never read out
-    of bounds; unchecked, such rows come out as zeros)."""
+    IndexError if an id / position / target was out of range.  When disabled
+    (the default: no host synchronisation per call) the kernels still never
+    read out of bounds -- such rows come out as zeros (targets count as
+    ignored) -- and still record the event in a per-device flag that
+    check_indices() reports."""
     global _index_checking
     _index_checking = bool(enabled)
+    # (switching modes keeps what unchecked calls recorded for check_indices;
+    # each checked call clears the record before it runs)
 
 
 def index_checking() -> bool:
     return _index_checking
 
 
+_flags = {}
+
+
+def check_indices() -> None:
+    """Raises IndexError if any index-taking call on any device met an
+    out-of-range id, position or target since the last check (or since it
+    raised), then clears the record.  Synchronises the devices that have
+    made such calls; call it where a synchronisation is paid anyway (e.g.
+    once per step)."""
+    bad = [i for i, f in _flags.items() if int(f.item()) != 0]
+    for i in bad:
+        _flags[i].zero_()
+    if bad:
+        raise IndexError(f"index out of range in a kernel call on device(s) {bad} since the last check")
+
+
 # ---------------------------------------------------------------- helpers
 def _stream(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw hipStream_t of the device's current torch stream (read without
+    building a Stream object: this runs on every call)."""
+    idx = device.index
+    return torch._C._cuda_getCurrentRawStream(idx if idx is not None else torch.cuda.current_device())
 
 
 def _need_gpu(name: str, t: torch.Tensor, dtype: Optional[torch.dtype] = torch.bfloat16) -> None:
@@ -52,11 +76,14 @@ def _need_gpu(name: str, t: torch.Tensor, dtype: Optional[torch.dtype] = torch.b
 def _as_rows(t: torch.Tensor, n: int):
     """Returns (tensor, row_stride, rows) for t viewed as [rows, n] with unit
     inner stride; copies to contiguous only if no such view exists."""
-    if t.numel() % n != 0:
-        raise RuntimeError(f"tensor of {t.numel()} elements is not a whole number of rows of {n}")
-    m = t.numel() // n
+    numel = t.numel()
+    if numel % n != 0:
+        raise RuntimeError(f"tensor of {numel} elements is not a whole number of rows of {n}")
+    m = numel // n
     if m == 0:
         return t, n, 0
+    if t.is_contiguous():
+        return t, n, m
     try:
         v = t.view(m, n)
         if n == 1 or v.stride(1) == 1:
@@ -84,14 +111,23 @@ def _weight_segments(w: torch.Tensor, n: int):
 
 
 def _flag(device: torch.device):
-    """A zeroed int32 error flag when index checking is on, else None."""
-    if not _index_checking:
-        return None
-    return torch.zeros(1, dtype=torch.int32, device=device)
+    """The device's persistent int32 out-of-range flag (allocated on first
+    use; kernels only ever set it, check_indices() clears it).  In checking
+    mode it is cleared before the call, so that the check after the call
+    reports that call alone."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    f = _flags.get(idx)
+    if f is None:
+        f = _flags[idx] = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", idx))
+    elif _index_checking:
+        f.zero_()
+    return f
 
 
 def _raise_if_flagged(flag, what: str) -> None:
-    if flag is not None and int(flag.item()) != 0:
+    """With index checking on: synchronise and raise if the flag is set."""
+    if _index_checking and flag is not None and int(flag.item()) != 0:
+        flag.zero_()
         raise IndexError(f"{what}: index out of range")
 
 

@@ -43,6 +43,27 @@ def test_embedding_fwd_out_of_range_flagged(gpu):
         kp.embedding(table, ids)
 
 
+def test_out_of_range_recorded_without_checking_mode(gpu):
+    """With per-call checking off (the default outside the tests), an
+    out-of-range id gives zero rows without a host synchronisation and is
+    reported by the next kp.check_indices(); the record is then cleared."""
+    table = torch.ones((10, 64), dtype=torch.bfloat16, device=gpu)
+    kp.set_index_checking(False)
+    try:
+        kp.check_indices()  # nothing recorded yet (or cleared)
+        out = kp.embedding(table, torch.tensor([1, 10, 3], device=gpu))
+        assert torch.count_nonzero(out[1]) == 0 and torch.count_nonzero(out[0]) == 64
+        grad = torch.ones((3, 64), dtype=torch.bfloat16, device=gpu)
+        kp.embedding_dense_backward(grad, torch.tensor([1, -5, 3], device=gpu), 10)
+        with pytest.raises(IndexError):
+            kp.check_indices()
+        kp.check_indices()  # cleared by the report
+        kp.embedding(table, torch.tensor([1, 2, 3], device=gpu))
+        kp.check_indices()
+    finally:
+        kp.set_index_checking(True)
+
+
 def _check_bwd(gpu, O, V, D, ids, grad, padding_idx=-1, scale=False):
     T = ids.numel()
     out = kp.embedding_dense_backward(grad.to(gpu), ids.to(gpu), V, padding_idx, scale)

@@ -213,3 +213,24 @@ def test_silu_backward_every_bf16_input_bitwise(gpu, op):
     same = (da.view(torch.int16) == ref.view(torch.int16)) | (torch.isnan(da) & torch.isnan(ref))
     bad = (~same).flatten().nonzero().flatten().tolist()
     assert not bad, f"{len(bad)} inputs differ, e.g. a={a.flatten()[bad[:5]].tolist()}"
+
+
+def test_fast_sigmoid_and_silu_arithmetic_every_bf16_input(gpu):
+    """The identities the kernels rely on, checked on the device over all
+    65536 bf16 bit patterns, fp32 bit for bit: the rcp + Newton sigmoid of the
+    backward equals the IEEE quotient 1 / (1 + expf(-x)) for every x with
+    |x| < 16 (the range it is used in), and the forward's fast bf16 silu
+    equals the bf16 rounding of x / (1 + expf(-x)) for every input (NaN as
+    NaN)."""
+    from kernelproblems_amd import _lib as L
+
+    outs = [torch.empty(65536, dtype=torch.int32, device=gpu) for _ in range(4)]
+    L.call("kp_swiglu_math_selftest", *[o.data_ptr() for o in outs], torch.cuda.current_stream().cuda_stream)
+    sf, si, lf, lr = (o.cpu().numpy().view(np.uint32) for o in outs)
+    x = (np.arange(65536, dtype=np.uint32) << 16).view(np.float32)
+    used = np.abs(x) < 16  # False for NaN
+    assert int(used.sum()) == 33536
+    assert np.array_equal(sf[used], si[used]), f"{int((sf[used] != si[used]).sum())} sigmoid values differ"
+    nan = np.isnan(lr.view(np.float32))
+    assert np.array_equal(np.isnan(lf.view(np.float32)), nan)
+    assert np.array_equal(lf[~nan], lr[~nan]), f"{int((lf[~nan] != lr[~nan]).sum())} silu values differ"
