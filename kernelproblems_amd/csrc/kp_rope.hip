@@ -3,8 +3,10 @@
 // One wave64 per (b, s) position handles every head of q and k at that
 // position, so the D/2 rotation angles are produced once per position and
 // shared by all H_q + H_k heads:
-//   - theta mode: lane f computes inv_freq[f] once per kernel (in fp64, rounded
-//     to fp32), then per position a = fp32(fp32(p) * inv_freq[f]) and
+//   - theta mode: inv_freq[f] = fp32(theta^(-2f/D)) (fp64 pow; for D = 128
+//     evaluated once per call on the host and passed in the kernel
+//     arguments, else by lane f in every wave), then per position
+//     a = fp32(fp32(p) * inv_freq[f]) and
 //     sincosf(a) (full-range OCML reduction, not a fast approximation).  The
 //     D/2 (cos, sin) pairs go to a per-wave LDS slot and are read back by the
 //     lanes that need them.
@@ -47,6 +49,11 @@ struct RopeArgs {
   int64_t frows, frs;  // rows, row stride in complex elements
   int conj;
   int32_t* err;
+  // theta mode with D = 128: inv_freq[f] = fp32(theta^(-2f/D)), evaluated
+  // once per call on the host (have_inv = 1) instead of in every wave (both
+  // kernels then read it, so their angles stay identical)
+  int have_inv;
+  float inv_freq[64];
 };
 
 // Output element offset o gets 8 values (16-byte bf16 / 32-byte fp32) or 1 value.
@@ -86,7 +93,9 @@ __global__ __launch_bounds__(kThreads) void rope_kernel(RopeArgs a) {
 #pragma unroll
   for (int k = 0; k < kMaxHalf / 64; ++k) {
     const int f = lane + 64 * k;
-    inv[k] = (!table && f < half) ? (float)pow(a.theta, -(double)(2 * f) / (double)a.D) : 0.f;
+    inv[k] = (!table && f < half)
+                 ? (a.have_inv ? a.inv_freq[f & 63] : (float)pow(a.theta, -(double)(2 * f) / (double)a.D))
+                 : 0.f;
   }
 
   const int64_t npos = a.B * a.S;
@@ -237,7 +246,7 @@ constexpr int kFastD = 128;
 constexpr int kFastMaxLoads = 16;
 
 template <int PAIRING, bool TABLE, int UPL>
-__global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
+__device__ __forceinline__ void rope_fast_body(const RopeArgs& a) {
   constexpr bool kHalf = PAIRING == KP_ROPE_HALF;
   constexpr int HD = kFastD / 2;
   constexpr int CPH = kHalf ? kFastD / 16 : kFastD / 8;  // units per head
@@ -290,7 +299,7 @@ __global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
     }
   } else {
     // lane f < D/2 produces angle f: fp32(fp32(p) * fp32(theta^(-2f/D)))
-    const float inv = (float)pow(a.theta, -(double)(2 * lane) / (double)kFastD);
+    const float inv = a.have_inv ? a.inv_freq[lane] : (float)pow(a.theta, -(double)(2 * lane) / (double)kFastD);
     float sn, cn;
     sincosf((float)p * inv, &sn, &cn);
     cs[wave][0][lane] = cn;
@@ -351,6 +360,11 @@ __global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
       }
     }
   }
+}
+
+template <int PAIRING, bool TABLE, int UPL>
+__global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
+  rope_fast_body<PAIRING, TABLE, UPL>(a);
 }
 
 typedef void (*RopeKernel)(RopeArgs);
@@ -454,6 +468,10 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
   a.frs = freq_row_stride;
   a.conj = conj ? 1 : 0;
   a.err = error_flag;
+  if (freqs_cis == nullptr && D == kFastD) {  // the fast kernel's angles: one evaluation per call
+    a.have_inv = 1;
+    for (int f = 0; f < kFastD / 2; ++f) a.inv_freq[f] = (float)pow(theta, -(double)(2 * f) / (double)kFastD);
+  }
   const int64_t npos = B * S;
   if (npos == 0) return KP_OK;
 
