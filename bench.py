@@ -857,6 +857,75 @@ def measure_probe(wl, steps, warmup):
             "chunks_per_thread": best, "us_by_tile": {str(k): round(v * 1e3, 3) for k, v in per_tile.items()}}
 
 
+def _tensors(x):
+    return [t for y in x for t in _tensors(y)] if isinstance(x, (tuple, list)) else [x]
+
+
+def _view_bytes(ts):
+    """Bytes of each distinct tensor view (a view is counted once even when
+    passed twice; an output returned as several views of one storage counts
+    once)."""
+    seen, total = set(), 0
+    for t in ts:
+        key = (t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), tuple(t.stride()))
+        if key not in seen:
+            seen.add(key)
+            total += t.numel() * t.element_size()
+    return total
+
+
+def measure_fragments(dev, steps, warmup):
+    """Every distinct fragment drop-in (kernelproblems_amd.fragments) at its
+    reference shape: kernel_function on rotating get_inputs sets (>= 1 GiB of
+    inputs or 2 sets), K calls timed with synchronisation on both sides.
+    moved_bytes = every input view and every distinct output once (an upper
+    bound where a fragment reads part of an input, e.g. the y of a saved
+    (y, rstd) tuple).  ref = the reference's own record of the fragment (its
+    eager time and fastest passing candidate on its H100), where it has one."""
+    import torch
+    from kernelproblems_amd import fragments as fr
+    try:
+        ref = json.loads((ROOT / "tests" / "golden" / "reference_times.json").read_text())
+    except (OSError, ValueError):
+        ref = {}
+    out = {}
+    ids = [f for f in fr.FRAGMENTS if f not in fr.SAME_AS and f not in fr.EQUIVALENT]
+    for fid in ids:
+        mod = fr.load(fid)
+        first = mod.get_inputs(device=dev, generator=torch.Generator(device=dev).manual_seed(1))
+        in_b = _view_bytes(_tensors(first))
+        R = max(2, min(8, math.ceil(MIN_ROTATION_BYTES / max(in_b, 1))))
+        sets = [first] + [mod.get_inputs(device=dev, generator=torch.Generator(device=dev).manual_seed(i + 2))
+                          for i in range(R - 1)]
+        res = mod.kernel_function(*sets[0])
+        out_b = _view_bytes(_tensors(res))
+        del res
+        for i in range(warmup):
+            mod.kernel_function(*sets[i % R])
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            mod.kernel_function(*sets[i % R])
+        torch.cuda.synchronize()
+        us = (time.perf_counter() - t0) * 1e6 / steps
+        gbs = (in_b + out_b) / us / 1e3
+        rec = {"us_per_call": round(us, 2), "moved_bytes": in_b + out_b,
+               # a gather reads only some rows of the table / flat buffer it is
+               # given: there moved_bytes overstates the traffic, and no rate
+               "GBps": round(gbs, 1) if gbs <= PEAK_GBS else None}
+        r = ref.get(fid)
+        if r:
+            rec["ref"] = r
+        out[fid] = rec
+        print(f"[bench] fragment {fid}: {us:.1f} us/call, {(in_b + out_b) / 1e6:.1f} MB moved"
+              + (f"; reference best {r['best_ms'] * 1e3:.1f} us ({r['best_backend']}), eager "
+                 f"{r.get('eager_ms', float('nan')) * 1e3:.1f} us on its H100" if r and "best_ms" in r else ""),
+              file=sys.stderr, flush=True)
+        del sets, first
+        torch.cuda.empty_cache()
+    return out
+
+
 def _cpu_model():
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -920,6 +989,8 @@ def main():
                     help="measure the headline workload only (profiling runs); by default every BASELINE "
                          "configuration (c1, c2, c3f, c3b, c4, c5f, c5b) gets a block under 'configs'")
     ap.add_argument("--all", action="store_true", help="also measure every other workload (no CPU baseline)")
+    ap.add_argument("--fragments", action="store_true",
+                    help="also time every distinct fragment drop-in at its reference shape (GPU only)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-probe", action="store_true", help="skip the streaming-ceiling probe")
     ap.add_argument("--no-dropin", action="store_true", help="skip timing the tensor-level drop-ins")
@@ -1060,6 +1131,8 @@ def main():
                 "bytes_per_call": w2.bytes_per_call,
             }
         line["fragments"] = frags
+    if args.fragments:
+        line["fragment_drop_ins"] = measure_fragments(dev, args.steps, args.warmup)
     print(json.dumps(line), flush=True)
     return 0
 

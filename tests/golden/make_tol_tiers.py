@@ -12,6 +12,11 @@ harness's own, where a candidate's record carries one; else computed from
 the torch.compile entry).  Fragments without a record get no entry; the
 tests then use the tier of their family at the base atol.
 
+It also writes tests/golden/reference_times.json: each record's eager time
+and its fastest passing candidate (backend, time), the reference's own
+per-fragment figures on its (H100) hardware, which bench.py --fragments
+prints beside this build's times.
+
     python tests/golden/make_tol_tiers.py
 """
 from __future__ import annotations
@@ -21,14 +26,30 @@ from pathlib import Path
 
 REFERENCE = Path("/root/reference")
 OUT = Path(__file__).resolve().parent / "tol_tiers.json"
+TIMES = Path(__file__).resolve().parent / "reference_times.json"
 TIERS = {"bitwise": (0.08, 1e-3), "reduction": (0.05, 1e-2), "complex": (0.05, 1e-2)}
 
 
+def times(rec):
+    best = None
+    for k, v in rec.items():
+        if isinstance(v, dict) and v.get("status") == "PASS" and "time_ms" in v:
+            if best is None or v["time_ms"] < best[1]:
+                best = (k, float(v["time_ms"]))
+    out = {"eager_ms": float(rec["eager_ms"])} if rec.get("eager_ms") is not None else {}
+    if best:
+        out.update({"best_backend": best[0], "best_ms": best[1]})
+    return out
+
+
 def main():
-    out = {}
+    out, tm = {}, {}
     for f in sorted(REFERENCE.glob("v*/*/benchmark.json")):
         rec = json.loads(f.read_text())
         fid = f"{f.parent.parent.name}/{f.parent.name}"
+        t = times(rec)
+        if t:
+            tm[fid] = t
         tier = atol_eff = rtol = compile_err = None
         for k, v in rec.items():
             if not isinstance(v, dict):
@@ -46,7 +67,8 @@ def main():
             rtol = base_rtol
         out[fid] = {"tier": tier, "atol_eff": atol_eff, "rtol": rtol, "compile_max_abs_err": compile_err}
     OUT.write_text(json.dumps(out, indent=1, sort_keys=True) + "\n")
-    print(f"wrote {OUT}: {len(out)} fragments")
+    TIMES.write_text(json.dumps(tm, indent=1, sort_keys=True) + "\n")
+    print(f"wrote {OUT}: {len(out)} fragments; {TIMES}: {len(tm)}")
 
 
 if __name__ == "__main__":
