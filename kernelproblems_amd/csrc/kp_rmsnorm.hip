@@ -180,9 +180,9 @@ int fwd_bpc(int64_t wave_slot_bytes) {
   return v ? v : auto_bpc(4, wave_slot_bytes, 128 * 1024, 8);
 }
 // At most 4 blocks per CU: the workspace holds one partial row per block.
-int bwd_bpc(int64_t wave_slot_bytes) {
+int bwd_bpc(int waves_per_block, int64_t wave_slot_bytes) {
   static const int v = env_int("KP_RMS_BWD_BPC", 0, 0, 4);
-  return v ? v : auto_bpc(kThreads / 64, wave_slot_bytes, 64 * 1024, 4);
+  return v ? v : auto_bpc(waves_per_block, wave_slot_bytes, 64 * 1024, 4);
 }
 
 // Fast-path row shapes: N = 512 * VPL * WPR, at most 5 16-byte chunks per
@@ -225,6 +225,23 @@ bool pick_vec(int64_t N, bool forward, int* vpl, int* wpr) {
     }
   }
   return false;
+}
+
+// Backward row shape: N = 8192 runs 8 waves per row with 2 chunks per lane in
+// 8-wave blocks (one row per block step; measured on MI355X at [16384, 8192]
+// with two x terms: 171.5 us against 175.5 us for 4 waves x 4 chunks in
+// 4-wave blocks, whose grid-wide row pass is otherwise the same).  Every other
+// width takes pick_vec's shape in 4-wave blocks.  *nw = waves per block.
+bool pick_bwd(int64_t N, int* vpl, int* wpr, int* nw) {
+  static const bool knobs = getenv("KP_RMS_VPL_MAX") != nullptr || getenv("KP_RMS_WPR_MIN") != nullptr;
+  if (N == 8192 && !knobs) {
+    *vpl = 2;
+    *wpr = 8;
+    *nw = 8;
+    return true;
+  }
+  *nw = kThreads / 64;
+  return pick_vec(N, false, vpl, wpr);
 }
 
 // Backward kernel for a fast-path shape, from its instantiation unit (fwd:
@@ -296,6 +313,7 @@ size_t fwd_bwd_workspace_size(int64_t M, int64_t N) {
 struct BwdPlan {
   BwdKernel vec;   // vectorized kernel, or nullptr for rms_bwd_generic
   int wpr;         // waves per row of the vectorized kernel
+  int threads;     // threads per block
   int blocks;      // row blocks = partial rows
   size_t lds;      // dynamic LDS of the vectorized kernel
 };
@@ -304,21 +322,21 @@ BwdPlan plan_bwd(const void* const* dy_terms, const int64_t* dy_strides, int n_d
                  const int64_t* x_strides, int n_x, const void* weight, int64_t w_seg_len, int64_t w_seg_stride,
                  const void* dx_residual, int64_t dxr_stride, const void* dx, int64_t dx_stride, bool want_dw,
                  const FwdOut* fo, int64_t M, int64_t N) {
-  BwdPlan p{nullptr, 1, 0, 0};
+  BwdPlan p{nullptr, 1, kThreads, 0, 0};
   if (M <= 0) return p;
-  int vpl = 0, wpr = 0;
-  bool vec = pick_vec(N, false, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) &&
+  int vpl = 0, wpr = 0, nw = kThreads / 64;
+  bool vec = pick_bwd(N, &vpl, &wpr, &nw) && rows_vec_ok(x_terms, x_strides, n_x) &&
              rows_vec_ok(dy_terms, dy_strides, n_dy) && aligned16(dx) && (dx_stride & 7) == 0;
   if (vec && dx_residual) vec = aligned16(dx_residual) && (dxr_stride & 7) == 0;
   if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
   if (vec && fo)
     vec = aligned16(fo->y) && (fo->ys & 7) == 0 && (fo->h == nullptr || (aligned16(fo->h) && (fo->hs & 7) == 0));
-  const int nw = kThreads / 64;
   p.vec = vec ? bwd_kernel(vpl, wpr, n_x, n_dy, dx_residual != nullptr, fo != nullptr) : nullptr;
   if (p.vec != nullptr) {
     const int rb = nw / wpr;
     p.wpr = wpr;
-    p.blocks = bwd_blocks(M, rb, bwd_bpc((int64_t)(n_x + n_dy + (dx_residual ? 1 : 0)) * vpl * 1024));
+    p.threads = nw * 64;
+    p.blocks = bwd_blocks(M, rb, bwd_bpc(nw, (int64_t)(n_x + n_dy + (dx_residual ? 1 : 0)) * vpl * 1024));
     p.lds = (want_dw && rb >= 2) ? (size_t)(rb / 2) * wpr * 512 * vpl * sizeof(float) : 0;
   } else {
     p.blocks = bwd_blocks(M, 1, 2);  // generic kernel: one row per block step, 2 blocks per CU
@@ -413,8 +431,8 @@ int rms_bwd_impl(const char* who, const void* const* dy_terms, const int64_t* dy
     }
     if (plan.vec != nullptr) {
       void* args[] = {&a};
-      launch_dominant_raw(reinterpret_cast<const void*>(plan.vec), dim3(plan.blocks), dim3(kThreads), args, plan.lds,
-                          s);
+      launch_dominant_raw(reinterpret_cast<const void*>(plan.vec), dim3(plan.blocks), dim3(plan.threads), args,
+                          plan.lds, s);
     } else {
       KP_LAUNCH_DOMINANT(rms_bwd_generic, dim3(plan.blocks), dim3(kThreads), 0, s, a);
     }
@@ -508,7 +526,13 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
   if (vec) {
     const int rb = 4 / wpr;
     const int64_t groups = ceil_div(M, rb);
-    const int64_t cap = (int64_t)cu_count() * fwd_bpc((int64_t)n_x * vpl * 1024);
+    // Rows of 4 waves (one row per block): one block per row, no persistent
+    // walk -- measured on MI355X at [16384, 8192] with two x terms: 170.5 us
+    // against 185 us for 2 pipelined blocks per CU.  Shorter rows (1 or 2
+    // waves) keep the pipelined grid ([4096, 4096]: 12.5 us against 13.8 us
+    // for one block per 4 rows).
+    const int64_t cap = wpr == 4 ? groups : (int64_t)cu_count() * fwd_bpc((int64_t)n_x * vpl * 1024);
+    if (groups > INT32_MAX) return fail(KP_EUNSUPPORTED, "%s: too many rows for one launch", who);
     const int grid = (int)(groups < cap ? groups : cap);
     void* args[] = {&a};
     launch_dominant_raw(reinterpret_cast<const void*>(fk), dim3(grid), dim3(kThreads), args, 0, s);
@@ -565,7 +589,9 @@ int kp_embedding_rmsnorm_fwd_bf16(const void* table, int64_t V, int64_t table_ro
     return fail(KP_EUNSUPPORTED, "%s: row shape / alignment without a fused kernel (N=%lld)", who, (long long)N);
   const int rb = 4 / wpr;
   const int64_t groups = ceil_div(T, rb);
-  const int64_t cap = (int64_t)cu_count() * fwd_bpc((int64_t)vpl * 1024);
+  // one block per row for rows of 4 waves, as in kp_rmsnorm_fwd_bf16
+  const int64_t cap = wpr == 4 ? groups : (int64_t)cu_count() * fwd_bpc((int64_t)vpl * 1024);
+  if (groups > INT32_MAX) return fail(KP_EUNSUPPORTED, "%s: too many rows for one launch", who);
   const int grid = (int)(groups < cap ? groups : cap);
   void* args[] = {&a};
   launch_dominant_raw(reinterpret_cast<const void*>(fk), dim3(grid), dim3(kThreads), args, 0, as_stream(stream));

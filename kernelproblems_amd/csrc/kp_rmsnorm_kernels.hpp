@@ -519,10 +519,10 @@ FwdKernel fwd_for_terms(int nx) {
 // epilogue) -- the ones the configurations and reference fragments use;
 // others run the generic kernel.
 // The fused forward + backward variants cover the chain fragments' terms:
-// (1 x, 1..3 dy, +- residual) and (2 x, 2 dy, residual).
-template <int VPL, int WPR>
+// (1 x, 1..3 dy, +- residual) and (2 x, 2 dy, residual).  NW waves per block
+// (4, or 8 for the 8-waves-per-row shape of N = 8192).
+template <int VPL, int WPR, int NW = kThreads / 64>
 BwdKernel bwd_for_terms(int nx, int ndy, bool res, bool fwd) {
-  constexpr int NW = kThreads / 64;
   if (fwd) {
     if (!res) {
       if (nx == 1 && ndy == 1) return rms_bwd_vec<VPL, WPR, 1, 1, false, NW, true>;
