@@ -16,6 +16,7 @@
 // [c*8, c*8+8) with [D/2 + c*8, ...); interleaved pairs are the 4 (2i, 2i+1)
 // pairs inside one chunk.  Arithmetic is fp32, one RNE rounding to bf16.
 #include <math.h>
+#include <stdlib.h>
 
 #include "kp_common.hpp"
 #include "kp_internal.hpp"
@@ -367,6 +368,158 @@ __global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
   rope_fast_body<PAIRING, TABLE, UPL>(a);
 }
 
+// ------------------------------------------------------------ tile path
+// D = 128, every tensor stored [B, S, H, 128] contiguously in and out (the
+// forward fragments and the rotate-half configuration), H a multiple of 4,
+// bf16 outputs.  Unlike rope_fast (one wave per position, up to 16 KiB per
+// wave), a block owns 512 consecutive 16-byte chunks of one tensor -- thread
+// t chunks t and t + 256, tensor 0's blocks first -- the short-lived,
+// fine-grained streaming layout that measured fastest on MI355X (c4: 56 us
+// against 58.5 us for rope_fast, bit-identical).  A head is 16 chunks, so a
+// lane's chunk index c = lane % 16 is fixed; a wave's 64 chunks are 4 heads
+// of one position (H % 4 == 0).  Rotate-half pairs chunk c with c ^ 8, i.e.
+// lane l with lane l ^ 8 of the same 16-lane DPP row (row_ror:8);
+// interleaved pairs are the 4 (2i, 2i+1) pairs inside a chunk.  Theta mode
+// evaluates the (cos, sin) of the tile's positions once per block (threads
+// f, f + 64, ... of position slot i / 64) into LDS behind one barrier; table
+// mode reads the position's row of the table (L2-resident).  Arithmetic,
+// rounding and angles are those of rope_fast, so both give identical bits.
+constexpr int kTileChunks = 2 * kThreads;
+constexpr int kTileMaxPos = kTileChunks / 64 + 1;  // H >= 4: a position is >= 64 chunks
+
+template <int PAIRING, bool TABLE>
+__global__ __launch_bounds__(kThreads) void rope_tile(RopeArgs a, int64_t nb0) {
+  constexpr bool kHalf = PAIRING == KP_ROPE_HALF;
+  constexpr int FPU = kHalf ? 8 : 4;  // angles per chunk
+  __shared__ float cs[TABLE ? 1 : kTileMaxPos][2][64];
+  const int lane = threadIdx.x & 63;
+  const bool second = (int64_t)blockIdx.x >= nb0;
+  const RopeTensor& T = a.t[second ? 1 : 0];
+  const int64_t tile = second ? (int64_t)blockIdx.x - nb0 : (int64_t)blockIdx.x;
+  const int64_t cpp = T.H * 16;  // chunks per position
+  const int64_t C = a.B * a.S * cpp;
+  const int64_t k0 = tile * kTileChunks;
+  float inv = 0.f;
+  if constexpr (!TABLE) inv = a.inv_freq[lane];  // requested before the data: its wait is not the data's
+  __builtin_amdgcn_sched_barrier(0);
+  // Chunks past the tensor's end (last tile only) re-read the last chunk and store nothing.
+  u32x4 v[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t k = k0 + threadIdx.x + kThreads * u;
+    v[u] = ld16_stream(T.x + (k < C ? k : C - 1) * 8);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  const int64_t ps0 = k0 / cpp;
+  auto position = [&](int64_t ps) -> int64_t {
+    const int64_t b = ps / a.S, s = ps - b * a.S;
+    if (a.pos == nullptr) return s;
+    return a.pb == 8 ? static_cast<const int64_t*>(a.pos)[b * a.psb + s * a.pss]
+                     : (int64_t) static_cast<const int32_t*>(a.pos)[b * a.psb + s * a.pss];
+  };
+  if constexpr (!TABLE) {
+    const int64_t klast = (k0 + kTileChunks < C ? k0 + kTileChunks : C) - 1;
+    const int npos = (int)(klast / cpp - ps0 + 1);
+    for (int i = threadIdx.x; i < npos * 64; i += kThreads) {
+      float sn, cn;
+      sincosf((float)position(ps0 + i / 64) * inv, &sn, &cn);
+      cs[i / 64][0][lane] = cn;
+      cs[i / 64][1][lane] = sn;
+    }
+    __syncthreads();
+  }
+  const int c = lane & 15;
+  const int f0 = (kHalf ? (c & 7) : c) * FPU;
+  const bool lo = c < 8;
+  const float sgn = a.conj ? -1.f : 1.f;
+  uint16_t* out = static_cast<uint16_t*>(T.out);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t k = k0 + threadIdx.x + kThreads * u;
+    const int64_t ps = __builtin_amdgcn_readfirstlane((int)((k0 + (threadIdx.x & ~63) + kThreads * u) / cpp - ps0)) + ps0;
+    float cv[FPU], sv[FPU];
+    bool ok = true;
+    if constexpr (TABLE) {
+      // a wave wholly past the end (last tile) reads the last position's id and stores nothing
+      const int64_t p = position(ps < a.B * a.S ? ps : a.B * a.S - 1);
+      ok = p >= 0 && p < a.frows;
+      if (!ok && lane == 0 && a.err) *a.err = 1;
+      const float* frow = a.freqs + 2 * ((ok ? p : 0) * a.frs + f0);
+#pragma unroll
+      for (int q = 0; q < FPU / 2; ++q) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(frow + 4 * q);
+        cv[2 * q] = t[0];
+        sv[2 * q] = t[1];
+        cv[2 * q + 1] = t[2];
+        sv[2 * q + 1] = t[3];
+      }
+    } else {
+      const int slot = (int)(ps - ps0);
+#pragma unroll
+      for (int e = 0; e < FPU; e += 4) {
+        const f32x4 cq = *reinterpret_cast<const f32x4*>(&cs[slot][0][f0 + e]);
+        const f32x4 sq = *reinterpret_cast<const f32x4*>(&cs[slot][1][f0 + e]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          cv[e + j] = cq[j];
+          sv[e + j] = sq[j];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < FPU; ++e) sv[e] = sgn * sv[e];
+    float own[8], o[8];
+    unpack8(v[u], own);
+    if constexpr (kHalf) {
+      u32x4 pv;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pv[i] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v[u][i], 0x128, 0xF, 0xF, false);
+      float par[8];
+      unpack8(pv, par);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float oa, ob;
+        if (lo) {
+          rot(own[e], par[e], cv[e], sv[e], oa, ob);
+          o[e] = oa;
+        } else {
+          rot(par[e], own[e], cv[e], sv[e], oa, ob);
+          o[e] = ob;
+        }
+        if (!ok) o[e] = 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        rot(own[2 * q], own[2 * q + 1], cv[q], sv[q], o[2 * q], o[2 * q + 1]);
+        if (!ok) o[2 * q] = o[2 * q + 1] = 0.f;
+      }
+    }
+    if (k < C) st16_stream(out + k * 8, pack8(o));
+  }
+}
+
+// The tile path applies: D = 128, every tensor contiguous [B, S, H, 128] in
+// and out with H % 4 == 0, bf16 out, 16-byte aligned (and an aligned table
+// with an even row stride in table mode).
+bool tile_ok(const RopeArgs& a, bool table) {
+  static const bool enabled = [] {  // KP_ROPE_TILE=0 (tuning knob): one wave per position instead
+    const char* e = getenv("KP_ROPE_TILE");
+    return e == nullptr || atoi(e) != 0;
+  }();
+  if (!enabled || a.D != kFastD || (!table && !a.have_inv)) return false;
+  if (table && (!aligned16(a.freqs) || (a.frs & 1) != 0)) return false;
+  for (int i = 0; i < a.nt; ++i) {
+    const RopeTensor& t = a.t[i];
+    const int64_t hd = t.H * kFastD;
+    if (t.H <= 0 || (t.H & 3) != 0 || t.out_f32 || !aligned16(t.x) || !aligned16(t.out)) return false;
+    if (t.xs[2] != kFastD || t.xs[1] != hd || t.xs[0] != a.S * hd) return false;
+    if (t.os[2] != kFastD || t.os[1] != hd || t.os[0] != a.S * hd) return false;
+  }
+  return true;
+}
+
 typedef void (*RopeKernel)(RopeArgs);
 
 template <int PAIRING, bool TABLE>
@@ -477,6 +630,21 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
 
   bool vec = tensor_vec_ok(a.t[0], D, pairing) && (a.nt == 1 || tensor_vec_ok(a.t[1], D, pairing));
   const int64_t blocks_needed = ceil_div(npos, kWavesPerBlock);
+  if (vec && tile_ok(a, freqs_cis != nullptr)) {
+    const int64_t nb0 = ceil_div(npos * a.t[0].H * 16, kTileChunks);
+    const int64_t nb1 = a.nt > 1 ? ceil_div(npos * a.t[1].H * 16, kTileChunks) : 0;
+    if (nb0 + nb1 <= INT32_MAX) {
+      const bool tab = freqs_cis != nullptr, half = pairing == KP_ROPE_HALF;
+      const void* fk = half ? (tab ? reinterpret_cast<const void*>(rope_tile<KP_ROPE_HALF, true>)
+                                   : reinterpret_cast<const void*>(rope_tile<KP_ROPE_HALF, false>))
+                            : (tab ? reinterpret_cast<const void*>(rope_tile<KP_ROPE_INTERLEAVED, true>)
+                                   : reinterpret_cast<const void*>(rope_tile<KP_ROPE_INTERLEAVED, false>));
+      int64_t nb = nb0;
+      void* args[] = {&a, &nb};
+      launch_dominant_raw(fk, dim3((unsigned)(nb0 + nb1)), dim3(kThreads), args, 0, as_stream(stream));
+      return check_launch(who);
+    }
+  }
   if (vec) {
     const RopeKernel fk = pick_fast(a, pairing, freqs_cis != nullptr);
     if (fk != nullptr && blocks_needed <= INT32_MAX) {

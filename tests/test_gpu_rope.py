@@ -101,3 +101,50 @@ def test_rope_fp32_output(gpu, vec):
         pair = (2.0**-22 * xc.abs() * f.abs()).unsqueeze(-1).expand(*xc.shape, 2)
         bound = pair.reshape(x.shape)
         assert ((out.cpu().double() - exact).abs() <= bound).all()
+
+
+@pytest.mark.parametrize("pairing", ["half", "interleaved"])
+@pytest.mark.parametrize("table", [False, True])
+@pytest.mark.parametrize("conj", [False, True])
+def test_rope_tile_path_matches_position_path(gpu, oracle_lib, pairing, table, conj):
+    """Contiguous [B, S, H, 128] tensors with H % 4 == 0 take the tile kernel
+    (512-chunk blocks; here both tensors end in a partial tile: 33 * 4 * 16 =
+    2112 and 33 * 8 * 16 = 4224 chunks).  The same data read through a view
+    with a wider head stride takes the one-wave-per-position kernel: both must
+    give identical bits, and meet the oracle's bar."""
+    g = gen(900 + 4 * table + 2 * conj + (pairing == "half"))
+    B, S, Hq, Hk, D, P = 1, 33, 4, 8, 128, 64
+    q = randn_bf16((B, S, Hq, D), g)
+    k = randn_bf16((B, S, Hk, D), g)
+    pos = torch.randint(0, P, (B, S), generator=g) if table else (torch.arange(S) * 97 % 4096).repeat(B, 1)
+    kw = dict(positions=pos.to(gpu), pairing=pairing, conj=conj)
+    freqs = None
+    if table:
+        freqs = torch.complex(torch.randn(P, D // 2, generator=g), torch.randn(P, D // 2, generator=g))
+        kw["freqs_cis"] = freqs.to(gpu)
+    else:
+        kw["theta"] = 500000.0
+    qo, ko = kp.rope(q.to(gpu), k.to(gpu), **kw)
+    # head stride 2 * D: not the tile layout
+    qw = torch.zeros((B, S, Hq, 2 * D), dtype=torch.bfloat16, device=gpu)
+    kw_ = torch.zeros((B, S, Hk, 2 * D), dtype=torch.bfloat16, device=gpu)
+    qw[..., :D] = q.to(gpu)
+    kw_[..., :D] = k.to(gpu)
+    qf, kf = kp.rope(qw[..., :D], kw_[..., :D], **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(qo, qf) and torch.equal(ko, kf)
+    pn = pos.numpy()
+    for x, out in ((q, qo), (k, ko)):
+        if table:
+            exp = oracle_lib.rope(to_u16(x), pn, pairing=pairing, freqs=freqs.numpy(), conj=conj)
+        else:
+            exp = oracle_lib.rope(to_u16(x), pn, pairing=pairing, theta=500000.0, conj=conj)
+        assert_bf16_close(to_u16(out), exp, what="tile", max_ulp=1, min_exact=0.99, ulp_abs_slack=4e-6)
+
+
+def test_rope_tile_path_out_of_table_position(gpu):
+    """An id outside the table in the tile kernel: its rows are zero and the flag is raised."""
+    x = torch.ones((1, 6, 4, 128), dtype=torch.bfloat16, device=gpu)
+    freqs = torch.ones((3, 64), dtype=torch.complex64, device=gpu)
+    with pytest.raises(IndexError):
+        kp.rope(x, positions=torch.tensor([0, 1, 2, 3, 1, 0], device=gpu), freqs_cis=freqs, pairing="interleaved")
