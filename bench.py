@@ -43,9 +43,10 @@ over K steps with HIP events that the library has the runtime stamp at that
 kernel's own start and completion (kp_profile_dominant_kernel ->
 hipExtLaunchKernel), on the stream the kernel runs on.  roofline.ceiling is
 the same measurement for kp_stream_probe -- plain one-shot streaming of the
-workload's byte mix (same number and sizes of arrays read and written,
-16-byte non-temporal accesses, 1 or 4 chunks per thread, the faster of the
-two) -- so kernel_frac_of_ceiling says how close the kernel comes to what
+workload's byte mix (same number and sizes of arrays read and written, random
+bf16 values, 16-byte accesses, 1, 2, 4 or 8 chunks per thread, non-temporal or
+write-through stores, the fastest of the eight) -- so kernel_frac_of_ceiling
+says how close the kernel comes to what
 this GPU streams for those bytes.  The
 cpu_baseline is the torch CPU eager restatement of the
 fragment (oracle/torch_ref.py) on the same seeded inputs.
@@ -806,11 +807,19 @@ def measure_dropin(wl, steps, warmup):
             "host_us_per_call": round(host * 1e6 / steps, 3)}
 
 
+# Probe schedules: chunks per thread x store policy (kp_stream_probe); the
+# fastest for a workload's byte mix is its streaming ceiling.
+PROBE_TILES = (1, 2, 4, 8)
+PROBE_POLICIES = (0, 1)  # KP_STORE_NONTEMPORAL, KP_STORE_WRITE_THROUGH
+PROBE_POLICY_NAMES = {0: "nt", 1: "write-through"}
+
+
 def measure_probe(wl, steps, warmup):
     """The streaming ceiling of the workload's byte mix: kp_stream_probe over
-    fresh arrays of the same sizes (rotated past the Infinity Cache like the
-    workload's own), timed per launch like the dominant kernel, at 1 and at 4
-    chunks per thread; the faster tile size is the ceiling."""
+    fresh arrays of the same sizes holding random bf16 values (rotated past
+    the Infinity Cache like the workload's own), timed per launch like the
+    dominant kernel, under every schedule of PROBE_TILES x PROBE_POLICIES;
+    the fastest is the ceiling."""
     import torch
     from kernelproblems_amd import _lib as L
     if wl.probe_mix is None:
@@ -824,20 +833,23 @@ def measure_probe(wl, steps, warmup):
     for _ in range(R):
         ins = [torch.empty(in_b, dtype=torch.uint8, device=wl.dev) for _ in range(n_in)]
         outs = [torch.empty(out_b, dtype=torch.uint8, device=wl.dev) for _ in range(n_out)]
-        for t in ins:
-            t.fill_(1)
+        for t in ins:  # random bf16 values like the workloads' N(0, 1) data (bit toggling costs HBM time)
+            t.view(torch.bfloat16).normal_()
         sets.append((L.ptr_array([t.data_ptr() for t in ins]), L.ptr_array([t.data_ptr() for t in outs]), ins, outs))
 
-    def launch(i, per_thread):
+    def launch(i, schedule):
+        per_thread, policy = schedule
         ip, op, _, _ = sets[i % R]
-        st = lib.kp_stream_probe(ip, n_in, in_b, op, n_out, out_b, per_thread, stream)
+        st = lib.kp_stream_probe(ip, n_in, in_b, op, n_out, out_b, per_thread, policy, stream)
         if st != 0:
             raise L.KPError("kp_stream_probe", st, lib.kp_last_error_message().decode())
 
     per_tile = {}
-    for per_thread in (1, 4):
+    for per_thread in PROBE_TILES:
+      for policy in PROBE_POLICIES:
+        sched = (per_thread, policy)
         for i in range(warmup):
-            launch(i, per_thread)
+            launch(i, sched)
         starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
         stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
         for e in starts + stops:
@@ -845,16 +857,17 @@ def measure_probe(wl, steps, warmup):
         torch.cuda.synchronize()
         for i in range(steps):
             lib.kp_profile_dominant_kernel(starts[i].cuda_event, stops[i].cuda_event)
-            launch(warmup + i, per_thread)
+            launch(warmup + i, sched)
         lib.kp_profile_dominant_kernel(None, None)
         torch.cuda.synchronize()
-        per_tile[per_thread] = sum(starts[i].elapsed_time(stops[i]) for i in range(steps)) / steps
+        per_tile[sched] = sum(starts[i].elapsed_time(stops[i]) for i in range(steps)) / steps
     del sets
     torch.cuda.empty_cache()
     best = min(per_tile, key=per_tile.get)
     ms = per_tile[best]
     return {"GBps": per_set / (ms * 1e-3) / 1e9, "us": ms * 1e3, "mix": text, "bytes": per_set,
-            "chunks_per_thread": best, "us_by_tile": {str(k): round(v * 1e3, 3) for k, v in per_tile.items()}}
+            "chunks_per_thread": best[0], "stores": PROBE_POLICY_NAMES[best[1]],
+            "us_by_schedule": {f"{k[0]}/{PROBE_POLICY_NAMES[k[1]]}": round(v * 1e3, 3) for k, v in per_tile.items()}}
 
 
 def _tensors(x):
@@ -967,7 +980,8 @@ def _ceiling_json(r):
     if not c:
         return None
     return {"GBps": round(c["GBps"], 1), "frac_of_peak": round(c["GBps"] / PEAK_GBS, 4), "probe_us": round(c["us"], 3),
-            "probe_us_by_chunks_per_thread": c["us_by_tile"], "mix": c["mix"],
+            "probe_schedule": f"{c['chunks_per_thread']} chunk(s) per thread, {c['stores']} stores",
+            "probe_us_by_schedule": c["us_by_schedule"], "mix": c["mix"],
             "kernel_frac_of_ceiling": round(r["achieved"] / c["GBps"], 4)}
 
 

@@ -211,15 +211,20 @@ int kp_embedding_rmsnorm_fwd_bf16(const void* table, int64_t V, int64_t table_ro
 /* ------------------------------------------------------------------------
  * Streaming-ceiling probe (a measurement aid; no counterpart in the
  * reference).  Reads n_in (0..4) arrays of in_bytes each and writes n_out
- * (1..2; or 3 with n_in = 3) arrays of out_bytes each (sizes multiples of 16, arrays 16-byte
- * aligned) with the fragment kernels' access form: 16-byte non-temporal
- * loads and stores, 1 KiB per wave instruction, one-shot grid of 256-thread
- * blocks holding chunks_per_thread (1 or 4) chunks per thread per array.
- * bench.py times it on each workload's byte mix, at both tile sizes, to
- * report the bandwidth plain streaming of those bytes reaches on this GPU.
+ * (1..2; or 3 with n_in = 3) arrays of out_bytes each (sizes multiples of 16
+ * below 4 GiB, arrays 16-byte aligned) with the fragment kernels' access
+ * form: 16-byte non-temporal loads, 1 KiB per wave instruction, one-shot grid
+ * of 256-thread blocks holding chunks_per_thread (1, 2, 4 or 8) chunks per
+ * thread per array, stores non-temporal (KP_STORE_NONTEMPORAL) or
+ * device-scope write-through (KP_STORE_WRITE_THROUGH).  Inputs shorter than
+ * the outputs read as zeros past their end.  bench.py times it on each
+ * workload's byte mix under every tile size and store policy and reports the
+ * fastest as the bandwidth plain streaming of those bytes reaches on this GPU.
  */
+#define KP_STORE_NONTEMPORAL 0
+#define KP_STORE_WRITE_THROUGH 1
 int kp_stream_probe(const void* const* in, int n_in, int64_t in_bytes, void* const* out, int n_out,
-                    int64_t out_bytes, int chunks_per_thread, void* stream);
+                    int64_t out_bytes, int chunks_per_thread, int store_policy, void* stream);
 
 /* ------------------------------------------------------------------------
  * Embedding forward: out[t, :] = table[indices[t], :] (bit copy).

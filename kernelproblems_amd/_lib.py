@@ -27,6 +27,8 @@ KP_DTYPE_F32 = 0
 KP_DTYPE_BF16 = 1
 KP_ROPE_HALF = 0
 KP_ROPE_INTERLEAVED = 1
+KP_STORE_NONTEMPORAL = 0
+KP_STORE_WRITE_THROUGH = 1
 
 _STATUS = {
     KP_EINVAL: "invalid argument",
@@ -98,7 +100,7 @@ SIGNATURES = {
     "kp_rope_c64": (i32, [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64, vp, i64, i64,
                           i32, vp, vp]),
     "kp_unshard_bf16": (i32, [vp, i64, i64, pi64, pi64, pvp, i32, vp]),
-    "kp_stream_probe": (i32, [pvp, i32, i64, pvp, i32, i64, i32, vp]),
+    "kp_stream_probe": (i32, [pvp, i32, i64, pvp, i32, i64, i32, i32, vp]),
     "kp_embedding_rmsnorm_fwd_bf16": (i32, [vp, i64, i64, vp, i32, i64, vp, i64, i64, vp, i64, vp, i64, vp, i64, f32,
                                             vp, vp]),
     "kp_swiglu_fwd_bf16": (i32, [vp, i64, vp, i64, vp, i64, i64, i64, vp]),

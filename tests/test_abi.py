@@ -172,13 +172,17 @@ def test_embedding_rmsnorm_validation(lib):
 
 
 def test_stream_probe_validation(lib):
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 5, 64, L.ptr_array([32]), 1, 64, 4, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, 4, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16, 16]), 2, 64, L.ptr_array([32, 32, 32]), 3, 64, 4, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 60, L.ptr_array([32]), 1, 64, 4, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, 4, None)
-    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 1, 64, 2, None)
-    assert lib.kp_stream_probe(None, 0, 0, L.ptr_array([32]), 1, 0, 1, None) == L.KP_OK  # nothing to stream
+    nt = L.KP_STORE_NONTEMPORAL
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 5, 64, L.ptr_array([32]), 1, 64, 4, nt, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 0, 64, 4, nt, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16, 16]), 2, 64, L.ptr_array([32, 32, 32]), 3, 64, 4, nt, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 60, L.ptr_array([32]), 1, 64, 4, nt, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([24]), 1, 64, L.ptr_array([32]), 1, 64, 4, nt, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 1, 64, 3, nt, None)
+    _expect(lib, L.KP_EINVAL, "kp_stream_probe", L.ptr_array([16]), 1, 64, L.ptr_array([32]), 1, 64, 4, 7, None)
+    _expect(lib, L.KP_EUNSUPPORTED, "kp_stream_probe", L.ptr_array([16]), 1, 1 << 32, L.ptr_array([32]), 1, 64, 1, nt,
+            None)
+    assert lib.kp_stream_probe(None, 0, 0, L.ptr_array([32]), 1, 0, 1, nt, None) == L.KP_OK  # nothing to stream
 
 
 def test_rope_c64_validation(lib):

@@ -7,17 +7,19 @@ from kernelproblems_amd import _lib as L
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("per_thread", [1, 4])
+@pytest.mark.parametrize("per_thread", [1, 2, 4, 8])
+@pytest.mark.parametrize("policy", [L.KP_STORE_NONTEMPORAL, L.KP_STORE_WRITE_THROUGH])
 @pytest.mark.parametrize("n_in,n_out,in_b,out_b", [(2, 1, 1 << 16, 1 << 16), (3, 2, 48, 48), (4, 2, 1 << 15, 1 << 15), (1, 1, 4096, 65536),
                                                    (3, 3, 1 << 16, 1 << 16),
                                                    (0, 2, 0, 20000 * 16)])
-def test_stream_probe_outputs(gpu, n_in, n_out, in_b, out_b, per_thread):
+def test_stream_probe_outputs(gpu, n_in, n_out, in_b, out_b, per_thread, policy):
     g = torch.Generator().manual_seed(n_in * 10 + n_out)
     ins = [torch.randint(0, 1 << 30, (in_b // 4,), generator=g, dtype=torch.int64).to(torch.int32).to(gpu)
            for _ in range(n_in)]
     outs = [torch.full((out_b // 4,), -1, dtype=torch.int32, device=gpu) for _ in range(n_out)]
     L.call("kp_stream_probe", L.ptr_array([t.data_ptr() for t in ins]), n_in, in_b,
-           L.ptr_array([t.data_ptr() for t in outs]), n_out, out_b, per_thread, torch.cuda.current_stream(gpu).cuda_stream)
+           L.ptr_array([t.data_ptr() for t in outs]), n_out, out_b, per_thread, policy,
+           torch.cuda.current_stream(gpu).cuda_stream)
     torch.cuda.synchronize()
     n = out_b // 4
     idx = torch.arange(n, device=gpu)
