@@ -385,7 +385,7 @@ class Rope(Workload):
         nq, nk = B * S * Hq * D, B * S * Hk * D
         self.bytes_per_call = 2 * (nq + nk) * 2 + B * S * 8
         self.dominant_bytes = self.bytes_per_call
-        self.dominant_kernel = "rope_fast"
+        self.dominant_kernel = "rope_tile"
         self.probe_mix = (1, 1, (nq + nk) * 2, (nq + nk) * 2, f"copy of {(nq + nk) * 2 / 1e6:.1f} MB (q and k)")
         self.description = (f"C4 RoPE rotate-half: q [{B},{S},{Hq},{D}], k [{B},{S},{Hk},{D}] bf16, positions "
                             f"[{B},{S}] int64 0..{S - 1}, theta={theta:g}, cos/sin in fp32 in-kernel")
