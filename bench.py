@@ -429,7 +429,7 @@ class RopeComplex(Workload):
         # q and k read and written (8 B per complex), the gathered table row once per position, the id
         self.bytes_per_call = 2 * (nq + nk) * 8 + S * P * 8 + S * 4
         self.dominant_bytes = self.bytes_per_call
-        self.dominant_kernel = "rope_c64_kernel"
+        self.dominant_kernel = "rope_c64_tile"
         self.probe_mix = (1, 1, (nq + nk) * 8, (nq + nk) * 8, f"copy of {(nq + nk) * 8 / 1e6:.1f} MB (q and k)")
         self.description = (f"RoPE on complex64 q [1,{S},{Hq},{P}], k [1,{S},{Hk},{P}] (v1/075cb40f3d5d): times "
                             f"table rows gathered by int32 positions, complex64 out")

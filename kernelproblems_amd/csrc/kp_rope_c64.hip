@@ -114,6 +114,60 @@ __global__ __launch_bounds__(kThreads) void rope_c64_kernel(C64Args a) {
   }
 }
 
+// Tile path: every tensor stored [B, S, H, P] contiguously in and out with
+// H * P / 2 a multiple of 64 (the v1 captures: P = 64, H = 32 and 8).  A
+// block owns 512 consecutive 16-byte chunks of one tensor (thread t: chunks
+// t and t + 256, tensor 0's blocks first) -- the streaming probe's layout,
+// short-lived blocks instead of one wave walking a position's 10 KiB -- and a
+// wave's 64 chunks always lie in one position, whose id and table row are
+// then wave-uniform.  Same arithmetic as rope_c64_kernel, hence the same bits.
+constexpr int kTileChunks = 2 * kThreads;
+
+__global__ __launch_bounds__(kThreads) void rope_c64_tile(C64Args a, int64_t nb0) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const bool second = (int64_t)blockIdx.x >= nb0;
+  const C64Tensor& T = a.t[second ? 1 : 0];
+  const int64_t tile = second ? (int64_t)blockIdx.x - nb0 : (int64_t)blockIdx.x;
+  const int64_t cph = a.P / 2;       // chunks per head
+  const int64_t cpp = T.H * cph;     // chunks per position
+  const int64_t C = a.B * a.S * cpp;
+  const int64_t k0 = tile * kTileChunks;
+  // chunks past the tensor's end (last tile only) re-read the last chunk and store nothing
+  f32x4 v[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t k = k0 + threadIdx.x + kThreads * u;
+    v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(T.x) + (k < C ? k : C - 1));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int64_t k = k0 + threadIdx.x + kThreads * u;
+    const int64_t kw = k0 + (threadIdx.x & ~(kWave - 1)) + kThreads * u;  // the wave's first chunk
+    int64_t ps = kw / cpp;
+    ps = uniform64(ps < a.B * a.S ? ps : a.B * a.S - 1);
+    const int64_t b = ps / a.S, s = ps - b * a.S;
+    int64_t p = s;
+    if (a.pos) p = a.pb == 8 ? static_cast<const int64_t*>(a.pos)[b * a.psb + s * a.pss]
+                             : (int64_t) static_cast<const int32_t*>(a.pos)[b * a.psb + s * a.pss];
+    const bool ok = p >= 0 && p < a.frows;
+    if (!ok && lane == 0 && a.err) a.err[0] = 1;
+    const int64_t c = (k - kw + kw % cph) % cph;  // chunk within its head
+    const f32x4 t = *reinterpret_cast<const f32x4*>(a.freqs + 2 * (ok ? p : 0) * a.frs + 4 * c);
+    float o[4];
+    cmul(v[u][0], v[u][1], t[0], a.sgn * t[1], o[0], o[1]);
+    cmul(v[u][2], v[u][3], t[2], a.sgn * t[3], o[2], o[3]);
+    const f32x4 r = ok ? f32x4{o[0], o[1], o[2], o[3]} : f32x4{0.f, 0.f, 0.f, 0.f};
+    if (k < C) st16f_stream(reinterpret_cast<f32x4*>(T.out) + k, r);
+  }
+}
+
+bool tile_view(const C64Tensor& t, int64_t S, int64_t P) {
+  const int64_t hp = t.H * P;
+  return t.H > 0 && (hp / 2) % kWave == 0 && t.xs[2] == P && t.xs[1] == hp && t.xs[0] == S * hp && t.os[2] == P &&
+         t.os[1] == hp && t.os[0] == S * hp;
+}
+
 bool aligned_view(const void* p, const int64_t* st, int64_t P) {
   // 16-byte chunks: base aligned, every stride and P a whole number of 2 complex values
   return aligned16(p) && (P % 2 == 0) && st[0] % 2 == 0 && st[1] % 2 == 0 && st[2] % 2 == 0;
@@ -170,6 +224,19 @@ int kp_rope_c64(const void* x0, void* out0, int64_t H0, const int64_t* x0_stride
   bool vec = aligned_view(freqs_cis, fst, P);
   for (int i = 0; i < a.nt; ++i)
     vec = vec && aligned_view(a.t[i].x, a.t[i].xs, P) && aligned_view(a.t[i].out, a.t[i].os, P);
+  bool tile = vec;
+  for (int i = 0; i < a.nt; ++i) tile = tile && tile_view(a.t[i], S, P);
+  if (tile) {
+    const int64_t nb0 = ceil_div(npos * a.t[0].H * (P / 2), kTileChunks);
+    const int64_t nb1 = a.nt > 1 ? ceil_div(npos * a.t[1].H * (P / 2), kTileChunks) : 0;
+    if (nb0 + nb1 <= 0x7fffffffLL) {
+      int64_t nb = nb0;
+      void* targs[] = {&a, &nb};
+      launch_dominant_raw(reinterpret_cast<const void*>(rope_c64_tile), dim3((unsigned)(nb0 + nb1)), dim3(kThreads),
+                          targs, 0, as_stream(stream));
+      return check_launch(who);
+    }
+  }
   const int64_t blocks_needed = ceil_div(npos, kWavesPerBlock);
   const int64_t cap = (int64_t)cu_count() * 16;
   const unsigned grid = (unsigned)(blocks_needed < cap ? blocks_needed : cap);

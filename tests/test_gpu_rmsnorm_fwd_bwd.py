@@ -27,7 +27,7 @@ CASES = [
     (64, 4096, 2, 2, True),    # v6/408ac0979ac5
     (64, 4096, 1, 2, True),    # v6/e9198b707240
     (33, 4096, 1, 1, False),   # plain norm, ragged row count
-    (17, 8192, 1, 3, True),    # 4 waves per row
+    (17, 8192, 1, 3, True),    # 8 waves per row, 8-wave blocks
     (40, 512, 1, 1, True),     # 1 chunk per lane
     (9, 5120, 3, 1, False),    # no fused kernel for 3 x terms: forward then backward
     (7, 1000, 1, 2, True),     # generic shape: forward then backward

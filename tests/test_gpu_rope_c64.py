@@ -88,3 +88,54 @@ def test_full_shape_against_torch(gpu):
     for o, ref in ((qo, q * rows), (ko, k * rows)):
         d = torch.view_as_real(o) - torch.view_as_real(ref)
         assert float(d.abs().max()) <= 1e-5 * float(torch.view_as_real(ref).abs().max())
+
+
+@pytest.mark.parametrize("gather", [False, True])
+@pytest.mark.parametrize("conj", [False, True])
+def test_tile_path_matches_position_path(gpu, gather, conj):
+    """Contiguous tensors with H * P / 2 a multiple of 64 take the tile
+    kernel (here 2 * 37 * 128 and 2 * 37 * 64 chunks: both end in a partial
+    512-chunk tile); the same values read through a head-strided view take
+    the one-wave-per-position kernel.  Identical bits, and the oracle's bound."""
+    print(f"[rope c64 tile] gather={gather} conj={conj}", flush=True)
+    g = torch.Generator().manual_seed(11)
+    B, S, Hq, Hk, P, rows = 2, 37, 4, 2, 64, 50
+    q, k = _c64((B, S, Hq, P), g).to(gpu), _c64((B, S, Hk, P), g).to(gpu)
+    table = _c64((rows, P), g).to(gpu)
+    pos = (torch.randint(0, rows, (B, S), generator=g) if gather else None)
+    kw = dict(freqs_cis=table, positions=None if pos is None else pos.to(gpu), conj=conj)
+    qo, ko = kp.rope_complex(q, k, **kw)
+    qw = torch.zeros((B, S, Hq + 1, P), dtype=torch.complex64, device=gpu)
+    kw_ = torch.zeros((B, S, Hk + 1, P), dtype=torch.complex64, device=gpu)
+    qw[:, :, :Hq] = q
+    kw_[:, :, :Hk] = k
+    qf, kf = kp.rope_complex(qw[:, :, :Hq], kw_[:, :, :Hk], **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(qo.view(torch.float32), qf.view(torch.float32))
+    assert torch.equal(ko.view(torch.float32), kf.view(torch.float32))
+    tn = table.cpu().numpy()
+    pn = None if pos is None else pos.numpy()
+    for x, o in ((q, qo), (k, ko)):
+        xn = x.cpu().numpy()
+        exact = oracle.rope_c64(xn, tn, pn, conj=conj)
+        p_ = np.broadcast_to(np.arange(S), (B, S)) if pn is None else pn
+        rows_ = tn[p_][:, :, None, :]
+        _check(o, exact, xn.astype(np.complex128), (np.conj(rows_) if conj else rows_).astype(np.complex128))
+
+
+def test_tile_path_out_of_range_positions(gpu):
+    """The tile kernel (H * P / 2 = 64) on ids outside the table: flagged,
+    their rows zero, the others right."""
+    q = torch.randn(1, 4, 2, 64, dtype=torch.complex64, device=gpu)
+    t = torch.randn(3, 64, dtype=torch.complex64, device=gpu)
+    pos = torch.tensor([[0, 3, 1, -1]], device=gpu)
+    with pytest.raises(IndexError):
+        kp.rope_complex(q, freqs_cis=t, positions=pos)
+    kp.set_index_checking(False)
+    try:
+        qo, _ = kp.rope_complex(q, freqs_cis=t, positions=pos)
+    finally:
+        kp.set_index_checking(True)
+    assert not qo[0, 1].any() and not qo[0, 3].any()
+    exact = oracle.rope_c64(q[:, [0, 2]].cpu().numpy(), t.cpu().numpy(), np.array([[0, 1]]))
+    assert np.allclose(qo[:, [0, 2]].cpu().numpy(), exact, rtol=1e-6, atol=1e-6)
