@@ -7,7 +7,10 @@ The default run measures every BASELINE configuration (c1, c2, c3f, c3b, c4,
 c5f, c5b) and prints one JSON line: the headline workload (c2, configs[1])
 in the top-level fields and one block per configuration under "configs",
 each with its whole-call rate, roofline (dominant kernel), traffic, CPU
-baseline and the tensor-level drop-in's time per call.
+baseline and the tensor-level drop-in's time per call.  When --steps is
+below 100, each block also carries a "steady" pass of 100 calls: the timed
+loop's fixed cost (first launch, closing synchronisation; ~20 us) spread over
+few steps inflates the per-call time of the small configurations.
 
 A step is one call of the fragment (one pass of the hot path over one batch
 of synthetic input, already resident in HBM).  Workloads are the
@@ -65,6 +68,7 @@ ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
 PEAK_GBS = 8000.0  # MI355X HBM3E
+STEADY_STEPS = 100  # calls in the steady-state pass reported beside a shorter timed loop
 MIN_ROTATION_BYTES = 1 << 30
 
 
@@ -1034,6 +1038,14 @@ def main():
         r = measure_gpu(wl, args.steps, args.warmup)
         print(f"[bench] {name}: {r['ms_per_step'] * 1e3:.1f} us/call, {r['value']:.0f} GB/s, dominant kernel "
               f"{r['dominant_ms'] * 1e3:.1f} us -> {r['achieved']:.0f} GB/s", file=sys.stderr, flush=True)
+        # With few steps the timed loop's fixed cost (the first launch's latency and the closing
+        # synchronisation, ~20 us) is spread over few calls; a second, longer pass gives the
+        # steady per-call time beside it.
+        r["steady"] = None
+        if args.steps < STEADY_STEPS:
+            st = measure_gpu(wl, STEADY_STEPS, args.warmup)
+            r["steady"] = {"steps": STEADY_STEPS, "us_per_call": round(st["ms_per_step"] * 1e3, 3),
+                           "GBps": round(st["value"], 1), "kernel_us": round(st["dominant_ms"] * 1e3, 3)}
         r["dropin"] = None if args.no_dropin else measure_dropin(wl, args.steps, args.warmup)
         if r["dropin"]:
             d = r["dropin"]
@@ -1078,6 +1090,7 @@ def main():
             "pct_of_peak": round(100 * r["value"] / PEAK_GBS, 2),
             "bytes_per_call": wl.bytes_per_call,
             "roofline": roofline(name, wl, r),
+            "steady": r["steady"],
             "dropin": r["dropin"],
             "cpu_baseline": cpu,
         }
