@@ -997,6 +997,67 @@ def load_traffic(name):
         return None
 
 
+def measure_probe_sizes(dev, steps, warmup):
+    """Streaming time against size: kp_stream_probe (the fastest of its eight
+    schedules) for a copy, 2 reads + 1 write and 2 reads + 2 writes of 4 MiB
+    to 256 MiB arrays of random bf16 values, rotated past the Infinity Cache,
+    timed as K back-to-back launches; a least-squares fit of
+    t = fixed + bytes / rate over the sizes from 16 MiB says how much of a
+    small launch is ramp and drain rather than bandwidth."""
+    import torch
+    from kernelproblems_amd import _lib as L
+    lib = L.lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+    def best(n_in, n_out, nbytes):
+        R = max(2, math.ceil(MIN_ROTATION_BYTES / ((n_in + n_out) * nbytes)))
+        sets = []
+        for _ in range(R):
+            ins = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n_in)]
+            outs = [torch.empty(nbytes, dtype=torch.uint8, device=dev) for _ in range(n_out)]
+            for t in ins:
+                t.view(torch.bfloat16).normal_()
+            sets.append((L.ptr_array([t.data_ptr() for t in ins]), L.ptr_array([t.data_ptr() for t in outs]), ins, outs))
+        times = {}
+        for per_thread in PROBE_TILES:
+            for policy in PROBE_POLICIES:
+                def launch(i):
+                    ip, op, _, _ = sets[i % R]
+                    st = lib.kp_stream_probe(ip, n_in, nbytes, op, n_out, nbytes, per_thread, policy, stream)
+                    if st != 0:
+                        raise L.KPError("kp_stream_probe", st, lib.kp_last_error_message().decode())
+                for i in range(warmup):
+                    launch(i)
+                torch.cuda.synchronize()
+                e0.record()
+                for i in range(steps):
+                    launch(i)
+                e1.record()
+                torch.cuda.synchronize()
+                times[(per_thread, policy)] = e0.elapsed_time(e1) * 1e3 / steps
+        del sets
+        torch.cuda.empty_cache()
+        k = min(times, key=times.get)
+        return times[k], k
+
+    out = {}
+    for n_in, n_out, name in ((1, 1, "copy"), (2, 1, "2 reads + 1 write"), (2, 2, "2 reads + 2 writes")):
+        pts = []
+        for mib in (4, 8, 16, 32, 64, 128, 256):
+            us, k = best(n_in, n_out, mib << 20)
+            total = (n_in + n_out) * (mib << 20)
+            pts.append({"MiB_per_array": mib, "bytes": total, "us": round(us, 3), "GBps": round(total / us / 1e3, 1),
+                        "schedule": f"{k[0]}/{PROBE_POLICY_NAMES[k[1]]}"})
+            print(f"[bench] probe {name}, {mib} MiB per array: {us:.2f} us", file=sys.stderr, flush=True)
+        xs = [p["bytes"] for p in pts if p["MiB_per_array"] >= 16]
+        ys = [p["us"] for p in pts if p["MiB_per_array"] >= 16]
+        mx, my = sum(xs) / len(xs), sum(ys) / len(ys)
+        slope = sum((x - mx) * (y - my) for x, y in zip(xs, ys)) / sum((x - mx) ** 2 for x in xs)
+        out[name] = {"points": pts, "fit_fixed_us": round(my - slope * mx, 3), "fit_GBps": round(1e-3 / slope, 1)}
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -1013,6 +1074,8 @@ def main():
     ap.add_argument("--no-probe", action="store_true", help="skip the streaming-ceiling probe")
     ap.add_argument("--no-dropin", action="store_true", help="skip timing the tensor-level drop-ins")
     ap.add_argument("--cpu-seconds", type=float, default=3.0, help="CPU baseline budget per configuration")
+    ap.add_argument("--probe-sizes", action="store_true",
+                    help="instead of the workloads: streaming time against array size (fixed cost + rate fit)")
     ap.add_argument("--copy-calibration-mib", type=int, default=0,
                     help="after the workload, run 5 plain device copies of this many MiB (a known-size "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -1031,6 +1094,9 @@ def main():
         return 1
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.probe_sizes:
+        print(json.dumps({"probe_sizes": measure_probe_sizes(dev, args.steps, args.warmup)}), flush=True)
+        return 0
 
     def run(name, with_cpu):
         print(f"[bench] preparing {name}", file=sys.stderr, flush=True)
