@@ -73,9 +73,13 @@ __device__ __forceinline__ void store1(const RopeTensor& T, int64_t o, float v) 
   else static_cast<uint16_t*>(T.out)[o] = f_to_bf(v);
 }
 
+// (a, b) rotated by the angle with cosine c and sine s.  The contraction is
+// spelled out -- one rounded product, then one fma -- so that every kernel of
+// this file (compiled separately, each free to contract a * c - b * s its
+// own way) produces the same bits for the same operands.
 __device__ __forceinline__ void rot(float a, float b, float c, float s, float& oa, float& ob) {
-  oa = a * c - b * s;
-  ob = b * c + a * s;
+  oa = __builtin_fmaf(a, c, -(b * s));
+  ob = __builtin_fmaf(b, c, a * s);
 }
 
 // TABLE is a template parameter so that each instantiation reads its angles
@@ -376,56 +380,84 @@ __global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
 // t chunks t and t + 256, tensor 0's blocks first -- the short-lived,
 // fine-grained streaming layout that measured fastest on MI355X (c4: 56 us
 // against 58.5 us for rope_fast, bit-identical).  A head is 16 chunks, so a
-// lane's chunk index c = lane % 16 is fixed; a wave's 64 chunks are 4 heads
-// of one position (H % 4 == 0).  Rotate-half pairs chunk c with c ^ 8, i.e.
-// lane l with lane l ^ 8 of the same 16-lane DPP row (row_ror:8);
-// interleaved pairs are the 4 (2i, 2i+1) pairs inside a chunk.  Theta mode
-// evaluates the (cos, sin) of the tile's positions once per block (threads
-// f, f + 64, ... of position slot i / 64) into LDS behind one barrier; table
-// mode reads the position's row of the table (L2-resident).  Arithmetic,
-// rounding and angles are those of rope_fast, so both give identical bits.
+// lane's chunk index c = lane % 16 is fixed; a wave's 64 chunks are a group
+// of 4 heads of one position (H % 4 == 0), so a block is 8 groups and wave w
+// takes groups 8 tile + w and 8 tile + w + 4.  Every index is 32-bit (the
+// host keeps each tensor below 2^31 chunks) and wave-uniform, the group's
+// position being a multiply-high division by the groups per position, so
+// the per-chunk work is the rotation alone.  Rotate-half pairs chunk c with
+// c ^ 8, i.e. lane l with lane l ^ 8 of the same 16-lane DPP row
+// (row_ror:8); interleaved pairs are the 4 (2i, 2i+1) pairs inside a chunk.
+// Theta mode evaluates the (cos, sin) of the tile's (at most 8) positions
+// once per block (threads f, f + 64, ... of position slot i / 64) into LDS
+// behind one barrier; table mode reads the position's row of the table
+// (L2-resident).  Arithmetic, rounding and angles are those of rope_fast, so
+// both give identical bits.
 constexpr int kTileChunks = 2 * kThreads;
-constexpr int kTileMaxPos = kTileChunks / 64 + 1;  // H >= 4: a position is >= 64 chunks
+constexpr int kTileGroups = kTileChunks / 64;  // 8
+constexpr int kTileMaxPos = kTileGroups;       // a position is >= 1 group
+
+struct TileTensor {
+  const uint16_t* x;
+  uint16_t* out;
+  uint32_t groups;  // B * S * H / 4
+  Div32 gpp;        // groups per position, H / 4
+};
+struct TileArgs {
+  TileTensor t[2];
+  uint32_t nb0;  // blocks of tensor 0
+  uint32_t npos;  // B * S
+  Div32 S;
+  const void* pos;
+  int pb;
+  int64_t psb, pss;
+  const float* freqs;
+  int64_t frows, frs;
+  int conj;
+  int32_t* err;
+  float inv_freq[64];
+};
+
+// Position id of flattened position ps = b S + s (ps < 2^31).
+__device__ __forceinline__ int64_t tile_position(const TileArgs& a, uint32_t ps) {
+  const uint32_t b = div32(ps, a.S), s = ps - b * a.S.d;
+  if (a.pos == nullptr) return s;
+  const int64_t i = (int64_t)b * a.psb + (int64_t)s * a.pss;
+  return a.pb == 8 ? static_cast<const int64_t*>(a.pos)[i] : (int64_t) static_cast<const int32_t*>(a.pos)[i];
+}
 
 template <int PAIRING, bool TABLE>
-__global__ __launch_bounds__(kThreads) void rope_tile(RopeArgs a, int64_t nb0) {
+__global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
   constexpr bool kHalf = PAIRING == KP_ROPE_HALF;
   constexpr int FPU = kHalf ? 8 : 4;  // angles per chunk
   __shared__ float cs[TABLE ? 1 : kTileMaxPos][2][64];
   const int lane = threadIdx.x & 63;
-  const bool second = (int64_t)blockIdx.x >= nb0;
-  const RopeTensor& T = a.t[second ? 1 : 0];
-  const int64_t tile = second ? (int64_t)blockIdx.x - nb0 : (int64_t)blockIdx.x;
-  const int64_t cpp = T.H * 16;  // chunks per position
-  const int64_t C = a.B * a.S * cpp;
-  const int64_t k0 = tile * kTileChunks;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const bool second = blockIdx.x >= a.nb0;
+  const TileTensor& T = a.t[second ? 1 : 0];
+  const uint32_t g0 = (second ? blockIdx.x - a.nb0 : blockIdx.x) * kTileGroups;
+  const uint32_t glast = T.groups - 1;
   float inv = 0.f;
   if constexpr (!TABLE) inv = a.inv_freq[lane];  // requested before the data: its wait is not the data's
   __builtin_amdgcn_sched_barrier(0);
-  // Chunks past the tensor's end (last tile only) re-read the last chunk and store nothing.
+  // Groups past the tensor's end (last tile only) re-read the last group and store nothing.
   u32x4 v[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int64_t k = k0 + threadIdx.x + kThreads * u;
-    v[u] = ld16_stream(T.x + (k < C ? k : C - 1) * 8);
+    const uint32_t g = g0 + wave + 4 * u;
+    v[u] = ld16_stream(T.x + ((size_t)(g < glast ? g : glast) * 64 + lane) * 8);
   }
   __builtin_amdgcn_sched_barrier(0);
 
-  const int64_t ps0 = k0 / cpp;
-  auto position = [&](int64_t ps) -> int64_t {
-    const int64_t b = ps / a.S, s = ps - b * a.S;
-    if (a.pos == nullptr) return s;
-    return a.pb == 8 ? static_cast<const int64_t*>(a.pos)[b * a.psb + s * a.pss]
-                     : (int64_t) static_cast<const int32_t*>(a.pos)[b * a.psb + s * a.pss];
-  };
+  const uint32_t ps0 = div32(g0, T.gpp);
   if constexpr (!TABLE) {
-    const int64_t klast = (k0 + kTileChunks < C ? k0 + kTileChunks : C) - 1;
-    const int npos = (int)(klast / cpp - ps0 + 1);
+    const uint32_t gl = g0 + kTileGroups - 1 < glast ? g0 + kTileGroups - 1 : glast;
+    const int npos = (int)(div32(gl, T.gpp) - ps0) + 1;
     for (int i = threadIdx.x; i < npos * 64; i += kThreads) {
       float sn, cn;
-      sincosf((float)position(ps0 + i / 64) * inv, &sn, &cn);
-      cs[i / 64][0][lane] = cn;
-      cs[i / 64][1][lane] = sn;
+      sincosf((float)tile_position(a, ps0 + (uint32_t)(i >> 6)) * inv, &sn, &cn);
+      cs[i >> 6][0][lane] = cn;
+      cs[i >> 6][1][lane] = sn;
     }
     __syncthreads();
   }
@@ -433,16 +465,14 @@ __global__ __launch_bounds__(kThreads) void rope_tile(RopeArgs a, int64_t nb0) {
   const int f0 = (kHalf ? (c & 7) : c) * FPU;
   const bool lo = c < 8;
   const float sgn = a.conj ? -1.f : 1.f;
-  uint16_t* out = static_cast<uint16_t*>(T.out);
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int64_t k = k0 + threadIdx.x + kThreads * u;
-    const int64_t ps = __builtin_amdgcn_readfirstlane((int)((k0 + (threadIdx.x & ~63) + kThreads * u) / cpp - ps0)) + ps0;
+    const uint32_t g = g0 + wave + 4 * u;
+    const uint32_t ps = div32(g < glast ? g : glast, T.gpp);
     float cv[FPU], sv[FPU];
     bool ok = true;
     if constexpr (TABLE) {
-      // a wave wholly past the end (last tile) reads the last position's id and stores nothing
-      const int64_t p = position(ps < a.B * a.S ? ps : a.B * a.S - 1);
+      const int64_t p = tile_position(a, ps);
       ok = p >= 0 && p < a.frows;
       if (!ok && lane == 0 && a.err) *a.err = 1;
       const float* frow = a.freqs + 2 * ((ok ? p : 0) * a.frs + f0);
@@ -496,7 +526,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(RopeArgs a, int64_t nb0) {
         if (!ok) o[2 * q] = o[2 * q + 1] = 0.f;
       }
     }
-    if (k < C) st16_stream(out + k * 8, pack8(o));
+    if (g <= glast) st16_stream(T.out + ((size_t)g * 64 + lane) * 8, pack8(o));
   }
 }
 
@@ -510,10 +540,13 @@ bool tile_ok(const RopeArgs& a, bool table) {
   }();
   if (!enabled || a.D != kFastD || (!table && !a.have_inv)) return false;
   if (table && (!aligned16(a.freqs) || (a.frs & 1) != 0)) return false;
+  const int64_t npos = a.B * a.S;
+  if (npos <= 0 || npos > INT32_MAX) return false;
   for (int i = 0; i < a.nt; ++i) {
     const RopeTensor& t = a.t[i];
     const int64_t hd = t.H * kFastD;
     if (t.H <= 0 || (t.H & 3) != 0 || t.out_f32 || !aligned16(t.x) || !aligned16(t.out)) return false;
+    if (t.H > INT32_MAX / 16 || npos * t.H * 16 > INT32_MAX) return false;  // 32-bit chunk indices
     if (t.xs[2] != kFastD || t.xs[1] != hd || t.xs[0] != a.S * hd) return false;
     if (t.os[2] != kFastD || t.os[1] != hd || t.os[0] != a.S * hd) return false;
   }
@@ -631,19 +664,32 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
   bool vec = tensor_vec_ok(a.t[0], D, pairing) && (a.nt == 1 || tensor_vec_ok(a.t[1], D, pairing));
   const int64_t blocks_needed = ceil_div(npos, kWavesPerBlock);
   if (vec && tile_ok(a, freqs_cis != nullptr)) {
-    const int64_t nb0 = ceil_div(npos * a.t[0].H * 16, kTileChunks);
-    const int64_t nb1 = a.nt > 1 ? ceil_div(npos * a.t[1].H * 16, kTileChunks) : 0;
-    if (nb0 + nb1 <= INT32_MAX) {
-      const bool tab = freqs_cis != nullptr, half = pairing == KP_ROPE_HALF;
-      const void* fk = half ? (tab ? reinterpret_cast<const void*>(rope_tile<KP_ROPE_HALF, true>)
-                                   : reinterpret_cast<const void*>(rope_tile<KP_ROPE_HALF, false>))
-                            : (tab ? reinterpret_cast<const void*>(rope_tile<KP_ROPE_INTERLEAVED, true>)
-                                   : reinterpret_cast<const void*>(rope_tile<KP_ROPE_INTERLEAVED, false>));
-      int64_t nb = nb0;
-      void* args[] = {&a, &nb};
-      launch_dominant_raw(fk, dim3((unsigned)(nb0 + nb1)), dim3(kThreads), args, 0, as_stream(stream));
-      return check_launch(who);
-    }
+    TileArgs ta{};
+    for (int i = 0; i < a.nt; ++i)
+      ta.t[i] = TileTensor{a.t[i].x, static_cast<uint16_t*>(a.t[i].out), (uint32_t)(npos * (a.t[i].H / 4)),
+                           make_div32((uint32_t)(a.t[i].H / 4))};
+    ta.nb0 = (uint32_t)ceil_div(ta.t[0].groups, kTileGroups);
+    const int64_t nb1 = a.nt > 1 ? ceil_div(ta.t[1].groups, kTileGroups) : 0;
+    ta.npos = (uint32_t)npos;
+    ta.S = make_div32((uint32_t)S);
+    ta.pos = a.pos;
+    ta.pb = a.pb;
+    ta.psb = a.psb;
+    ta.pss = a.pss;
+    ta.freqs = a.freqs;
+    ta.frows = a.frows;
+    ta.frs = a.frs;
+    ta.conj = a.conj;
+    ta.err = a.err;
+    for (int f = 0; f < 64; ++f) ta.inv_freq[f] = a.inv_freq[f];
+    const bool tab = freqs_cis != nullptr, half = pairing == KP_ROPE_HALF;
+    const void* fk = half ? (tab ? reinterpret_cast<const void*>(rope_tile<KP_ROPE_HALF, true>)
+                                 : reinterpret_cast<const void*>(rope_tile<KP_ROPE_HALF, false>))
+                          : (tab ? reinterpret_cast<const void*>(rope_tile<KP_ROPE_INTERLEAVED, true>)
+                                 : reinterpret_cast<const void*>(rope_tile<KP_ROPE_INTERLEAVED, false>));
+    void* args[] = {&ta};
+    launch_dominant_raw(fk, dim3((unsigned)(ta.nb0 + nb1)), dim3(kThreads), args, 0, as_stream(stream));
+    return check_launch(who);
   }
   if (vec) {
     const RopeKernel fk = pick_fast(a, pairing, freqs_cis != nullptr);

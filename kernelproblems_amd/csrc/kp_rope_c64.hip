@@ -45,9 +45,12 @@ struct C64Args {
   int32_t* err;
 };
 
+// (a + bi)(c + di) in fp32 with the contraction spelled out (one rounded
+// product, then one fma per component), so the tile and per-position kernels
+// give the same bits whatever the compiler would fuse in each.
 __device__ __forceinline__ void cmul(float a, float b, float c, float d, float& re, float& im) {
-  re = a * c - b * d;
-  im = a * d + b * c;
+  re = __builtin_fmaf(a, c, -(b * d));
+  im = __builtin_fmaf(a, d, b * c);
 }
 
 template <bool VEC>
@@ -119,46 +122,70 @@ __global__ __launch_bounds__(kThreads) void rope_c64_kernel(C64Args a) {
 // block owns 512 consecutive 16-byte chunks of one tensor (thread t: chunks
 // t and t + 256, tensor 0's blocks first) -- the streaming probe's layout,
 // short-lived blocks instead of one wave walking a position's 10 KiB -- and a
-// wave's 64 chunks always lie in one position, whose id and table row are
-// then wave-uniform.  Same arithmetic as rope_c64_kernel, hence the same bits.
+// wave's 64 chunks (a group) always lie in one position, whose id and table
+// row are then wave-uniform: wave w takes groups 8 tile + w and 8 tile + w + 4.
+// Indices are 32-bit (each tensor below 2^31 chunks, checked on the host);
+// the group's position and a chunk's place in its head are multiply-high
+// divisions by launch-fixed divisors.  Same arithmetic as rope_c64_kernel,
+// hence the same bits.
 constexpr int kTileChunks = 2 * kThreads;
+constexpr int kTileGroups = kTileChunks / kWave;  // 8
 
-__global__ __launch_bounds__(kThreads) void rope_c64_tile(C64Args a, int64_t nb0) {
+struct C64TileTensor {
+  const float* x;
+  float* out;
+  uint32_t groups;  // B * S * H * P / 128
+  Div32 gpp;        // groups per position, H * P / 128
+};
+struct C64TileArgs {
+  C64TileTensor t[2];
+  uint32_t nb0;  // blocks of tensor 0
+  Div32 S;
+  Div32 cph;     // chunks per head, P / 2
+  const void* pos;
+  int pb;
+  int64_t psb, pss;
+  const float* freqs;
+  int64_t frows, frs;
+  float sgn;
+  int32_t* err;
+};
+
+__global__ __launch_bounds__(kThreads) void rope_c64_tile(C64TileArgs a) {
   const int lane = threadIdx.x & (kWave - 1);
-  const bool second = (int64_t)blockIdx.x >= nb0;
-  const C64Tensor& T = a.t[second ? 1 : 0];
-  const int64_t tile = second ? (int64_t)blockIdx.x - nb0 : (int64_t)blockIdx.x;
-  const int64_t cph = a.P / 2;       // chunks per head
-  const int64_t cpp = T.H * cph;     // chunks per position
-  const int64_t C = a.B * a.S * cpp;
-  const int64_t k0 = tile * kTileChunks;
-  // chunks past the tensor's end (last tile only) re-read the last chunk and store nothing
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const bool second = blockIdx.x >= a.nb0;
+  const C64TileTensor& T = a.t[second ? 1 : 0];
+  const uint32_t g0 = (second ? blockIdx.x - a.nb0 : blockIdx.x) * kTileGroups;
+  const uint32_t glast = T.groups - 1;
+  // groups past the tensor's end (last tile only) re-read the last group and store nothing
   f32x4 v[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int64_t k = k0 + threadIdx.x + kThreads * u;
-    v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(T.x) + (k < C ? k : C - 1));
+    const uint32_t g = g0 + wave + 4 * u;
+    v[u] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(T.x) + (size_t)(g < glast ? g : glast) * kWave + lane);
   }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    const int64_t k = k0 + threadIdx.x + kThreads * u;
-    const int64_t kw = k0 + (threadIdx.x & ~(kWave - 1)) + kThreads * u;  // the wave's first chunk
-    int64_t ps = kw / cpp;
-    ps = uniform64(ps < a.B * a.S ? ps : a.B * a.S - 1);
-    const int64_t b = ps / a.S, s = ps - b * a.S;
+    const uint32_t g = g0 + wave + 4 * u, gc = g < glast ? g : glast;
+    const uint32_t ps = div32(gc, T.gpp);
+    const uint32_t b = div32(ps, a.S), s = ps - b * a.S.d;
     int64_t p = s;
-    if (a.pos) p = a.pb == 8 ? static_cast<const int64_t*>(a.pos)[b * a.psb + s * a.pss]
-                             : (int64_t) static_cast<const int32_t*>(a.pos)[b * a.psb + s * a.pss];
+    if (a.pos) {
+      const int64_t i = (int64_t)b * a.psb + (int64_t)s * a.pss;
+      p = a.pb == 8 ? static_cast<const int64_t*>(a.pos)[i] : (int64_t) static_cast<const int32_t*>(a.pos)[i];
+    }
     const bool ok = p >= 0 && p < a.frows;
     if (!ok && lane == 0 && a.err) a.err[0] = 1;
-    const int64_t c = (k - kw + kw % cph) % cph;  // chunk within its head
+    const uint32_t x = (gc - ps * T.gpp.d) * kWave + lane;  // chunk within its position
+    const uint32_t c = x - div32(x, a.cph) * a.cph.d;       // chunk within its head
     const f32x4 t = *reinterpret_cast<const f32x4*>(a.freqs + 2 * (ok ? p : 0) * a.frs + 4 * c);
     float o[4];
     cmul(v[u][0], v[u][1], t[0], a.sgn * t[1], o[0], o[1]);
     cmul(v[u][2], v[u][3], t[2], a.sgn * t[3], o[2], o[3]);
     const f32x4 r = ok ? f32x4{o[0], o[1], o[2], o[3]} : f32x4{0.f, 0.f, 0.f, 0.f};
-    if (k < C) st16f_stream(reinterpret_cast<f32x4*>(T.out) + k, r);
+    if (g <= glast) st16f_stream(reinterpret_cast<f32x4*>(T.out) + (size_t)g * kWave + lane, r);
   }
 }
 
@@ -226,13 +253,30 @@ int kp_rope_c64(const void* x0, void* out0, int64_t H0, const int64_t* x0_stride
     vec = vec && aligned_view(a.t[i].x, a.t[i].xs, P) && aligned_view(a.t[i].out, a.t[i].os, P);
   bool tile = vec;
   for (int i = 0; i < a.nt; ++i) tile = tile && tile_view(a.t[i], S, P);
-  if (tile) {
-    const int64_t nb0 = ceil_div(npos * a.t[0].H * (P / 2), kTileChunks);
-    const int64_t nb1 = a.nt > 1 ? ceil_div(npos * a.t[1].H * (P / 2), kTileChunks) : 0;
-    if (nb0 + nb1 <= 0x7fffffffLL) {
-      int64_t nb = nb0;
-      void* targs[] = {&a, &nb};
-      launch_dominant_raw(reinterpret_cast<const void*>(rope_c64_tile), dim3((unsigned)(nb0 + nb1)), dim3(kThreads),
+  if (tile && npos <= INT32_MAX) {
+    C64TileArgs ta{};
+    bool fits = true;
+    for (int i = 0; i < a.nt; ++i) {
+      const int64_t gpp = a.t[i].H * P / (2 * kWave);
+      fits = fits && gpp <= INT32_MAX / kWave && npos * gpp * kWave <= INT32_MAX;  // 32-bit chunk indices
+      if (fits) ta.t[i] = C64TileTensor{a.t[i].x, a.t[i].out, (uint32_t)(npos * gpp), make_div32((uint32_t)gpp)};
+    }
+    if (fits) {
+      ta.nb0 = (uint32_t)ceil_div(ta.t[0].groups, kTileGroups);
+      const int64_t nb1 = a.nt > 1 ? ceil_div(ta.t[1].groups, kTileGroups) : 0;
+      ta.S = make_div32((uint32_t)S);
+      ta.cph = make_div32((uint32_t)(P / 2));
+      ta.pos = a.pos;
+      ta.pb = a.pb;
+      ta.psb = a.psb;
+      ta.pss = a.pss;
+      ta.freqs = a.freqs;
+      ta.frows = a.frows;
+      ta.frs = a.frs;
+      ta.sgn = a.sgn;
+      ta.err = a.err;
+      void* targs[] = {&ta};
+      launch_dominant_raw(reinterpret_cast<const void*>(rope_c64_tile), dim3((unsigned)(ta.nb0 + nb1)), dim3(kThreads),
                           targs, 0, as_stream(stream));
       return check_launch(who);
     }

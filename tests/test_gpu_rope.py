@@ -106,14 +106,18 @@ def test_rope_fp32_output(gpu, vec):
 @pytest.mark.parametrize("pairing", ["half", "interleaved"])
 @pytest.mark.parametrize("table", [False, True])
 @pytest.mark.parametrize("conj", [False, True])
-def test_rope_tile_path_matches_position_path(gpu, oracle_lib, pairing, table, conj):
+@pytest.mark.parametrize("B,S,Hq,Hk", [(1, 33, 4, 8), (3, 19, 12, 20)])
+def test_rope_tile_path_matches_position_path(gpu, oracle_lib, pairing, table, conj, B, S, Hq, Hk):
     """Contiguous [B, S, H, 128] tensors with H % 4 == 0 take the tile kernel
-    (512-chunk blocks; here both tensors end in a partial tile: 33 * 4 * 16 =
-    2112 and 33 * 8 * 16 = 4224 chunks).  The same data read through a view
-    with a wider head stride takes the one-wave-per-position kernel: both must
-    give identical bits, and meet the oracle's bar."""
-    g = gen(900 + 4 * table + 2 * conj + (pairing == "half"))
-    B, S, Hq, Hk, D, P = 1, 33, 4, 8, 128, 64
+    (512-chunk blocks; both tensors end in a partial tile, e.g. 33 * 4 * 16 =
+    2112 and 33 * 8 * 16 = 4224 chunks; the second shape has 3 and 5 head
+    groups per position and 3 batch rows, so a block's positions and their
+    batch rows come from divisions by 3, 5 and 19).  The same data read
+    through a view with a wider head stride takes the one-wave-per-position
+    kernel: both must give identical bits, and meet the oracle's bar."""
+    print(f"[rope tile] {pairing} table={table} conj={conj} B={B} S={S} H={Hq},{Hk}", flush=True)
+    g = gen(900 + 4 * table + 2 * conj + (pairing == "half") + 8 * B)
+    D, P = 128, 64
     q = randn_bf16((B, S, Hq, D), g)
     k = randn_bf16((B, S, Hk, D), g)
     pos = torch.randint(0, P, (B, S), generator=g) if table else (torch.arange(S) * 97 % 4096).repeat(B, 1)

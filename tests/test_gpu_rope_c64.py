@@ -92,14 +92,17 @@ def test_full_shape_against_torch(gpu):
 
 @pytest.mark.parametrize("gather", [False, True])
 @pytest.mark.parametrize("conj", [False, True])
-def test_tile_path_matches_position_path(gpu, gather, conj):
+@pytest.mark.parametrize("B,S,Hq,Hk,P", [(2, 37, 4, 2, 64), (3, 11, 8, 16, 48)])
+def test_tile_path_matches_position_path(gpu, gather, conj, B, S, Hq, Hk, P):
     """Contiguous tensors with H * P / 2 a multiple of 64 take the tile
-    kernel (here 2 * 37 * 128 and 2 * 37 * 64 chunks: both end in a partial
-    512-chunk tile); the same values read through a head-strided view take
-    the one-wave-per-position kernel.  Identical bits, and the oracle's bound."""
-    print(f"[rope c64 tile] gather={gather} conj={conj}", flush=True)
-    g = torch.Generator().manual_seed(11)
-    B, S, Hq, Hk, P, rows = 2, 37, 4, 2, 64, 50
+    kernel (e.g. 2 * 37 * 128 and 2 * 37 * 64 chunks: both end in a partial
+    512-chunk tile; with P = 48 a head is 24 chunks, so a wave's 64 chunks
+    straddle heads and a chunk's place in its head is a division by 24); the
+    same values read through a head-strided view take the one-wave-per-
+    position kernel.  Identical bits, and the oracle's bound."""
+    print(f"[rope c64 tile] gather={gather} conj={conj} B={B} S={S} H={Hq},{Hk} P={P}", flush=True)
+    g = torch.Generator().manual_seed(11 + P)
+    rows = 50
     q, k = _c64((B, S, Hq, P), g).to(gpu), _c64((B, S, Hk, P), g).to(gpu)
     table = _c64((rows, P), g).to(gpu)
     pos = (torch.randint(0, rows, (B, S), generator=g) if gather else None)
