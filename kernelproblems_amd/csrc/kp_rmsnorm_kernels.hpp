@@ -82,7 +82,20 @@ __host__ __device__ __forceinline__ int64_t part_index(int64_t c, int64_t p, int
 }
 
 __device__ __forceinline__ int64_t w_index(int64_t c, int64_t seg_len, int64_t seg_stride) {
+  if (c < seg_len) return c;  // first segment, i.e. every column of a contiguous weight: no division
+  if (((uint64_t)c | (uint64_t)seg_len) < 0x80000000ull) {  // 32-bit divide (a 64-bit one is ~100 instructions)
+    const uint32_t q = (uint32_t)c / (uint32_t)seg_len;
+    return (int64_t)q * seg_stride + (c - (int64_t)q * seg_len);
+  }
   return (c / seg_len) * seg_stride + (c % seg_len);
+}
+
+// Row groups of block b in a grid of G blocks walking groups b, b + G, ...
+// (b < G <= ngroups): ngroups fits 32 bits for any tensor that fits in
+// memory, so the divide is a 32-bit one.
+__device__ __forceinline__ int64_t block_trips(int64_t ngroups, int64_t b, int64_t G) {
+  if (ngroups <= 0x7fffffffLL) return (int64_t)((uint32_t)(ngroups - 1 - b) / (uint32_t)G) + 1;
+  return (ngroups - 1 - b) / G + 1;
 }
 
 // Raw (not yet summed) 16-byte chunks of up to NT row terms.  Rows are
@@ -218,6 +231,12 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   const int part = wave % WPR, rloc = wave / WPR;
   const int64_t col = (int64_t)part * SEG + lane * 8;
 
+  // Rows of 4 waves run one block per row (a one-shot grid, three blocks per
+  // CU): a new block waits ~1024 cycles before its loads, which paces the
+  // refill of a CU's slots.  Measured at [16384, 8192], two x terms, on one
+  // box: 171.0 us against 172.4 us without the pause, 174.2 us with half of
+  // it, 171.4 us with twice it.
+  if constexpr (WPR == 4) __builtin_amdgcn_s_sleep(16);
   float wf[VPL * 8];
   {
     u32x4 wv[VPL];
@@ -243,7 +262,7 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   ++it
   // Exact trip count: the grid never exceeds the row-group count, so every
   // block owns nb >= 1 groups and nothing is prefetched past its last one.
-  const int64_t nb = (ngroups - 1 - blockIdx.x) / G + 1;
+  const int64_t nb = block_trips(ngroups, blockIdx.x, G);
   int64_t g = blockIdx.x, k = 0;
   KP_LOAD(s0, g);
   for (; k + 2 < nb; k += 2, g += 2 * G) {
@@ -445,7 +464,7 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
                                           it);                                                                         \
   ++it
   // Exact trip count (see rms_fwd_vec): nb >= 1 groups per block.
-  const int64_t nb = (ngroups - 1 - blockIdx.x) / G + 1;
+  const int64_t nb = block_trips(ngroups, blockIdx.x, G);
   int64_t g = blockIdx.x, k = 0;
   KP_LOAD(0, g);
   for (; k + 2 < nb; k += 2, g += 2 * G) {
