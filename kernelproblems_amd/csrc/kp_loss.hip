@@ -370,12 +370,14 @@ struct RowTarget {
   bool valid;
 };
 
-__device__ __forceinline__ RowTarget fb_target(const FbArgs& a, int64_t row) {
-  const int64_t t = target_at(a.targets, a.tbytes, row);
+__device__ __forceinline__ RowTarget fb_target_of(const FbArgs& a, int64_t t) {
   const bool in_range = t >= 0 && t < a.V;
   const bool valid = t != a.ignore && in_range;
   if (t != a.ignore && !in_range && threadIdx.x == 0 && a.err) a.err[0] = 1;
   return RowTarget{valid ? t : -1, valid ? -a.g : 0.0f, valid};
+}
+__device__ __forceinline__ RowTarget fb_target(const FbArgs& a, int64_t row) {
+  return fb_target_of(a, target_at(a.targets, a.tbytes, row));
 }
 
 // Thread 0 records the row's loss lse - x_t (x_t loaded before any store of
@@ -439,6 +441,25 @@ __device__ __forceinline__ void fb_load_row(rsrc_t r, int tid, int64_t cpr, u32x
   for (int k = 0; k < KC; ++k) v[k] = __builtin_amdgcn_raw_buffer_load_b128(r, fb_off(tid, k, cpr), 0, kBufNT);
 }
 
+// Target of `row` (int32 or int64 ids) by two 4-byte buffer loads and no
+// branch: a load under a branch makes the wait-count pass drain every
+// outstanding load and store at the join, i.e. the whole previous row's
+// stores and this row's loads.  For int32 ids the high word may fall past
+// the array, where the descriptor's range check returns 0.
+__device__ __forceinline__ void fb_target_load(const FbArgs& a, int64_t row, uint32_t& lo, uint32_t& hi) {
+  const rsrc_t r = row_rsrc(a.targets, (uint32_t)(a.M * a.tbytes));
+  const uint32_t off = (uint32_t)(row * a.tbytes);
+  lo = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  hi = (uint32_t)__builtin_amdgcn_raw_buffer_load_b32(r, off + 4u, 0, 0);
+}
+// The words pass through an empty asm first, so that the compiler neither
+// sinks the high word's load into a branch nor reads the words before the
+// row's own loads are issued.
+__device__ __forceinline__ int64_t fb_target_value(const FbArgs& a, uint32_t lo, uint32_t hi) {
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  return a.tbytes == 8 ? (int64_t)(((uint64_t)hi << 32) | lo) : (int64_t)(int32_t)lo;
+}
+
 // Persistent: one block per CU walks rows blockIdx.x, + gridDim.x, ...; the
 // next row's loads are issued as soon as the previous row's stores are, so
 // the store stream of one row overlaps the load stream of the next (754 us
@@ -461,11 +482,20 @@ __global__ __launch_bounds__(kFbThreads) void xent_fwd_bwd_vec(FbArgs a) {
     // being hoisted out of the loop (16 more live VGPRs)
     int tid = threadIdx.x;
     asm volatile("" : "+v"(tid));
+    // the row's target is requested ahead of its data: vmcnt counts in issue
+    // order, so waiting for the target afterwards does not wait for the row
+    uint32_t t_lo, t_hi;
+    fb_target_load(a, row, t_lo, t_hi);
+    __builtin_amdgcn_sched_barrier(0);
     fb_load_row<KC>(row_rsrc(a.logits + row * a.rs, row_bytes), tid, cpr, v);
     __builtin_amdgcn_sched_barrier(0);
     const rsrc_t ro = row_rsrc(a.out + row * a.ors, row_bytes);
-    const RowTarget rt = fb_target(a, row);
-    const float xt = (a.row_loss != nullptr && tid == 0 && rt.valid) ? bf_to_f(a.logits[row * a.rs + rt.t]) : 0.0f;
+    const RowTarget rt = fb_target_of(a, fb_target_value(a, t_lo, t_hi));
+    // x_t for the row loss, loaded by every lane without a branch (an invalid
+    // target reads out of range: 0) and consumed only before the block
+    // combine, so its wait is not a wait for the whole row; thread 0 uses it
+    uint16_t xtb = (uint16_t)__builtin_amdgcn_raw_buffer_load_b16(
+        row_rsrc(a.logits + row * a.rs, row_bytes), rt.valid ? (uint32_t)rt.t * 2u : kOutOfRange, 0, 0);
     float m = -INFINITY;
 #pragma unroll
     for (int k = 0; k < KC; ++k) {
@@ -491,7 +521,8 @@ __global__ __launch_bounds__(kFbThreads) void xent_fwd_bwd_vec(FbArgs a) {
       }
       s = (part[0] + part[1]) + (part[2] + part[3]);
     }
-    asm volatile("" ::"v"(xt));  // x_t has arrived before the barrier: other waves may overwrite it after
+    asm volatile("" : "+v"(xtb));  // x_t has arrived before the barrier: other waves may overwrite it after
+    const float xt = (a.row_loss != nullptr && tid == 0 && rt.valid) ? bf_to_f(xtb) : 0.0f;
     block_combine<kWaves>(R, s, red[parity]);
     const float lg = log2f(s);
     fb_row_loss(a, row, rt, R, lg, xt);
@@ -687,7 +718,8 @@ int kp_cross_entropy_fwd_bwd_bf16(const void* logits, int64_t row_stride, int64_
     const int64_t cpr = V / 8;
     const bool vec = V % 8 == 0 && aligned16(logits) && aligned16(grad_logits) &&
                      (M == 1 || (row_stride % 8 == 0 && out_row_stride % 8 == 0)) &&
-                     cpr <= (int64_t)kFbThreads * kFbMaxChunks;
+                     cpr <= (int64_t)kFbThreads * kFbMaxChunks &&
+                     M * target_bytes <= 0xffffffffLL;  // the targets' buffer descriptor is 32-bit
     void* args[] = {&a};
     if (vec) {
       int kc = 1;

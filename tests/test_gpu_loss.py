@@ -199,6 +199,23 @@ def test_fwd_bwd_matches_oracle(gpu, kind, M, V):
     assert torch.equal(kp.cross_entropy_forward_backward(x, t, gl), out)  # without the forward outputs
 
 
+@pytest.mark.parametrize("M,V", [(5, 128256), (9, 16384), (1, 8)])
+def test_fwd_bwd_int32_targets(gpu, M, V):
+    """int32 targets in the register-row kernel: the last row's id is the
+    array's last 4 bytes (its would-be high word lies past the end), ignored
+    rows carry -100 as int32.  Same bits as with the same ids as int64."""
+    print(f"[xent fwd+bwd int32] [{M},{V}]", flush=True)
+    g = torch.Generator().manual_seed(M * 23 + V)
+    x = _logits(M, V, g, gpu, "contig")
+    t64 = _targets(M, V, g, gpu)
+    gl = 1 / 8192
+    o64, l64, w64 = kp.cross_entropy_forward_backward(x, t64, gl, scale=gl, return_loss=True)
+    o32, l32, w32 = kp.cross_entropy_forward_backward(x, t64.to(torch.int32), gl, scale=gl, return_loss=True)
+    assert torch.equal(o32, o64) and float(l32) == float(l64) and float(w32) == float(w64)
+    eo, bad = oracle.cross_entropy_fwd_bwd(to_u16(x), t64.cpu().numpy(), gl)
+    assert bad == 0 and ulp_bf16(to_u16(o32), eo).max() <= 1
+
+
 def test_fwd_bwd_special_rows(gpu):
     """Confident rows (a dominant target logit: the target gradient g (p - 1)
     cancels), masked vocabulary, large logits, ramps; out-of-range targets
