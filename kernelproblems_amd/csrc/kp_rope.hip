@@ -464,7 +464,10 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
   const int c = lane & 15;
   const int f0 = (kHalf ? (c & 7) : c) * FPU;
   const bool lo = c < 8;
-  const float sgn = a.conj ? -1.f : 1.f;
+  // Rotate-half, lane holding x1 (lo): x1 c - x2 s; holding x2: x2 c + x1 s --
+  // both fma(own, c, partner * s') with s' = -s or s, the same roundings as
+  // rot()'s two outputs (the negation is exact).  conj flips s' again.
+  const float sgn = (a.conj ? -1.f : 1.f) * ((kHalf && lo) ? -1.f : 1.f);
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const uint32_t g = g0 + wave + 4 * u;
@@ -509,14 +512,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
       unpack8(pv, par);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        float oa, ob;
-        if (lo) {
-          rot(own[e], par[e], cv[e], sv[e], oa, ob);
-          o[e] = oa;
-        } else {
-          rot(par[e], own[e], cv[e], sv[e], oa, ob);
-          o[e] = ob;
-        }
+        o[e] = __builtin_fmaf(own[e], cv[e], par[e] * sv[e]);
         if (!ok) o[e] = 0.f;
       }
     } else {
