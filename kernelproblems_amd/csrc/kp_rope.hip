@@ -375,7 +375,7 @@ __global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
 // ------------------------------------------------------------ tile path
 // D = 128, every tensor stored [B, S, H, 128] contiguously in and out (the
 // forward fragments and the rotate-half configuration), H a multiple of 4,
-// bf16 outputs.  Unlike rope_fast (one wave per position, up to 16 KiB per
+// bf16 or fp32 outputs.  Unlike rope_fast (one wave per position, up to 16 KiB per
 // wave), a block owns 512 consecutive 16-byte chunks of one tensor -- thread
 // t chunks t and t + 256, tensor 0's blocks first -- the short-lived,
 // fine-grained streaming layout that measured fastest on MI355X (c4: 56 us
@@ -399,9 +399,10 @@ constexpr int kTileMaxPos = kTileGroups;       // a position is >= 1 group
 
 struct TileTensor {
   const uint16_t* x;
-  uint16_t* out;
+  void* out;        // bf16, or fp32 when out_f32
   uint32_t groups;  // B * S * H / 4
   Div32 gpp;        // groups per position, H / 4
+  int out_f32;
 };
 struct TileArgs {
   TileTensor t[2];
@@ -522,7 +523,16 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
         if (!ok) o[2 * q] = o[2 * q + 1] = 0.f;
       }
     }
-    if (g <= glast) st16_stream(T.out + ((size_t)g * 64 + lane) * 8, pack8(o));
+    if (g <= glast) {
+      const size_t e0 = ((size_t)g * 64 + lane) * 8;  // first element of this chunk
+      if (T.out_f32) {  // block-uniform: the fp32 rotation result, 32 bytes per chunk
+        float* of = static_cast<float*>(T.out) + e0;
+        st16f_stream(of, f32x4{o[0], o[1], o[2], o[3]});
+        st16f_stream(of + 4, f32x4{o[4], o[5], o[6], o[7]});
+      } else {
+        st16_stream(static_cast<uint16_t*>(T.out) + e0, pack8(o));
+      }
+    }
   }
 }
 
@@ -541,7 +551,7 @@ bool tile_ok(const RopeArgs& a, bool table) {
   for (int i = 0; i < a.nt; ++i) {
     const RopeTensor& t = a.t[i];
     const int64_t hd = t.H * kFastD;
-    if (t.H <= 0 || (t.H & 3) != 0 || t.out_f32 || !aligned16(t.x) || !aligned16(t.out)) return false;
+    if (t.H <= 0 || (t.H & 3) != 0 || !aligned16(t.x) || !aligned16(t.out)) return false;
     if (t.H > INT32_MAX / 16 || npos * t.H * 16 > INT32_MAX) return false;  // 32-bit chunk indices
     if (t.xs[2] != kFastD || t.xs[1] != hd || t.xs[0] != a.S * hd) return false;
     if (t.os[2] != kFastD || t.os[1] != hd || t.os[0] != a.S * hd) return false;
@@ -662,8 +672,8 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
   if (vec && tile_ok(a, freqs_cis != nullptr)) {
     TileArgs ta{};
     for (int i = 0; i < a.nt; ++i)
-      ta.t[i] = TileTensor{a.t[i].x, static_cast<uint16_t*>(a.t[i].out), (uint32_t)(npos * (a.t[i].H / 4)),
-                           make_div32((uint32_t)(a.t[i].H / 4))};
+      ta.t[i] = TileTensor{a.t[i].x, a.t[i].out, (uint32_t)(npos * (a.t[i].H / 4)),
+                           make_div32((uint32_t)(a.t[i].H / 4)), a.t[i].out_f32};
     ta.nb0 = (uint32_t)ceil_div(ta.t[0].groups, kTileGroups);
     const int64_t nb1 = a.nt > 1 ? ceil_div(ta.t[1].groups, kTileGroups) : 0;
     ta.npos = (uint32_t)npos;

@@ -146,6 +146,35 @@ def test_rope_tile_path_matches_position_path(gpu, oracle_lib, pairing, table, c
         assert_bf16_close(to_u16(out), exp, what="tile", max_ulp=1, min_exact=0.99, ulp_abs_slack=4e-6)
 
 
+@pytest.mark.parametrize("table", [False, True])
+def test_rope_tile_fp32_output(gpu, table):
+    """fp32 outputs (the un-rounded rotation of v7/0f38bc55457c) through the
+    tile kernel: identical to the one-wave-per-position kernel's fp32 output
+    on a head-strided view of the same data, and rounding it gives the bf16
+    result bit for bit."""
+    print(f"[rope tile fp32] table={table}", flush=True)
+    g = gen(950 + table)
+    B, S, Hq, Hk, D, P = 2, 21, 12, 4, 128, 64
+    q = randn_bf16((B, S, Hq, D), g).to(gpu)
+    k = randn_bf16((B, S, Hk, D), g).to(gpu)
+    pos = (torch.randint(0, P, (B, S), generator=g) if table else (torch.arange(S) * 31 % 4096).repeat(B, 1)).to(gpu)
+    kw = dict(positions=pos, pairing="half")
+    if table:
+        kw["freqs_cis"] = torch.complex(torch.randn(P, D // 2, generator=g), torch.randn(P, D // 2, generator=g)).to(gpu)
+    else:
+        kw["theta"] = 500000.0
+    q32, k32 = kp.rope(q, k, q_dtype=torch.float32, k_dtype=torch.float32, **kw)
+    qb, kb = kp.rope(q, k, **kw)
+    qw = torch.zeros((B, S, Hq, 2 * D), dtype=torch.bfloat16, device=gpu)
+    qw[..., :D] = q
+    kw_ = torch.zeros((B, S, Hk, 2 * D), dtype=torch.bfloat16, device=gpu)
+    kw_[..., :D] = k
+    qf, kf = kp.rope(qw[..., :D], kw_[..., :D], q_dtype=torch.float32, k_dtype=torch.float32, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(q32, qf) and torch.equal(k32, kf)
+    assert torch.equal(q32.to(torch.bfloat16), qb) and torch.equal(k32.to(torch.bfloat16), kb)
+
+
 def test_rope_tile_path_out_of_table_position(gpu):
     """An id outside the table in the tile kernel: its rows are zero and the flag is raised."""
     x = torch.ones((1, 6, 4, 128), dtype=torch.bfloat16, device=gpu)
