@@ -307,6 +307,22 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
                  const float* freqs_cis, int64_t freq_rows, int64_t freq_row_stride,
                  int conj, int out_f32_mask, int32_t* error_flag, void* stream);
 
+/* kp_rope_bf16 with every output written twice: out0_copy (and out1_copy,
+ * required when x1 != NULL) receive the same values as out0 / out1, laid out
+ * with the same strides, from one pass over the inputs.  Replaces the
+ * fragment that rotates q and k twice and returns both pairs as separate
+ * tensors:
+ *   v5/ca76bd89ec38/problem.py:10-132 (and its repeat v4/6b92d6e665ab)
+ * A copy may not be its own output (KP_EINVAL).
+ */
+int kp_rope_bf16_twice(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides,
+                       const int64_t* out0_strides, const void* x1, void* out1, int64_t H1,
+                       const int64_t* x1_strides, const int64_t* out1_strides, int64_t B, int64_t S, int64_t D,
+                       const void* positions, int pos_bytes, int64_t pos_stride_b, int64_t pos_stride_s,
+                       int pairing, double theta, const float* freqs_cis, int64_t freq_rows,
+                       int64_t freq_row_stride, int conj, int out_f32_mask, void* out0_copy, void* out1_copy,
+                       int32_t* error_flag, void* stream);
+
 /* ------------------------------------------------------------------------
  * Rotary position embedding on complex64 data: q and k already viewed as
  * complex (fp32 (re, im) pairs), multiplied by a complex64 table row per

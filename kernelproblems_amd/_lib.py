@@ -97,6 +97,11 @@ SIGNATURES = {
         [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64,
          i32, f64, vp, i64, i64, i32, i32, vp, vp],
     ),
+    "kp_rope_bf16_twice": (
+        i32,
+        [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64,
+         i32, f64, vp, i64, i64, i32, i32, vp, vp, vp, vp],
+    ),
     "kp_rope_c64": (i32, [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64, vp, i64, i64,
                           i32, vp, vp]),
     "kp_unshard_bf16": (i32, [vp, i64, i64, pi64, pi64, pvp, i32, vp]),

@@ -403,6 +403,7 @@ struct TileTensor {
   uint32_t groups;  // B * S * H / 4
   Div32 gpp;        // groups per position, H / 4
   int out_f32;
+  void* out2;       // a second copy of the output (same layout), or NULL
 };
 struct TileArgs {
   TileTensor t[2];
@@ -529,8 +530,15 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
         float* of = static_cast<float*>(T.out) + e0;
         st16f_stream(of, f32x4{o[0], o[1], o[2], o[3]});
         st16f_stream(of + 4, f32x4{o[4], o[5], o[6], o[7]});
+        if (T.out2) {
+          float* of2 = static_cast<float*>(T.out2) + e0;
+          st16f_stream(of2, f32x4{o[0], o[1], o[2], o[3]});
+          st16f_stream(of2 + 4, f32x4{o[4], o[5], o[6], o[7]});
+        }
       } else {
-        st16_stream(static_cast<uint16_t*>(T.out) + e0, pack8(o));
+        const u32x4 pk = pack8(o);
+        st16_stream(static_cast<uint16_t*>(T.out) + e0, pk);
+        if (T.out2) st16_stream(static_cast<uint16_t*>(T.out2) + e0, pk);
       }
     }
   }
@@ -616,12 +624,14 @@ using namespace kp;
 
 extern "C" {
 
-int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides, const int64_t* out0_strides,
-                 const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,
-                 int64_t B, int64_t S, int64_t D, const void* positions, int pos_bytes, int64_t pos_stride_b,
-                 int64_t pos_stride_s, int pairing, double theta, const float* freqs_cis, int64_t freq_rows,
-                 int64_t freq_row_stride, int conj, int out_f32_mask, int32_t* error_flag, void* stream) {
-  static const char* who = "kp_rope_bf16";
+// Both entry points: out0_copy / out1_copy (kp_rope_bf16_twice) receive the
+// same values as out0 / out1, laid out with the same strides.
+static int rope_impl(const char* who, const void* x0, void* out0, int64_t H0, const int64_t* x0_strides,
+                     const int64_t* out0_strides, const void* x1, void* out1, int64_t H1,
+                     const int64_t* x1_strides, const int64_t* out1_strides, int64_t B, int64_t S, int64_t D,
+                     const void* positions, int pos_bytes, int64_t pos_stride_b, int64_t pos_stride_s, int pairing,
+                     double theta, const float* freqs_cis, int64_t freq_rows, int64_t freq_row_stride, int conj,
+                     int out_f32_mask, void* out0_copy, void* out1_copy, int32_t* error_flag, void* stream) {
   if (x0 == nullptr || out0 == nullptr || x0_strides == nullptr || out0_strides == nullptr)
     return fail(KP_EINVAL, "%s: tensor 0 needs x, out and strides", who);
   if (x1 != nullptr && (out1 == nullptr || x1_strides == nullptr || out1_strides == nullptr))
@@ -669,11 +679,12 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
 
   bool vec = tensor_vec_ok(a.t[0], D, pairing) && (a.nt == 1 || tensor_vec_ok(a.t[1], D, pairing));
   const int64_t blocks_needed = ceil_div(npos, kWavesPerBlock);
-  if (vec && tile_ok(a, freqs_cis != nullptr)) {
+  const bool copies_aligned = (out0_copy == nullptr || aligned16(out0_copy)) && (out1_copy == nullptr || aligned16(out1_copy));
+  if (vec && copies_aligned && tile_ok(a, freqs_cis != nullptr)) {
     TileArgs ta{};
     for (int i = 0; i < a.nt; ++i)
       ta.t[i] = TileTensor{a.t[i].x, a.t[i].out, (uint32_t)(npos * (a.t[i].H / 4)),
-                           make_div32((uint32_t)(a.t[i].H / 4)), a.t[i].out_f32};
+                           make_div32((uint32_t)(a.t[i].H / 4)), a.t[i].out_f32, i == 0 ? out0_copy : out1_copy};
     ta.nb0 = (uint32_t)ceil_div(ta.t[0].groups, kTileGroups);
     const int64_t nb1 = a.nt > 1 ? ceil_div(ta.t[1].groups, kTileGroups) : 0;
     ta.npos = (uint32_t)npos;
@@ -697,24 +708,62 @@ int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strid
     launch_dominant_raw(fk, dim3((unsigned)(ta.nb0 + nb1)), dim3(kThreads), args, 0, as_stream(stream));
     return check_launch(who);
   }
-  if (vec) {
-    const RopeKernel fk = pick_fast(a, pairing, freqs_cis != nullptr);
+  // Other layouts: one launch per copy (the copies' rows are written by a
+  // second pass over the inputs).
+  const bool copies = out0_copy != nullptr;
+  if (copies) vec = vec && copies_aligned;
+  for (int rep = 0; rep < (copies ? 2 : 1); ++rep) {
+    if (rep == 1) {
+      a.t[0].out = out0_copy;
+      if (a.nt > 1) a.t[1].out = out1_copy;
+    }
+    const RopeKernel fk = vec ? pick_fast(a, pairing, freqs_cis != nullptr) : nullptr;
     if (fk != nullptr && blocks_needed <= INT32_MAX) {
       void* args[] = {&a};
       launch_dominant_raw(reinterpret_cast<const void*>(fk), dim3((unsigned)blocks_needed), dim3(kThreads), args, 0,
                           as_stream(stream));
-      return check_launch(who);
+    } else {
+      const int64_t cap = (int64_t)cu_count() * 16;
+      const int grid = (int)(blocks_needed < cap ? blocks_needed : cap);
+      hipStream_t s = as_stream(stream);
+      const bool tab = freqs_cis != nullptr;
+      if (vec && tab) KP_LAUNCH_DOMINANT((rope_kernel<true, true>), dim3(grid), dim3(kThreads), 0, s, a);
+      else if (vec) KP_LAUNCH_DOMINANT((rope_kernel<true, false>), dim3(grid), dim3(kThreads), 0, s, a);
+      else if (tab) KP_LAUNCH_DOMINANT((rope_kernel<false, true>), dim3(grid), dim3(kThreads), 0, s, a);
+      else KP_LAUNCH_DOMINANT((rope_kernel<false, false>), dim3(grid), dim3(kThreads), 0, s, a);
     }
+    const int st = check_launch(who);
+    if (st != KP_OK) return st;
   }
-  const int64_t cap = (int64_t)cu_count() * 16;
-  const int grid = (int)(blocks_needed < cap ? blocks_needed : cap);
-  hipStream_t s = as_stream(stream);
-  const bool tab = freqs_cis != nullptr;
-  if (vec && tab) KP_LAUNCH_DOMINANT((rope_kernel<true, true>), dim3(grid), dim3(kThreads), 0, s, a);
-  else if (vec) KP_LAUNCH_DOMINANT((rope_kernel<true, false>), dim3(grid), dim3(kThreads), 0, s, a);
-  else if (tab) KP_LAUNCH_DOMINANT((rope_kernel<false, true>), dim3(grid), dim3(kThreads), 0, s, a);
-  else KP_LAUNCH_DOMINANT((rope_kernel<false, false>), dim3(grid), dim3(kThreads), 0, s, a);
-  return check_launch(who);
+  return KP_OK;
+}
+
+int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides, const int64_t* out0_strides,
+                 const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,
+                 int64_t B, int64_t S, int64_t D, const void* positions, int pos_bytes, int64_t pos_stride_b,
+                 int64_t pos_stride_s, int pairing, double theta, const float* freqs_cis, int64_t freq_rows,
+                 int64_t freq_row_stride, int conj, int out_f32_mask, int32_t* error_flag, void* stream) {
+  return rope_impl("kp_rope_bf16", x0, out0, H0, x0_strides, out0_strides, x1, out1, H1, x1_strides, out1_strides, B,
+                   S, D, positions, pos_bytes, pos_stride_b, pos_stride_s, pairing, theta, freqs_cis, freq_rows,
+                   freq_row_stride, conj, out_f32_mask, nullptr, nullptr, error_flag, stream);
+}
+
+int kp_rope_bf16_twice(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides,
+                       const int64_t* out0_strides, const void* x1, void* out1, int64_t H1,
+                       const int64_t* x1_strides, const int64_t* out1_strides, int64_t B, int64_t S, int64_t D,
+                       const void* positions, int pos_bytes, int64_t pos_stride_b, int64_t pos_stride_s,
+                       int pairing, double theta, const float* freqs_cis, int64_t freq_rows,
+                       int64_t freq_row_stride, int conj, int out_f32_mask, void* out0_copy, void* out1_copy,
+                       int32_t* error_flag, void* stream) {
+  static const char* who = "kp_rope_bf16_twice";
+  if (out0_copy == nullptr || (x1 != nullptr && out1_copy == nullptr))
+    return fail(KP_EINVAL, "%s: every rotated tensor needs its copy", who);
+  if (out0_copy == out0 || (x1 != nullptr && out1_copy == out1))
+    return fail(KP_EINVAL, "%s: a copy must not be its own output", who);
+  return rope_impl(who, x0, out0, H0, x0_strides, out0_strides, x1, out1, H1, x1_strides, out1_strides, B, S, D,
+                   positions, pos_bytes, pos_stride_b, pos_stride_s, pairing, theta, freqs_cis, freq_rows,
+                   freq_row_stride, conj, out_f32_mask, out0_copy, x1 != nullptr ? out1_copy : nullptr, error_flag,
+                   stream);
 }
 
 }  // extern "C"

@@ -22,6 +22,6 @@ def table_rows(freqs: torch.Tensor) -> torch.Tensor:
     return freqs.reshape(-1, freqs.shape[-1])
 
 
-def rotate(x, k=None, *, freqs, positions=None, q_dtype=torch.bfloat16, k_dtype=torch.bfloat16):
+def rotate(x, k=None, *, freqs, positions=None, q_dtype=torch.bfloat16, k_dtype=torch.bfloat16, copies=False):
     return F.rope(x, k, positions=positions, freqs_cis=freqs, pairing="interleaved",
-                  q_dtype=q_dtype, k_dtype=k_dtype)
+                  q_dtype=q_dtype, k_dtype=k_dtype, copies=copies)

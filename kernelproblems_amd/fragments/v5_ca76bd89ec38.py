@@ -2,7 +2,7 @@
 twice (the graph rotates q and k once for attention and once more for the
 recompute) as [1, H, S, D] transposed views: v5/ca76bd89ec38/problem.py:10-132
 (inputs :135-140).  The two pairs are separate tensors, as in the fragment;
-each comes from its own launch of the rotation kernel."""
+one launch reads q and k once and writes both pairs."""
 import torch
 
 from ._common import randint, randn
@@ -17,11 +17,8 @@ def get_inputs(device="cuda", generator=None):
 
 
 def rotate_twice(pos, freqs, mm_q, mm_k):
-    outs = []
-    for _ in range(2):
-        q, k = rotate(heads(mm_q), heads(mm_k), freqs=freqs, positions=pos.view(1, -1))
-        outs += [q.transpose(1, 2), k.transpose(1, 2)]
-    return tuple(outs)
+    q, k, q2, k2 = rotate(heads(mm_q), heads(mm_k), freqs=freqs, positions=pos.view(1, -1), copies=True)
+    return q.transpose(1, 2), k.transpose(1, 2), q2.transpose(1, 2), k2.transpose(1, 2)
 
 
 def kernel_function(arg586_1, arg582_1, mm_217, mm_218):

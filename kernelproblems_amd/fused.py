@@ -485,6 +485,7 @@ def rope(
     conj: bool = False,
     q_dtype: torch.dtype = torch.bfloat16,
     k_dtype: torch.dtype = torch.bfloat16,
+    copies: bool = False,
 ):
     """Rotary embedding of q (and k) laid out [B, S, H, D] (unit stride on D).
 
@@ -495,7 +496,9 @@ def rope(
     pairing "half" = (i, i + D/2), "interleaved" = (2i, 2i+1).  conj=True
     rotates by the conjugate (backward).  q_dtype / k_dtype pick each
     output's type, bf16 or fp32 (the fp32 rotation result without the final
-    rounding).  Returns contiguous (q_out, k_out).
+    rounding).  Returns contiguous (q_out, k_out); with copies=True, returns
+    (q_out, k_out, q_copy, k_copy), the copies separate tensors holding the
+    same values, written by the same pass over q and k (kp_rope_bf16_twice).
     """
     for dt in (q_dtype, k_dtype):
         if dt not in (torch.bfloat16, torch.float32):
@@ -533,12 +536,24 @@ def rope(
             raise RuntimeError("rope: need theta > 0 or freqs_cis")
         th = float(theta)
     flag = _flag(dev) if freqs_cis is not None else None
+    f32_mask = (1 if q_dtype == torch.float32 else 0) | (2 if k is not None and k_dtype == torch.float32 else 0)
+    if copies:
+        q_copy = torch.empty_like(q_out)
+        k_copy = torch.empty_like(k_out) if k_out is not None else None
+        L.call(
+            "kp_rope_bf16_twice",
+            q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(qs), L.i64_array(list(q_out.stride()[:3])),
+            *k_args,
+            B, S, D, pos_ptr, pos_bytes, psb, pss, mode, th, f_ptr, frows, frs, 1 if conj else 0, f32_mask,
+            q_copy.data_ptr(), _ptr(k_copy), _ptr(flag), _stream(dev),
+        )
+        _raise_if_flagged(flag, "rope")
+        return q_out, k_out, q_copy, k_copy
     L.call(
         "kp_rope_bf16",
         q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(qs), L.i64_array(list(q_out.stride()[:3])),
         *k_args,
-        B, S, D, pos_ptr, pos_bytes, psb, pss, mode, th, f_ptr, frows, frs, 1 if conj else 0,
-        (1 if q_dtype == torch.float32 else 0) | (2 if k is not None and k_dtype == torch.float32 else 0),
+        B, S, D, pos_ptr, pos_bytes, psb, pss, mode, th, f_ptr, frows, frs, 1 if conj else 0, f32_mask,
         _ptr(flag), _stream(dev),
     )
     _raise_if_flagged(flag, "rope")

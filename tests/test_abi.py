@@ -93,6 +93,12 @@ def test_rope_validation(lib):
             0, 0, -1.0, None, 0, 0, 0, 0, None, None)  # theta <= 0 without a table
     _expect(lib, L.KP_EINVAL, "kp_rope_bf16", 16, 32, 1, st, st, None, None, 0, None, None, *common, 8, None, 0, 0,
             0, 5, 1e4, None, 0, 0, 0, 0, None, None)  # unknown pairing
+    _expect(lib, L.KP_EINVAL, "kp_rope_bf16_twice", 16, 32, 1, st, st, None, None, 0, None, None, *common, 8, None,
+            0, 0, 0, 0, 1e4, None, 0, 0, 0, 0, None, None, None, None)  # no copy
+    _expect(lib, L.KP_EINVAL, "kp_rope_bf16_twice", 16, 32, 1, st, st, None, None, 0, None, None, *common, 8, None,
+            0, 0, 0, 0, 1e4, None, 0, 0, 0, 0, 32, None, None, None)  # the copy is the output itself
+    _expect(lib, L.KP_EINVAL, "kp_rope_bf16_twice", 16, 32, 1, st, st, 48, 64, 1, st, st, *common, 8, None,
+            0, 0, 0, 0, 1e4, None, 0, 0, 0, 0, 96, None, None, None)  # k without its copy
 
 
 def test_unshard_validation(lib):

@@ -181,3 +181,38 @@ def test_rope_tile_path_out_of_table_position(gpu):
     freqs = torch.ones((3, 64), dtype=torch.complex64, device=gpu)
     with pytest.raises(IndexError):
         kp.rope(x, positions=torch.tensor([0, 1, 2, 3, 1, 0], device=gpu), freqs_cis=freqs, pairing="interleaved")
+
+
+@pytest.mark.parametrize("tile", [True, False])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_rope_copies_equal_single_outputs(gpu, tile, out_dtype):
+    """kp_rope_bf16_twice (v5/ca76bd89ec38: the pair returned twice): both
+    copies hold exactly the bits of one kp_rope_bf16 call, for the tile
+    kernel (contiguous [B, S, H, 128]) and for the per-position kernel (a
+    head-strided view, one launch per copy); the copies are distinct
+    tensors."""
+    print(f"[rope copies] tile={tile} dtype={out_dtype}", flush=True)
+    g = gen(970 + tile + 2 * (out_dtype == torch.float32))
+    B, S, Hq, Hk, D, P = 1, 37, 8, 4, 128, 64
+    q = randn_bf16((B, S, Hq, D), g).to(gpu)
+    k = randn_bf16((B, S, Hk, D), g).to(gpu)
+    if not tile:
+        qw = torch.zeros((B, S, Hq, 2 * D), dtype=torch.bfloat16, device=gpu)
+        kw_ = torch.zeros((B, S, Hk, 2 * D), dtype=torch.bfloat16, device=gpu)
+        qw[..., :D] = q
+        kw_[..., :D] = k
+        q, k = qw[..., :D], kw_[..., :D]
+    pos = torch.randint(0, P, (B, S), generator=g).to(gpu)
+    freqs = torch.complex(torch.randn(P, D // 2, generator=g), torch.randn(P, D // 2, generator=g)).to(gpu)
+    kw = dict(positions=pos, freqs_cis=freqs, pairing="interleaved", q_dtype=out_dtype, k_dtype=out_dtype)
+    qo, ko = kp.rope(q, k, **kw)
+    q1, k1, q2, k2 = kp.rope(q, k, copies=True, **kw)
+    torch.cuda.synchronize()
+    for a in (q1, q2):
+        assert torch.equal(a, qo)
+    for a in (k1, k2):
+        assert torch.equal(a, ko)
+    assert q1.data_ptr() != q2.data_ptr() and k1.data_ptr() != k2.data_ptr()
+    qs, _, qs2, ks2 = kp.rope(q, None, copies=True, **kw)
+    torch.cuda.synchronize()
+    assert ks2 is None and torch.equal(qs, qo) and torch.equal(qs2, qo)
