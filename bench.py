@@ -874,6 +874,63 @@ def measure_probe(wl, steps, warmup):
             "us_by_schedule": {f"{k[0]}/{PROBE_POLICY_NAMES[k[1]]}": round(v * 1e3, 3) for k, v in per_tile.items()}}
 
 
+def measure_vendor(wl, steps, warmup):
+    """torch-ROCm's own elementwise kernels on the workload's byte mix, as a
+    ceiling written by someone else: 1 read + 1 write of equal size ->
+    copy_, 2 reads + 1 write -> add(out=), 3 reads + 1 write ->
+    addcmul(out=), a pure write (an fp32 table) -> zero_(); random bf16
+    inputs rotated past the Infinity Cache, each op timed by events on the
+    stream it runs on.  None for mixes with no single torch op."""
+    import torch
+    if wl.probe_mix is None:
+        return None
+    n_in, n_out, in_b, out_b, _ = wl.probe_mix
+    if n_out != 1:
+        return None
+    if in_b == out_b and n_in in (1, 2, 3):
+        op = {1: "copy_", 2: "add(out=)", 3: "addcmul(out=)"}[n_in]
+        per_set, numel = (n_in + 1) * in_b, in_b // 2
+    elif n_in == 1 and out_b > 8 * in_b:  # the embedding backward: the dense fp32 table dominates
+        op, per_set, numel = "zero_() of the fp32 output", out_b, out_b // 4
+    else:
+        return None
+    R = max(2, math.ceil(MIN_ROTATION_BYTES / per_set))
+    sets = []
+    for _ in range(R):
+        if op.startswith("zero_"):
+            sets.append((torch.empty(numel, dtype=torch.float32, device=wl.dev),))
+            continue
+        ins = [torch.empty(numel, dtype=torch.bfloat16, device=wl.dev).normal_() for _ in range(n_in)]
+        sets.append((torch.empty(numel, dtype=torch.bfloat16, device=wl.dev), *ins))
+
+    def launch(i):
+        t = sets[i % R]
+        if op.startswith("zero_"):
+            t[0].zero_()
+        elif n_in == 1:
+            t[0].copy_(t[1])
+        elif n_in == 2:
+            torch.add(t[1], t[2], out=t[0])
+        else:
+            torch.addcmul(t[1], t[2], t[3], out=t[0])
+
+    for i in range(warmup):
+        launch(i)
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    stops = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for i in range(steps):
+        starts[i].record()
+        launch(warmup + i)
+        stops[i].record()
+    torch.cuda.synchronize()
+    ms = sum(starts[i].elapsed_time(stops[i]) for i in range(steps)) / steps
+    del sets
+    torch.cuda.empty_cache()
+    return {"op": f"torch {op}", "us": round(ms * 1e3, 3), "bytes": per_set,
+            "GBps": round(per_set / (ms * 1e-3) / 1e9, 1), "frac_of_peak": round(per_set / (ms * 1e-3) / 1e9 / PEAK_GBS, 4)}
+
+
 def _tensors(x):
     return [t for y in x for t in _tensors(y)] if isinstance(x, (tuple, list)) else [x]
 
@@ -986,7 +1043,7 @@ def _ceiling_json(r):
     return {"GBps": round(c["GBps"], 1), "frac_of_peak": round(c["GBps"] / PEAK_GBS, 4), "probe_us": round(c["us"], 3),
             "probe_schedule": f"{c['chunks_per_thread']} chunk(s) per thread, {c['stores']} stores",
             "probe_us_by_schedule": c["us_by_schedule"], "mix": c["mix"],
-            "kernel_frac_of_ceiling": round(r["achieved"] / c["GBps"], 4)}
+            "kernel_frac_of_ceiling": round(r["achieved"] / c["GBps"], 4), "vendor": c.get("vendor")}
 
 
 def load_traffic(name):
@@ -1123,6 +1180,11 @@ def main():
             print(f"[bench] {name}: streaming ceiling of its mix ({c['mix']}): {c['us']:.1f} us at "
                   f"{c['chunks_per_thread']} chunk(s)/thread -> {c['GBps']:.0f} GB/s; "
                   f"dominant kernel at {r['achieved'] / c['GBps']:.1%} of it", file=sys.stderr, flush=True)
+            c["vendor"] = measure_vendor(wl, args.steps, args.warmup)
+            if c["vendor"]:
+                v = c["vendor"]
+                print(f"[bench] {name}: {v['op']} on the same mix: {v['us']:.1f} us -> {v['GBps']:.0f} GB/s",
+                      file=sys.stderr, flush=True)
         cpu = None
         if with_cpu:
             print(f"[bench] cpu baseline {name}", file=sys.stderr, flush=True)

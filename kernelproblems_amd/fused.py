@@ -2,7 +2,10 @@
 
 Each function validates its tensors (device, dtype, shapes), allocates the
 outputs and any workspace with torch's caching allocator, and enqueues the
-HIP kernels on the current stream of the input's device.  Nothing here
+HIP kernels on the current stream of the input's device.  rms_norm,
+rms_norm_backward, embedding, rope and rope_complex -- the entry points most
+fragments call -- do all of that in the native module _kp_torch
+(csrc/kp_torch.cpp), which halves their host time per call.  Nothing here
 computes on the CPU and nothing falls back to torch ops: a CPU tensor, an
 unsupported dtype or a missing library raises.
 
@@ -19,6 +22,23 @@ from typing import Optional, Sequence
 import torch
 
 from . import _lib as L
+
+_native_mod = None
+
+
+def _native():
+    """The native wrapper module (_kp_torch.so, built beside libkp_hip.so)."""
+    global _native_mod
+    if _native_mod is None:
+        try:
+            from . import _kp_torch
+        except ImportError as e:
+            raise RuntimeError(
+                f"kernelproblems_amd/_kp_torch.so is missing or does not load ({e}): build it with "
+                "`python -m kernelproblems_amd.build` (there is no CPU fallback)") from e
+        _native_mod = _kp_torch
+    return _native_mod
+
 
 _index_checking = os.environ.get("KP_CHECK_INDICES", "0") not in ("", "0")
 
@@ -151,37 +171,7 @@ def rms_norm(
     bf16(h * rstd * w), rstd = 1/sqrt(mean(h^2) + eps) over the trailing n
     elements.  Returns (h or None, y, rstd[M] or None); y has x_terms[0]'s shape.
     """
-    if not 1 <= len(x_terms) <= 3:
-        raise RuntimeError("rms_norm: 1..3 input terms")
-    x0 = x_terms[0]
-    _need_gpu("rms_norm input", x0)
-    shape, dev = x0.shape, x0.device
-    rows, strides, m = [], [], None
-    for i, t in enumerate(x_terms):
-        _need_gpu(f"rms_norm input {i}", t)
-        if t.numel() != x0.numel() or t.device != dev:
-            raise RuntimeError("rms_norm: input terms must have the same number of elements and device")
-        tt, rs, mm = _as_rows(t, n)
-        rows.append(tt)
-        strides.append(rs)
-        m = mm
-    w_t, seg_len, seg_stride = (None, n, n)
-    if weight is not None:
-        _need_gpu("rms_norm weight", weight)
-        w_t, seg_len, seg_stride = _weight_segments(weight, n)
-    y = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-    h = torch.empty(shape, dtype=torch.bfloat16, device=dev) if (return_h and len(x_terms) > 1) else None
-    rstd = torch.empty(m, dtype=torch.float32, device=dev) if return_rstd else None
-    L.call(
-        "kp_rmsnorm_fwd_bf16",
-        L.ptr_array([t.data_ptr() for t in rows]), L.i64_array(strides), len(rows),
-        _ptr(w_t), seg_len, seg_stride,
-        _ptr(h), n, y.data_ptr(), n, _ptr(rstd),
-        m, n, float(eps), _stream(dev),
-    )
-    if return_h and h is None:
-        h = x0
-    return h, y, rstd
+    return _native().rms_norm(x_terms, weight, float(eps), int(n), bool(return_h), bool(return_rstd))
 
 
 def _bwd_operands(who, dy_terms, x_terms, weight, n, dx_residual):
@@ -252,32 +242,8 @@ def rms_norm_backward(
     (fp32 sum), "f32_bf16" (the reference's bf16 rounding widened to fp32),
     "bf16", or None.  Returns (dx, dw).
     """
-    who = "rms_norm_backward"
-    dev, shape, m, dyr, dys, xr, xs, (w_t, seg_len, seg_stride), res_t, res_s = _bwd_operands(
-        who, dy_terms, x_terms, weight, n, dx_residual)
-    rstd_t = None
-    if rstd is not None:
-        _need_gpu(f"{who} rstd", rstd, torch.float32)
-        if rstd.numel() != m:
-            raise RuntimeError(f"{who}: rstd has {rstd.numel()} values, expected {m}")
-        rstd_t = rstd.contiguous()
-    dx = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-    dw_f32, dw_bf16 = _dw_outputs(who, dw, weight, n, dev)
-    ws_bytes = int(L.lib().kp_rmsnorm_bwd_workspace_size(m, n)) if dw is not None else 0
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev) if dw is not None else None
-    L.call(
-        "kp_rmsnorm_bwd_bf16",
-        L.ptr_array([t.data_ptr() for t in dyr]), L.i64_array(dys), len(dyr),
-        L.ptr_array([t.data_ptr() for t in xr]), L.i64_array(xs), len(xr),
-        _ptr(rstd_t), _ptr(w_t), seg_len, seg_stride,
-        _ptr(res_t), res_s, dx.data_ptr(), n,
-        _ptr(dw_f32), _ptr(dw_bf16), 1 if dw == "f32_bf16" else 0,
-        m, n, float(eps), _ptr(ws), ws_bytes, _stream(dev),
-    )
-    out_dw = dw_f32 if dw_f32 is not None else dw_bf16
-    if weight is not None and out_dw is not None:
-        out_dw = out_dw.view(weight.shape)
-    return (dx if want_dx else None), out_dw
+    return _native().rms_norm_backward(dy_terms, x_terms, rstd, weight, float(eps), int(n), dx_residual,
+                                       bool(want_dx), dw)
 
 
 def rms_norm_forward_backward(
@@ -340,19 +306,8 @@ def _index_info(indices: torch.Tensor):
 
 def embedding(table: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
     """out[..., :] = table[indices[...], :] (bit copy), shape indices.shape + [D]."""
-    _need_gpu("embedding weight", table)
-    if table.dim() != 2:
-        raise RuntimeError("embedding: weight must be 2-D")
-    idx, ib = _index_info(indices)
-    V, D = table.shape
-    tt, trs, _ = _as_rows(table, D)
-    out = torch.empty((*indices.shape, D), dtype=torch.bfloat16, device=table.device)
-    flag = _flag(table.device)
-    L.call(
-        "kp_embedding_fwd_bf16",
-        tt.data_ptr(), V, D, trs, idx.data_ptr(), ib, idx.numel(), out.data_ptr(), D,
-        _ptr(flag), _stream(table.device),
-    )
+    flag = _flag(table.device) if table.is_cuda else None
+    out = _native().embedding(table, indices, flag)
     _raise_if_flagged(flag, "embedding")
     return out
 
@@ -445,33 +400,7 @@ def embedding_dense_backward(
 
 
 # ---------------------------------------------------------------- RoPE
-def _rope_strides(t: torch.Tensor):
-    if t.dim() != 4:
-        raise RuntimeError(f"rope: expected [B, S, H, D], got shape {tuple(t.shape)}")
-    if t.shape[3] > 1 and t.stride(3) != 1:
-        t = t.contiguous()
-    return t, [t.stride(0), t.stride(1), t.stride(2)]
-
-
-def _positions(positions: Optional[torch.Tensor], B: int, S: int, dev):
-    """(pointer, bytes per id, stride over b, stride over s) of a [B, S],
-    [1, S] or [S] integer position tensor, or no positions (None)."""
-    if positions is None:
-        return None, 0, 0, 0
-    if positions.device != dev or positions.dtype not in (torch.int32, torch.int64):
-        raise RuntimeError("rope: positions must be an int32/int64 tensor on the same device")
-    if positions.dim() == 1:
-        if positions.shape[0] != S:
-            raise RuntimeError("rope: 1-D positions must have S entries")
-        psb, pss = 0, positions.stride(0)
-    elif positions.dim() == 2:
-        if positions.shape[1] != S or positions.shape[0] not in (1, B):
-            raise RuntimeError("rope: 2-D positions must be [B, S] or [1, S]")
-        psb = positions.stride(0) if positions.shape[0] == B else 0
-        pss = positions.stride(1)
-    else:
-        raise RuntimeError("rope: positions must be 1-D or 2-D")
-    return positions.data_ptr(), positions.element_size(), psb, pss
+_PAIRING = {"half": L.KP_ROPE_HALF, "interleaved": L.KP_ROPE_INTERLEAVED}
 
 
 def rope(
@@ -503,61 +432,14 @@ def rope(
     for dt in (q_dtype, k_dtype):
         if dt not in (torch.bfloat16, torch.float32):
             raise RuntimeError(f"rope: output dtype must be bfloat16 or float32, got {dt}")
-    _need_gpu("rope q", q)
-    dev = q.device
-    q, qs = _rope_strides(q)
-    B, S, Hq, D = q.shape
-    q_out = torch.empty((B, S, Hq, D), dtype=q_dtype, device=dev)
-    k_out = None
-    k_args = [None, None, 0, None, None]
-    if k is not None:
-        _need_gpu("rope k", k)
-        k, ks = _rope_strides(k)
-        if k.shape[0] != B or k.shape[1] != S or k.shape[3] != D:
-            raise RuntimeError("rope: q and k must agree on B, S and D")
-        k_out = torch.empty(k.shape, dtype=k_dtype, device=dev)
-        k_args = [k.data_ptr(), k_out.data_ptr(), k.shape[2], L.i64_array(ks),
-                  L.i64_array(list(k_out.stride()[:3]))]
-    pos_ptr, pos_bytes, psb, pss = _positions(positions, B, S, dev)
-    mode = {"half": L.KP_ROPE_HALF, "interleaved": L.KP_ROPE_INTERLEAVED}.get(pairing)
+    mode = _PAIRING.get(pairing)
     if mode is None:
         raise ValueError(f"rope: pairing must be 'half' or 'interleaved', got {pairing!r}")
-    f_ptr, frows, frs = None, 0, 0
-    th = 0.0
-    if freqs_cis is not None:
-        if freqs_cis.device != dev or freqs_cis.dtype != torch.complex64:
-            raise RuntimeError("rope: freqs_cis must be complex64 on the same device")
-        if freqs_cis.shape[-1] != D // 2:
-            raise RuntimeError(f"rope: freqs_cis last dim must be D/2={D // 2}")
-        fc, frs, frows = _as_rows(freqs_cis, D // 2)
-        f_ptr = torch.view_as_real(fc).data_ptr() if fc.numel() else fc.data_ptr()
-    else:
-        if theta is None or not (theta > 0) or not math.isfinite(theta):
-            raise RuntimeError("rope: need theta > 0 or freqs_cis")
-        th = float(theta)
-    flag = _flag(dev) if freqs_cis is not None else None
-    f32_mask = (1 if q_dtype == torch.float32 else 0) | (2 if k is not None and k_dtype == torch.float32 else 0)
-    if copies:
-        q_copy = torch.empty_like(q_out)
-        k_copy = torch.empty_like(k_out) if k_out is not None else None
-        L.call(
-            "kp_rope_bf16_twice",
-            q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(qs), L.i64_array(list(q_out.stride()[:3])),
-            *k_args,
-            B, S, D, pos_ptr, pos_bytes, psb, pss, mode, th, f_ptr, frows, frs, 1 if conj else 0, f32_mask,
-            q_copy.data_ptr(), _ptr(k_copy), _ptr(flag), _stream(dev),
-        )
-        _raise_if_flagged(flag, "rope")
-        return q_out, k_out, q_copy, k_copy
-    L.call(
-        "kp_rope_bf16",
-        q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(qs), L.i64_array(list(q_out.stride()[:3])),
-        *k_args,
-        B, S, D, pos_ptr, pos_bytes, psb, pss, mode, th, f_ptr, frows, frs, 1 if conj else 0, f32_mask,
-        _ptr(flag), _stream(dev),
-    )
+    flag = _flag(q.device) if (freqs_cis is not None and q.is_cuda) else None
+    out = _native().rope(q, k, positions, None if theta is None else float(theta), freqs_cis, mode, bool(conj),
+                         q_dtype == torch.float32, k_dtype == torch.float32, bool(copies), flag)
     _raise_if_flagged(flag, "rope")
-    return q_out, k_out
+    return out
 
 
 def rope_complex(q: torch.Tensor, k: Optional[torch.Tensor] = None, *, freqs_cis: torch.Tensor,
@@ -568,36 +450,10 @@ def rope_complex(q: torch.Tensor, k: Optional[torch.Tensor] = None, *, freqs_cis
     v1/075cb40f3d5d/problem.py:8-27.  positions: [B, S], [1, S] or [S]
     integers, default s.  conj=True multiplies by the conjugate table.
     Returns contiguous complex64 (q_out, k_out)."""
-    _need_gpu("rope_complex q", q, torch.complex64)
-    dev = q.device
-    if q.dim() != 4:
-        raise RuntimeError(f"rope_complex: expected [B, S, H, P], got shape {tuple(q.shape)}")
-    if q.shape[3] > 1 and q.stride(3) != 1:
-        q = q.contiguous()
-    B, S, Hq, P = q.shape
-    q_out = torch.empty(q.shape, dtype=torch.complex64, device=dev)
-    k_out = None
-    k_args = [None, None, 0, None, None]
-    if k is not None:
-        _need_gpu("rope_complex k", k, torch.complex64)
-        if k.dim() != 4 or k.shape[0] != B or k.shape[1] != S or k.shape[3] != P:
-            raise RuntimeError("rope_complex: q and k must agree on B, S and P")
-        if k.shape[3] > 1 and k.stride(3) != 1:
-            k = k.contiguous()
-        k_out = torch.empty(k.shape, dtype=torch.complex64, device=dev)
-        k_args = [k.data_ptr(), k_out.data_ptr(), k.shape[2], L.i64_array(list(k.stride()[:3])),
-                  L.i64_array(list(k_out.stride()[:3]))]
-    if freqs_cis.device != dev or freqs_cis.dtype != torch.complex64 or freqs_cis.shape[-1] != P:
-        raise RuntimeError(f"rope_complex: freqs_cis must be complex64 on the same device with last dim {P}")
-    fc, frs, frows = _as_rows(freqs_cis, P)
-    pos_ptr, pos_bytes, psb, pss = _positions(positions, B, S, dev)
-    flag = _flag(dev)
-    if B * S:
-        L.call("kp_rope_c64", q.data_ptr(), q_out.data_ptr(), Hq, L.i64_array(list(q.stride()[:3])),
-               L.i64_array(list(q_out.stride()[:3])), *k_args, B, S, P, pos_ptr, pos_bytes, psb, pss,
-               torch.view_as_real(fc).data_ptr(), frows, frs, 1 if conj else 0, _ptr(flag), _stream(dev))
+    flag = _flag(q.device) if q.is_cuda else None
+    out = _native().rope_complex(q, k, freqs_cis, positions, bool(conj), flag)
     _raise_if_flagged(flag, "rope_complex")
-    return q_out, k_out
+    return out
 
 
 # ---------------------------------------------------------------- FSDP unshard
