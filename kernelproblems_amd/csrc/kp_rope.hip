@@ -432,7 +432,9 @@ template <int PAIRING, bool TABLE>
 __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
   constexpr bool kHalf = PAIRING == KP_ROPE_HALF;
   constexpr int FPU = kHalf ? 8 : 4;  // angles per chunk
-  __shared__ float cs[TABLE ? 1 : kTileMaxPos][2][64];
+  // Theta mode: per position slot cos, s' = sc sin and -s' (sc = -1 for conj),
+  // so that no lane multiplies its sines by a sign.
+  __shared__ float cs[TABLE ? 1 : kTileMaxPos][3][64];
   const int lane = threadIdx.x & 63;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const bool second = blockIdx.x >= a.nb0;
@@ -458,8 +460,10 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     for (int i = threadIdx.x; i < npos * 64; i += kThreads) {
       float sn, cn;
       sincosf((float)tile_position(a, ps0 + (uint32_t)(i >> 6)) * inv, &sn, &cn);
+      const float sp = a.conj ? -sn : sn;
       cs[i >> 6][0][lane] = cn;
-      cs[i >> 6][1][lane] = sn;
+      cs[i >> 6][1][lane] = sp;
+      cs[i >> 6][2][lane] = -sp;
     }
     __syncthreads();
   }
@@ -491,10 +495,11 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
       }
     } else {
       const int slot = (int)(ps - ps0);
+      const int srow = (kHalf && lo) ? 2 : 1;  // the sign sgn below, taken from the table
 #pragma unroll
       for (int e = 0; e < FPU; e += 4) {
         const f32x4 cq = *reinterpret_cast<const f32x4*>(&cs[slot][0][f0 + e]);
-        const f32x4 sq = *reinterpret_cast<const f32x4*>(&cs[slot][1][f0 + e]);
+        const f32x4 sq = *reinterpret_cast<const f32x4*>(&cs[slot][srow][f0 + e]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           cv[e + j] = cq[j];
@@ -502,8 +507,10 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
         }
       }
     }
+    if constexpr (TABLE) {
 #pragma unroll
-    for (int e = 0; e < FPU; ++e) sv[e] = sgn * sv[e];
+      for (int e = 0; e < FPU; ++e) sv[e] = sgn * sv[e];
+    }
     float own[8], o[8];
     unpack8(v[u], own);
     if constexpr (kHalf) {

@@ -216,3 +216,21 @@ def test_rope_copies_equal_single_outputs(gpu, tile, out_dtype):
     qs, _, qs2, ks2 = kp.rope(q, None, copies=True, **kw)
     torch.cuda.synchronize()
     assert ks2 is None and torch.equal(qs, qo) and torch.equal(qs2, qo)
+
+
+def test_native_wrapper_raises_kperror_with_the_library_message(gpu):
+    """A status from the C ABI surfaces through the native wrappers as
+    KPError carrying the library's message (odd head dim: KP_EINVAL), and
+    the tensor checks raise RuntimeError before any launch."""
+    print("[native errors]", flush=True)
+    x = torch.zeros((1, 4, 2, 7), dtype=torch.bfloat16, device=gpu)
+    with pytest.raises(kp.KPError, match="kp_rope_bf16"):
+        kp.rope(x, theta=1e4)
+    with pytest.raises(RuntimeError, match="q and k must agree"):
+        kp.rope(torch.zeros((1, 4, 2, 8), dtype=torch.bfloat16, device=gpu),
+                torch.zeros((1, 5, 2, 8), dtype=torch.bfloat16, device=gpu), theta=1e4)
+    with pytest.raises(RuntimeError, match="freqs_cis last dim"):
+        kp.rope(torch.zeros((1, 4, 2, 8), dtype=torch.bfloat16, device=gpu),
+                freqs_cis=torch.zeros((4, 3), dtype=torch.complex64, device=gpu))
+    with pytest.raises(RuntimeError, match="rstd has 3 values, expected 4"):
+        kp.rms_norm_backward([x.view(4, 14)], [x.view(4, 14)], torch.zeros(3, device=gpu), None, 1e-5, 14, dw=None)

@@ -260,3 +260,23 @@ def test_bench_rejects_more_than_one_gpu():
     assert r.returncode == 2
     assert "measures one GPU" in r.stderr and "--gpus 2" in r.stderr
     assert r.stdout == ""
+
+
+def test_native_wrapper_module_loads():
+    """_kp_torch (csrc/kp_torch.cpp) is built beside libkp_hip.so and binds
+    the entry points fused.* routes through it; its checks raise the same
+    RuntimeError as the Python ones, before any device work."""
+    from kernelproblems_amd import fused as F
+
+    m = F._native()
+    for name in ("rms_norm", "rms_norm_backward", "embedding", "rope", "rope_complex"):
+        assert callable(getattr(m, name)), name
+    x = torch.zeros(4, 8, dtype=BF)
+    with pytest.raises(RuntimeError, match="1..3 input terms"):
+        kp.rms_norm([], None, 1e-5, 8)
+    with pytest.raises(RuntimeError, match="expected a GPU tensor, got device cpu"):
+        kp.rms_norm([x, x], None, 1e-5, 8)
+    with pytest.raises(RuntimeError, match="GPU tensor"):
+        kp.rope_complex(torch.zeros(1, 2, 1, 4, dtype=torch.complex64), freqs_cis=torch.zeros(2, 4, dtype=torch.complex64))
+    with pytest.raises(ValueError, match="pairing"):
+        kp.rope(torch.zeros(1, 2, 1, 8, dtype=BF), theta=1e4, pairing="diagonal")
