@@ -60,9 +60,7 @@ struct RopeArgs {
 // Output element offset o gets 8 values (16-byte bf16 / 32-byte fp32) or 1 value.
 __device__ __forceinline__ void store8p(void* out, int out_f32, int64_t o, const float* v) {
   if (out_f32) {
-    float* p = static_cast<float*>(out) + o;
-    st16f_stream(p, f32x4{v[0], v[1], v[2], v[3]});
-    st16f_stream(p + 4, f32x4{v[4], v[5], v[6], v[7]});
+    st32f(static_cast<float*>(out) + o, v);
   } else {
     st16_stream(static_cast<uint16_t*>(out) + o, pack8(v));
   }
@@ -534,14 +532,8 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     if (g <= glast) {
       const size_t e0 = ((size_t)g * 64 + lane) * 8;  // first element of this chunk
       if (T.out_f32) {  // block-uniform: the fp32 rotation result, 32 bytes per chunk
-        float* of = static_cast<float*>(T.out) + e0;
-        st16f_stream(of, f32x4{o[0], o[1], o[2], o[3]});
-        st16f_stream(of + 4, f32x4{o[4], o[5], o[6], o[7]});
-        if (T.out2) {
-          float* of2 = static_cast<float*>(T.out2) + e0;
-          st16f_stream(of2, f32x4{o[0], o[1], o[2], o[3]});
-          st16f_stream(of2 + 4, f32x4{o[4], o[5], o[6], o[7]});
-        }
+        st32f(static_cast<float*>(T.out) + e0, o);
+        if (T.out2) st32f(static_cast<float*>(T.out2) + e0, o);
       } else {
         const u32x4 pk = pack8(o);
         st16_stream(static_cast<uint16_t*>(T.out) + e0, pk);
