@@ -2,12 +2,13 @@
 
 Each function validates its tensors (device, dtype, shapes), allocates the
 outputs and any workspace with torch's caching allocator, and enqueues the
-HIP kernels on the current stream of the input's device.  rms_norm,
-rms_norm_backward, embedding, rope and rope_complex -- the entry points most
-fragments call -- do all of that in the native module _kp_torch
-(csrc/kp_torch.cpp), which halves their host time per call.  Nothing here
-computes on the CPU and nothing falls back to torch ops: a CPU tensor, an
-unsupported dtype or a missing library raises.
+HIP kernels on the current stream of the input's device -- all of it in one
+call into the native module _kp_torch (csrc/kp_torch.cpp), which calls the C
+ABI of libkp_hip.so: a call costs the kernel launches plus a few allocations
+of host time (about half of what the same work took through ctypes).  This
+module keeps the per-device out-of-range flag and the index-checking mode.
+Nothing here computes on the CPU and nothing falls back to torch ops: a CPU
+tensor, an unsupported dtype or a missing library raises.
 
 The aten-compatible drop-ins (``kernelproblems_amd.aten``) and the
 per-fragment ``kernel_function``s (``kernelproblems_amd.fragments``) are
@@ -15,7 +16,6 @@ thin compositions of these.
 """
 from __future__ import annotations
 
-import math
 import os
 from typing import Optional, Sequence
 
@@ -77,59 +77,6 @@ def check_indices() -> None:
 
 
 # ---------------------------------------------------------------- helpers
-def _stream(device: torch.device) -> int:
-    """The raw hipStream_t of the device's current torch stream (read without
-    building a Stream object: this runs on every call)."""
-    idx = device.index
-    return torch._C._cuda_getCurrentRawStream(idx if idx is not None else torch.cuda.current_device())
-
-
-def _need_gpu(name: str, t: torch.Tensor, dtype: Optional[torch.dtype] = torch.bfloat16) -> None:
-    if not isinstance(t, torch.Tensor):
-        raise TypeError(f"{name}: expected a tensor, got {type(t).__name__}")
-    if t.device.type != "cuda":
-        raise RuntimeError(f"{name}: expected a GPU tensor, got device {t.device} (no CPU path exists)")
-    if dtype is not None and t.dtype != dtype:
-        raise RuntimeError(f"{name}: expected dtype {dtype}, got {t.dtype}")
-
-
-def _as_rows(t: torch.Tensor, n: int):
-    """Returns (tensor, row_stride, rows) for t viewed as [rows, n] with unit
-    inner stride; copies to contiguous only if no such view exists."""
-    numel = t.numel()
-    if numel % n != 0:
-        raise RuntimeError(f"tensor of {numel} elements is not a whole number of rows of {n}")
-    m = numel // n
-    if m == 0:
-        return t, n, 0
-    if t.is_contiguous():
-        return t, n, m
-    try:
-        v = t.view(m, n)
-        if n == 1 or v.stride(1) == 1:
-            return t, v.stride(0), m
-    except RuntimeError:
-        pass
-    t = t.contiguous()
-    return t, n, m
-
-
-def _weight_segments(w: torch.Tensor, n: int):
-    """(tensor, seg_len, seg_stride): element i of the flattened weight sits at
-    (i // seg_len) * seg_stride + i % seg_len.  Covers contiguous vectors and
-    2-D row-strided views such as an [8, 512] slice of an FSDP flat buffer."""
-    if w.numel() != n:
-        raise RuntimeError(f"weight has {w.numel()} elements, expected {n}")
-    if w.dim() == 1 and (w.stride(0) == 1 or n == 1):
-        return w, n, n
-    if w.dim() == 2 and (w.stride(1) == 1 or w.shape[1] == 1):
-        return w, w.shape[1], w.stride(0)
-    if w.is_contiguous():
-        return w, n, n
-    w = w.contiguous()
-    return w, n, n
-
-
 def _flag(device: torch.device):
     """The device's persistent int32 out-of-range flag (allocated on first
     use; kernels only ever set it, check_indices() clears it).  In checking
@@ -151,10 +98,6 @@ def _raise_if_flagged(flag, what: str) -> None:
         raise IndexError(f"{what}: index out of range")
 
 
-def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
-    return None if t is None else t.data_ptr()
-
-
 # ---------------------------------------------------------------- RMSNorm
 def rms_norm(
     x_terms: Sequence[torch.Tensor],
@@ -172,54 +115,6 @@ def rms_norm(
     elements.  Returns (h or None, y, rstd[M] or None); y has x_terms[0]'s shape.
     """
     return _native().rms_norm(x_terms, weight, float(eps), int(n), bool(return_h), bool(return_rstd))
-
-
-def _bwd_operands(who, dy_terms, x_terms, weight, n, dx_residual):
-    """Row views of the backward's operands: (dev, x shape, M, dy rows,
-    dy strides, x rows, x strides, weight segments, residual rows, stride)."""
-    dy0 = dy_terms[0]
-    _need_gpu(f"{who} grad_out", dy0)
-    dev, shape = dy0.device, x_terms[0].shape
-    dyr, dys = [], []
-    m = None
-    for i, t in enumerate(dy_terms):
-        _need_gpu(f"{who} grad term {i}", t)
-        if t.numel() != dy0.numel():
-            raise RuntimeError(f"{who}: grad terms must have the same number of elements")
-        tt, rs, m = _as_rows(t, n)
-        dyr.append(tt)
-        dys.append(rs)
-    xr, xs = [], []
-    for i, t in enumerate(x_terms):
-        _need_gpu(f"{who} input term {i}", t)
-        if t.numel() != dy0.numel():
-            raise RuntimeError(f"{who}: input and grad must have the same number of elements")
-        tt, rs, _ = _as_rows(t, n)
-        xr.append(tt)
-        xs.append(rs)
-    w_seg = (None, n, n)
-    if weight is not None:
-        _need_gpu(f"{who} weight", weight)
-        w_seg = _weight_segments(weight, n)
-    res_t, res_s = None, n
-    if dx_residual is not None:
-        _need_gpu(f"{who} residual", dx_residual)
-        res_t, res_s, _ = _as_rows(dx_residual, n)
-    return dev, shape, m, dyr, dys, xr, xs, w_seg, res_t, res_s
-
-
-def _dw_outputs(who, dw, weight, n, dev):
-    dw_f32 = dw_bf16 = None
-    if dw is not None:
-        if weight is None:
-            raise RuntimeError(f"{who}: no weight, no weight gradient")
-        if dw in ("f32", "f32_bf16"):
-            dw_f32 = torch.empty(n, dtype=torch.float32, device=dev)
-        elif dw == "bf16":
-            dw_bf16 = torch.empty(n, dtype=torch.bfloat16, device=dev)
-        else:
-            raise ValueError(f"{who}: unknown dw mode {dw!r}")
-    return dw_f32, dw_bf16
 
 
 def rms_norm_backward(
@@ -266,44 +161,11 @@ def rms_norm_forward_backward(
     both y = bf16(x * rstd * w) and the backward (as rms_norm_backward with
     rstd=None).  Returns (y, dx, dw, h or None, rstd or None); y and dx have
     x_terms[0]'s shape, h is only produced for several x terms."""
-    who = "rms_norm_forward_backward"
-    dev, shape, m, dyr, dys, xr, xs, (w_t, seg_len, seg_stride), res_t, res_s = _bwd_operands(
-        who, dy_terms, x_terms, weight, n, dx_residual)
-    y = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-    dx = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-    h = torch.empty(shape, dtype=torch.bfloat16, device=dev) if (return_h and len(x_terms) > 1) else None
-    rstd = torch.empty(m, dtype=torch.float32, device=dev) if return_rstd else None
-    dw_f32, dw_bf16 = _dw_outputs(who, dw, weight, n, dev)
-    ws_bytes = int(L.lib().kp_rmsnorm_fwd_bwd_workspace_size(m, n))
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    L.call(
-        "kp_rmsnorm_fwd_bwd_bf16",
-        L.ptr_array([t.data_ptr() for t in dyr]), L.i64_array(dys), len(dyr),
-        L.ptr_array([t.data_ptr() for t in xr]), L.i64_array(xs), len(xr),
-        _ptr(w_t), seg_len, seg_stride,
-        _ptr(h), n, y.data_ptr(), n, _ptr(rstd),
-        _ptr(res_t), res_s, dx.data_ptr(), n,
-        _ptr(dw_f32), _ptr(dw_bf16), 1 if dw == "f32_bf16" else 0,
-        m, n, float(eps), ws.data_ptr(), ws_bytes, _stream(dev),
-    )
-    out_dw = dw_f32 if dw_f32 is not None else dw_bf16
-    if weight is not None and out_dw is not None:
-        out_dw = out_dw.view(weight.shape)
-    if return_h and h is None:
-        h = x_terms[0]
-    return y, dx, out_dw, h, rstd
+    return _native().rms_norm_forward_backward(dy_terms, x_terms, weight, float(eps), int(n), dx_residual, dw,
+                                               bool(return_h), bool(return_rstd))
 
 
 # ---------------------------------------------------------------- embedding
-def _index_info(indices: torch.Tensor):
-    if indices.device.type != "cuda":
-        raise RuntimeError(f"indices must be a GPU tensor, got {indices.device}")
-    if indices.dtype not in (torch.int64, torch.int32):
-        raise RuntimeError(f"indices must be int64 or int32, got {indices.dtype}")
-    idx = indices.contiguous()
-    return idx, idx.element_size()
-
-
 def embedding(table: torch.Tensor, indices: torch.Tensor) -> torch.Tensor:
     """out[..., :] = table[indices[...], :] (bit copy), shape indices.shape + [D]."""
     flag = _flag(table.device) if table.is_cuda else None
@@ -328,33 +190,10 @@ def embedding_rms_norm(
     view as in rms_norm.  Returns (h or None, y, rstd or None), shaped
     indices.shape + [D].  Row shapes without a fused kernel run the gather
     and the norm as two launches (same results)."""
-    _need_gpu("embedding_rms_norm table", table)
-    if table.dim() != 2:
-        raise RuntimeError("embedding_rms_norm: table must be 2-D")
-    idx, ib = _index_info(indices)
-    V, D = table.shape
-    dev = table.device
-    tt, trs, _ = _as_rows(table, D)
-    T = idx.numel()
-    y = torch.empty((*indices.shape, D), dtype=torch.bfloat16, device=dev)
-    h = torch.empty_like(y) if return_h else None
-    rstd = torch.empty(indices.shape, dtype=torch.float32, device=dev) if return_rstd else None
-    w_t, seg_len, seg_stride = (None, D, D)
-    if weight is not None:
-        _need_gpu("embedding_rms_norm weight", weight)
-        w_t, seg_len, seg_stride = _weight_segments(weight, D)
-    flag = _flag(dev)
-    st = L.lib().kp_embedding_rmsnorm_fwd_bf16(
-        tt.data_ptr(), V, trs, idx.data_ptr(), ib, T, _ptr(w_t), seg_len, seg_stride, _ptr(h), D, y.data_ptr(), D,
-        _ptr(rstd), D, float(eps), _ptr(flag), _stream(dev))
-    if st == L.KP_EUNSUPPORTED:
-        emb = embedding(table, indices)
-        _, y, r = rms_norm([emb], weight, eps, D, return_rstd=return_rstd)
-        return (emb if return_h else None), y, (r.view(indices.shape) if return_rstd else None)
-    if st != L.KP_OK:
-        raise L.KPError("kp_embedding_rmsnorm_fwd_bf16", st, L.lib().kp_last_error_message().decode())
+    flag = _flag(table.device) if table.is_cuda else None
+    out = _native().embedding_rms_norm(table, indices, weight, float(eps), bool(return_h), bool(return_rstd), flag)
     _raise_if_flagged(flag, "embedding_rms_norm")
-    return h, y, rstd
+    return out
 
 
 def embedding_dense_backward(
@@ -369,32 +208,12 @@ def embedding_dense_backward(
 ) -> torch.Tensor:
     """Dense [num_weights, D] gradient of an embedding, fp32 accumulation,
     deterministic sort-and-segment, every row written once."""
-    _need_gpu("embedding_dense_backward grad_output", grad_output)
-    idx, ib = _index_info(indices)
-    T = idx.numel()
-    D = grad_output.shape[-1]
-    if grad_output.numel() != T * D:
-        raise RuntimeError(
-            f"embedding_dense_backward: grad_output {tuple(grad_output.shape)} does not match {T} indices")
-    g, grs, _ = _as_rows(grad_output, D)
-    if out_dtype == torch.float32:
-        code = L.KP_DTYPE_F32
-    elif out_dtype == torch.bfloat16:
-        code = L.KP_DTYPE_BF16
-    else:
+    if out_dtype not in (torch.float32, torch.bfloat16):
         raise RuntimeError(f"embedding_dense_backward: unsupported out_dtype {out_dtype}")
-    dev = grad_output.device
-    out = torch.empty((num_weights, D), dtype=out_dtype, device=dev)
-    ws_bytes = int(L.lib().kp_embedding_bwd_workspace_size(T, num_weights, D))
-    ws = torch.empty(max(ws_bytes, 16), dtype=torch.uint8, device=dev)
-    flag = _flag(dev)
-    L.call(
-        "kp_embedding_bwd_bf16",
-        g.data_ptr(), grs, idx.data_ptr(), ib, T, num_weights, D,
-        -1 if padding_idx is None else int(padding_idx), 1 if scale_grad_by_freq else 0,
-        out.data_ptr(), code, 1 if round_to_bf16 else 0, ws.data_ptr(), ws_bytes,
-        _ptr(flag), _stream(dev),
-    )
+    flag = _flag(grad_output.device) if grad_output.is_cuda else None
+    out = _native().embedding_dense_backward(grad_output, indices, int(num_weights),
+                                             -1 if padding_idx is None else int(padding_idx), bool(scale_grad_by_freq),
+                                             out_dtype == torch.float32, bool(round_to_bf16), flag)
     _raise_if_flagged(flag, "embedding_dense_backward")
     return out
 
@@ -466,63 +285,16 @@ def unshard(flat: torch.Tensor, shards: int, split_sizes: Sequence[int], keep: S
     tensor -- the view -> split_with_sizes -> clone chain of an FSDP unshard,
     done for all kept segments in one launch.
     """
-    _need_gpu("unshard buffer", flat)
-    if flat.dim() == 1:
-        if flat.numel() % shards != 0:
-            raise RuntimeError(f"unshard: {flat.numel()} elements do not split into {shards} shards")
-        row_len = flat.numel() // shards
-        if flat.stride(0) != 1 and flat.numel() > 1:
-            flat = flat.contiguous()
-        stride = row_len
-    elif flat.dim() == 2 and flat.shape[0] == shards and (flat.stride(1) == 1 or flat.shape[1] == 1):
-        row_len, stride = flat.shape[1], flat.stride(0)
-    else:
-        raise RuntimeError(f"unshard: expected a 1-D buffer or a [{shards}, L] view, got {tuple(flat.shape)}")
-    if sum(split_sizes) != row_len:
-        raise RuntimeError(f"unshard: split sizes sum to {sum(split_sizes)}, shard row has {row_len}")
-    offs = [0]
-    for s in split_sizes:
-        offs.append(offs[-1] + s)
-    outs = [torch.empty((shards, split_sizes[i]), dtype=torch.bfloat16, device=flat.device) for i in keep]
-    for start in range(0, len(outs), 16):
-        sel = list(range(start, min(start + 16, len(outs))))
-        L.call(
-            "kp_unshard_bf16",
-            flat.data_ptr(), shards, stride,
-            L.i64_array([offs[keep[i]] for i in sel]), L.i64_array([split_sizes[keep[i]] for i in sel]),
-            L.ptr_array([outs[i].data_ptr() for i in sel]), len(sel), _stream(flat.device),
-        )
-    return outs
+    return _native().unshard(flat, int(shards), [int(v) for v in split_sizes], [int(i) for i in keep])
 
 
 # ---------------------------------------------------------------- SwiGLU gate
-def _same_rows(name: str, ts: Sequence[torch.Tensor]):
-    """Views of same-shape bf16 GPU tensors as [rows, N] (unit inner stride)."""
-    shape = ts[0].shape
-    for i, t in enumerate(ts):
-        _need_gpu(f"{name} operand {i}", t)
-        if t.numel() != ts[0].numel() or (t.dim() and t.shape[-1] != shape[-1]):
-            raise RuntimeError(f"{name}: operand {i} has shape {tuple(t.shape)}, expected {tuple(shape)}")
-        if t.device != ts[0].device:
-            raise RuntimeError(f"{name}: operands on different devices")
-    n = shape[-1] if len(shape) else 1
-    if n == 0 or ts[0].numel() == 0:
-        return [(t, max(n, 1), 0) for t in ts], n
-    return [_as_rows(t, n) for t in ts], n
-
-
 def swiglu(a: torch.Tensor, b: torch.Tensor) -> torch.Tensor:
     """bf16(bf16(silu(a)) * b): the silu -> mul region between the w1/w3 and
     w2 projections of a feed-forward block (v8/c68dae22972b/problem.py:15-28),
     fp32 arithmetic (silu = a / (1 + exp(-a))).  Returns a contiguous tensor
     of a's shape."""
-    (ra, rb), n = _same_rows("swiglu", [a, b])
-    out = torch.empty(a.shape, dtype=torch.bfloat16, device=a.device)
-    m = ra[2]
-    if m:
-        L.call("kp_swiglu_fwd_bf16", ra[0].data_ptr(), ra[1], rb[0].data_ptr(), rb[1], out.data_ptr(), n, m, n,
-               _stream(a.device))
-    return out
+    return _native().swiglu(a, b)
 
 
 def swiglu_backward(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.Tensor):
@@ -531,25 +303,13 @@ def swiglu_backward(g: torch.Tensor, s: torch.Tensor, b: torch.Tensor, a: torch.
     da = silu_backward(bf16(g * b), a) = t * sig * (1 + a * (1 - sig)).
     s is the recomputed silu(a) the graph keeps.  Returns contiguous
     (db, da) of g's shape."""
-    (rg, rs, rb, ra), n = _same_rows("swiglu_backward", [g, s, b, a])
-    db = torch.empty(g.shape, dtype=torch.bfloat16, device=g.device)
-    da = torch.empty(g.shape, dtype=torch.bfloat16, device=g.device)
-    m = rg[2]
-    if m:
-        L.call("kp_swiglu_bwd_bf16", rg[0].data_ptr(), rg[1], rs[0].data_ptr(), rs[1], rb[0].data_ptr(), rb[1],
-               ra[0].data_ptr(), ra[1], db.data_ptr(), n, da.data_ptr(), n, m, n, _stream(g.device))
-    return db, da
+    return _native().swiglu_backward(g, s, b, a)
 
 
 def silu(a: torch.Tensor) -> torch.Tensor:
     """bf16(silu(a)) alone (v7/58e7a4d6cde3/problem.py:10-19), the same bits as
     eager's bf16 silu.  Returns a contiguous tensor of a's shape."""
-    (ra,), n = _same_rows("silu", [a])
-    out = torch.empty(a.shape, dtype=torch.bfloat16, device=a.device)
-    m = ra[2]
-    if m:
-        L.call("kp_silu_bf16", ra[0].data_ptr(), ra[1], out.data_ptr(), n, m, n, _stream(a.device))
-    return out
+    return _native().silu(a)
 
 
 def swiglu_forward_backward(a: torch.Tensor, b: torch.Tensor, g: torch.Tensor):
@@ -557,29 +317,10 @@ def swiglu_forward_backward(a: torch.Tensor, b: torch.Tensor, g: torch.Tensor):
     (v6/182d2dcd0652/problem.py:10-46): with s = bf16(silu(a)) kept in
     registers, h = bf16(s * b), db = bf16(g * s) and
     da = silu_backward(bf16(g * b), a).  Returns contiguous (h, db, da)."""
-    (ra, rb, rg), n = _same_rows("swiglu_forward_backward", [a, b, g])
-    h, db, da = (torch.empty(a.shape, dtype=torch.bfloat16, device=a.device) for _ in range(3))
-    m = ra[2]
-    if m:
-        L.call("kp_swiglu_fwd_bwd_bf16", ra[0].data_ptr(), ra[1], rb[0].data_ptr(), rb[1], rg[0].data_ptr(), rg[1],
-               h.data_ptr(), n, db.data_ptr(), n, da.data_ptr(), n, m, n, _stream(a.device))
-    return h, db, da
+    return _native().swiglu_forward_backward(a, b, g)
 
 
 # ---------------------------------------------------------------- cross-entropy
-def _targets(targets: torch.Tensor, M: int, device: torch.device):
-    if not isinstance(targets, torch.Tensor) or targets.device != device:
-        raise RuntimeError("cross_entropy: targets must be a tensor on the logits' device")
-    if targets.dtype not in (torch.int64, torch.int32):
-        raise RuntimeError(f"cross_entropy: targets must be int64 or int32, got {targets.dtype}")
-    if targets.numel() != M:
-        raise RuntimeError(f"cross_entropy: {targets.numel()} targets for {M} rows")
-    t = targets.reshape(-1)
-    if M > 1 and t.stride(0) != 1:
-        t = t.contiguous()
-    return t, t.element_size()
-
-
 def cross_entropy_loss(logits: torch.Tensor, targets: torch.Tensor, *, ignore_index: int = -100, scale: float = 1.0,
                        return_lse: bool = False):
     """Summed token cross-entropy of bf16 logits [..., V] against integer
@@ -588,21 +329,10 @@ def cross_entropy_loss(logits: torch.Tensor, targets: torch.Tensor, *, ignore_in
     nll_loss_forward(reduction sum) -> div region of v8/71f1d2c9f38b/problem.py:15-40
     without materialising the log-softmax.  Returns 0-dim fp32 tensors
     (loss, total_weight) and, with return_lse, the fp32 per-row logsumexp."""
-    _need_gpu("cross_entropy logits", logits)
-    dev = logits.device
-    V = logits.shape[-1] if logits.dim() else 1
-    lt, rs, M = _as_rows(logits, V)
-    t, tb = _targets(targets, M, dev)
-    loss = torch.empty((), dtype=torch.float32, device=dev)
-    tw = torch.empty((), dtype=torch.float32, device=dev)
-    lse = torch.empty(logits.shape[:-1], dtype=torch.float32, device=dev) if return_lse else None
-    ws_bytes = int(L.lib().kp_cross_entropy_fwd_workspace_size(M))
-    ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
-    flag = _flag(dev)
-    L.call("kp_cross_entropy_fwd_bf16", lt.data_ptr(), rs, M, V, t.data_ptr(), tb, int(ignore_index), float(scale),
-           loss.data_ptr(), tw.data_ptr(), _ptr(lse), _ptr(flag), ws.data_ptr(), ws_bytes, _stream(dev))
+    flag = _flag(logits.device) if logits.is_cuda else None
+    out = _native().cross_entropy_loss(logits, targets, int(ignore_index), float(scale), bool(return_lse), flag)
     _raise_if_flagged(flag, "cross_entropy")
-    return (loss, tw, lse) if return_lse else (loss, tw)
+    return out
 
 
 def cross_entropy_forward_backward(logits: torch.Tensor, targets: torch.Tensor, grad_loss: float, *,
@@ -617,30 +347,11 @@ def cross_entropy_forward_backward(logits: torch.Tensor, targets: torch.Tensor, 
     cross_entropy_loss(..., scale=scale) computes them.  in_place=True writes
     the gradient over the logits (which must then be contiguous) and
     returns them."""
-    _need_gpu("cross_entropy logits", logits)
-    dev = logits.device
-    V = logits.shape[-1] if logits.dim() else 1
-    lt, rs, M = _as_rows(logits, V)
-    t, tb = _targets(targets, M, dev)
-    if in_place:
-        if not logits.is_contiguous():
-            raise RuntimeError("cross_entropy_forward_backward: in_place needs contiguous logits")
-        out = logits
-    else:
-        out = torch.empty(logits.shape, dtype=torch.bfloat16, device=dev)
-    loss = tw = None
-    ws, ws_bytes = None, 0
-    if return_loss:
-        loss = torch.empty((), dtype=torch.float32, device=dev)
-        tw = torch.empty((), dtype=torch.float32, device=dev)
-        ws_bytes = int(L.lib().kp_cross_entropy_fwd_workspace_size(M))
-        ws = torch.empty(max(ws_bytes, 8), dtype=torch.uint8, device=dev)
-    flag = _flag(dev)
-    L.call("kp_cross_entropy_fwd_bwd_bf16", lt.data_ptr(), rs, M, V, t.data_ptr(), tb, int(ignore_index),
-           float(grad_loss), out.data_ptr(), V, float(scale), _ptr(loss), _ptr(tw), _ptr(flag), _ptr(ws), ws_bytes,
-           _stream(dev))
+    flag = _flag(logits.device) if logits.is_cuda else None
+    out = _native().cross_entropy_forward_backward(logits, targets, float(grad_loss), int(ignore_index), float(scale),
+                                                   bool(return_loss), bool(in_place), flag)
     _raise_if_flagged(flag, "cross_entropy_forward_backward")
-    return (out, loss, tw) if return_loss else out
+    return out
 
 
 def cross_entropy_backward(log_softmax: torch.Tensor, targets: torch.Tensor, grad_loss: float, *,
@@ -652,15 +363,7 @@ def cross_entropy_backward(log_softmax: torch.Tensor, targets: torch.Tensor, gra
     _log_softmax_backward_data -> _to_copy(bf16)).  grad_loss is the
     upstream gradient of the loss as a Python float (a constant in the
     fragment: 1 / 8192).  Returns a contiguous bf16 tensor of L's shape."""
-    _need_gpu("cross_entropy log_softmax", log_softmax, torch.float32)
-    dev = log_softmax.device
-    V = log_softmax.shape[-1] if log_softmax.dim() else 1
-    lt, rs, M = _as_rows(log_softmax, V)
-    t, tb = _targets(targets, M, dev)
-    out = torch.empty(log_softmax.shape, dtype=torch.bfloat16, device=dev)
-    flag = _flag(dev)
-    if M:
-        L.call("kp_cross_entropy_bwd_bf16", lt.data_ptr(), rs, t.data_ptr(), tb, int(ignore_index), float(grad_loss),
-               out.data_ptr(), V, M, V, _ptr(flag), _stream(dev))
+    flag = _flag(log_softmax.device) if log_softmax.is_cuda else None
+    out = _native().cross_entropy_backward(log_softmax, targets, float(grad_loss), int(ignore_index), flag)
     _raise_if_flagged(flag, "cross_entropy_backward")
     return out

@@ -264,12 +264,15 @@ def test_bench_rejects_more_than_one_gpu():
 
 def test_native_wrapper_module_loads():
     """_kp_torch (csrc/kp_torch.cpp) is built beside libkp_hip.so and binds
-    the entry points fused.* routes through it; its checks raise the same
-    RuntimeError as the Python ones, before any device work."""
+    every tensor-level entry point of fused.*; its checks raise RuntimeError
+    (ValueError for a bad option) before any device work."""
     from kernelproblems_amd import fused as F
 
     m = F._native()
-    for name in ("rms_norm", "rms_norm_backward", "embedding", "rope", "rope_complex"):
+    for name in ("rms_norm", "rms_norm_backward", "rms_norm_forward_backward", "embedding", "embedding_rms_norm",
+                 "embedding_dense_backward", "rope", "rope_complex", "unshard", "swiglu", "swiglu_backward", "silu",
+                 "swiglu_forward_backward", "cross_entropy_loss", "cross_entropy_forward_backward",
+                 "cross_entropy_backward"):
         assert callable(getattr(m, name)), name
     x = torch.zeros(4, 8, dtype=BF)
     with pytest.raises(RuntimeError, match="1..3 input terms"):
