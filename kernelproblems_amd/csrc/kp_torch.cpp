@@ -72,6 +72,11 @@ void* stream_of(const Tensor& t) { return c10::hip::getCurrentHIPStream(t.device
 
 void* ptr(const Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
 
+// The caller's per-device out-of-range flag (int32), if any.
+int32_t* flag_ptr(const std::optional<Tensor>& flag) {
+  return flag ? static_cast<int32_t*>(flag->data_ptr()) : nullptr;
+}
+
 // t viewed as [m, n] rows with unit inner stride: (tensor, row stride, m);
 // copies to contiguous only when no such view exists.
 struct Rows {
@@ -300,7 +305,7 @@ Tensor embedding(const Tensor& table, const Tensor& indices, const std::optional
   Tensor out = at::empty(shape, table.options().dtype(at::kBFloat16));
   check("kp_embedding_fwd_bf16",
         kp_embedding_fwd_bf16(t.t.data_ptr(), V, D, t.stride, idx.data_ptr(), ib, idx.numel(), out.data_ptr(), D,
-                              flag ? static_cast<int32_t*>(flag->data_ptr()) : nullptr, stream_of(table)));
+                              flag_ptr(flag), stream_of(table)));
   return out;
 }
 
@@ -327,7 +332,7 @@ py::tuple embedding_rms_norm(const Tensor& table, const Tensor& indices, const s
   }
   const int st = kp_embedding_rmsnorm_fwd_bf16(t.t.data_ptr(), V, t.stride, idx.data_ptr(), ib, T, ptr(ws.w), ws.len,
                                                ws.stride, ptr(h), D, y.data_ptr(), D, static_cast<float*>(ptr(rstd)), D,
-                                               (float)eps, flag ? static_cast<int32_t*>(flag->data_ptr()) : nullptr,
+                                               (float)eps, flag_ptr(flag),
                                                stream_of(table));
   if (st == KP_EUNSUPPORTED) {  // no fused kernel for this row shape: the gather, then the norm
     Tensor emb = embedding(table, indices, flag);
@@ -359,7 +364,7 @@ Tensor embedding_dense_backward(const Tensor& grad_output, const Tensor& indices
         kp_embedding_bwd_bf16(g.t.data_ptr(), g.stride, idx.data_ptr(), ib, T, num_weights, D, padding_idx,
                               scale_grad_by_freq ? 1 : 0, out.data_ptr(), out_f32 ? KP_DTYPE_F32 : KP_DTYPE_BF16,
                               round_to_bf16 ? 1 : 0, wsp.data_ptr(), ws_bytes,
-                              flag ? static_cast<int32_t*>(flag->data_ptr()) : nullptr, stream_of(grad_output)));
+                              flag_ptr(flag), stream_of(grad_output)));
   return out;
 }
 
@@ -485,10 +490,6 @@ Tensor targets_of(const py::object& targets, int64_t M, const at::Device& dev, i
   if (M > 1 && t.stride(0) != 1) t = t.contiguous();
   tb = (int)t.element_size();
   return t;
-}
-
-int32_t* flag_ptr(const std::optional<Tensor>& flag) {
-  return flag ? static_cast<int32_t*>(flag->data_ptr()) : nullptr;
 }
 
 py::tuple cross_entropy_loss(const Tensor& logits, const py::object& targets, int64_t ignore_index, double scale,
@@ -646,7 +647,7 @@ py::tuple rope(Tensor q, std::optional<Tensor> k, const std::optional<Tensor>& p
   if (k_out.defined())
     for (int i = 0; i < 3; ++i) kos[i] = k_out.stride(i);
   const int mask = (q_f32 ? 1 : 0) | (k_out.defined() && k_f32 ? 2 : 0);
-  int32_t* fl = flag ? static_cast<int32_t*>(flag->data_ptr()) : nullptr;
+  int32_t* fl = flag_ptr(flag);
   void* s = stream_of(q);
   if (copies) {
     Tensor q_copy = at::empty_like(q_out);
@@ -699,7 +700,7 @@ py::tuple rope_complex(Tensor q, std::optional<Tensor> k, const Tensor& freqs_ci
           kp_rope_c64(q.data_ptr(), q_out.data_ptr(), Hq, qs, qos, ptr(kk), ptr(k_out), kk.defined() ? kk.size(2) : 0,
                       kk.defined() ? ks : nullptr, k_out.defined() ? kos : nullptr, B, S, P, pos.p, pos.bytes, pos.sb,
                       pos.ss, static_cast<const float*>(f.t.data_ptr()), f.m, f.stride, conj ? 1 : 0,
-                      flag ? static_cast<int32_t*>(flag->data_ptr()) : nullptr, stream_of(q)));
+                      flag_ptr(flag), stream_of(q)));
   }
   return py::make_tuple(q_out, opt(k_out));
 }
