@@ -418,12 +418,25 @@ struct TileArgs {
   float inv_freq[64];
 };
 
-// Position id of flattened position ps = b S + s (ps < 2^31).
-__device__ __forceinline__ int64_t tile_position(const TileArgs& a, uint32_t ps) {
+// Position id of flattened position ps = b S + s (ps < 2^31), in two steps so
+// that its load can be issued early and waited for late: tile_pos_words
+// loads the id's 32-bit words without a branch on the id type (an int32 id
+// loads its one word twice) and without using them; tile_pos_value builds
+// the id from them.  Without a position tensor the id is s itself.
+struct PosWords {
+  uint32_t lo, hi;
+};
+__device__ __forceinline__ PosWords tile_pos_words(const TileArgs& a, uint32_t ps) {
+  if (a.pos == nullptr) return PosWords{0u, 0u};
   const uint32_t b = div32(ps, a.S), s = ps - b * a.S.d;
-  if (a.pos == nullptr) return s;
   const int64_t i = (int64_t)b * a.psb + (int64_t)s * a.pss;
-  return a.pb == 8 ? static_cast<const int64_t*>(a.pos)[i] : (int64_t) static_cast<const int32_t*>(a.pos)[i];
+  const bool wide = a.pb == 8;
+  const uint32_t* w = static_cast<const uint32_t*>(a.pos) + (wide ? 2 * i : i);
+  return PosWords{w[0], w[wide ? 1 : 0]};
+}
+__device__ __forceinline__ int64_t tile_pos_value(const TileArgs& a, PosWords w, uint32_t ps) {
+  if (a.pos == nullptr) return ps - div32(ps, a.S) * a.S.d;
+  return a.pb == 8 ? (int64_t)(((uint64_t)w.hi << 32) | w.lo) : (int64_t)(int32_t)w.lo;
 }
 
 template <int PAIRING, bool TABLE>
@@ -439,8 +452,31 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
   const TileTensor& T = a.t[second ? 1 : 0];
   const uint32_t g0 = (second ? blockIdx.x - a.nb0 : blockIdx.x) * kTileGroups;
   const uint32_t glast = T.groups - 1;
+  // Theta mode: everything the angles depend on -- the inverse frequency and
+  // the position ids of this thread's angle slots (vector loads) -- is
+  // requested before the data: vector loads complete in issue order, so
+  // waiting for these is not waiting for the data, and the sincos and the
+  // barrier overlap the data's latency instead of following it (c4: ids
+  // requested after the data cost ~2.5 us per call).
+  const uint32_t ps0 = div32(g0, T.gpp);
   float inv = 0.f;
-  if constexpr (!TABLE) inv = a.inv_freq[lane];  // requested before the data: its wait is not the data's
+  int npos = 0;
+  // theta: the positions of angle items t and t + 256 (slot clamped to the
+  // block's last, whose id is then unused); table: those of groups u = 0, 1
+  uint32_t pps[2];
+  PosWords pw[2];
+  if constexpr (!TABLE) {
+    inv = a.inv_freq[lane];
+    const uint32_t gl = g0 + kTileGroups - 1 < glast ? g0 + kTileGroups - 1 : glast;
+    npos = (int)(div32(gl, T.gpp) - ps0) + 1;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int slot = ((int)threadIdx.x + k * kThreads) >> 6;  // npos * 64 <= 2 * kThreads
+      pps[k] = ps0 + (uint32_t)(slot < npos ? slot : npos - 1);
+    }
+#pragma unroll
+    for (int k = 0; k < 2; ++k) pw[k] = tile_pos_words(a, pps[k]);
+  }
   __builtin_amdgcn_sched_barrier(0);
   // Groups past the tensor's end (last tile only) re-read the last group and store nothing.
   u32x4 v[2];
@@ -450,18 +486,29 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     v[u] = ld16_stream(T.x + ((size_t)(g < glast ? g : glast) * 64 + lane) * 8);
   }
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (TABLE) {
+    // table mode: a group's id is wave-uniform, a scalar load whose wait
+    // (lgkmcnt) is independent of the data's (vmcnt), so it follows the data
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const uint32_t g = g0 + wave + 4 * u;
+      pps[u] = div32(g < glast ? g : glast, T.gpp);
+      pw[u] = tile_pos_words(a, pps[u]);
+    }
+  }
 
-  const uint32_t ps0 = div32(g0, T.gpp);
   if constexpr (!TABLE) {
-    const uint32_t gl = g0 + kTileGroups - 1 < glast ? g0 + kTileGroups - 1 : glast;
-    const int npos = (int)(div32(gl, T.gpp) - ps0) + 1;
-    for (int i = threadIdx.x; i < npos * 64; i += kThreads) {
-      float sn, cn;
-      sincosf((float)tile_position(a, ps0 + (uint32_t)(i >> 6)) * inv, &sn, &cn);
-      const float sp = a.conj ? -sn : sn;
-      cs[i >> 6][0][lane] = cn;
-      cs[i >> 6][1][lane] = sp;
-      cs[i >> 6][2][lane] = -sp;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int i = (int)threadIdx.x + k * kThreads;
+      if (i < npos * 64) {
+        float sn, cn;
+        sincosf((float)tile_pos_value(a, pw[k], pps[k]) * inv, &sn, &cn);
+        const float sp = a.conj ? -sn : sn;
+        cs[i >> 6][0][lane] = cn;
+        cs[i >> 6][1][lane] = sp;
+        cs[i >> 6][2][lane] = -sp;
+      }
     }
     __syncthreads();
   }
@@ -479,7 +526,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     float cv[FPU], sv[FPU];
     bool ok = true;
     if constexpr (TABLE) {
-      const int64_t p = tile_position(a, ps);
+      const int64_t p = tile_pos_value(a, pw[u], pps[u]);
       ok = p >= 0 && p < a.frows;
       if (!ok && lane == 0 && a.err) *a.err = 1;
       const float* frow = a.freqs + 2 * ((ok ? p : 0) * a.frs + f0);
