@@ -146,3 +146,41 @@ def test_rmsnorm_empty_rows(gpu):
     assert y.shape == (0, 4096) and r.shape == (0,)
     dx, dw = kp.rms_norm_backward([x], [x], None, w, 1e-6, 4096)
     assert dx.shape == (0, 4096) and torch.count_nonzero(dw) == 0
+
+
+def test_row_layouts_give_the_contiguous_bits(gpu):
+    """The wrappers' row-layout rules (kp_torch.cpp as_rows): a padded row
+    stride and a 3-D view whose rows share one stride are read in place; a
+    transposed tensor (no [M, N] view with unit inner stride) is copied
+    first.  Every layout gives exactly the contiguous input's y, rstd, dx
+    and dw bits."""
+    print("[rms layouts]", flush=True)
+    g = gen(4242)
+    M, N = 64, 1024
+    x = randn_bf16((M, N), g).to(gpu)
+    dy = randn_bf16((M, N), g).to(gpu)
+    w = randn_bf16(N, g, 1.0, 0.02).to(gpu)
+    _, y0, r0 = kp.rms_norm([x], w, 1e-6, N)
+    dx0, dw0 = kp.rms_norm_backward([dy], [x], None, w, 1e-6, N)
+
+    def padded(t):
+        buf = torch.zeros((M, N + 64), dtype=t.dtype, device=gpu)
+        buf[:, :N] = t
+        return buf[:, :N]
+
+    def batched(t):  # [2, M/2, N] view of a [2, M/2, N + 128] buffer: one uniform row stride
+        buf = torch.zeros((2, M // 2, N + 128), dtype=t.dtype, device=gpu)
+        buf[:, :, :N] = t.view(2, M // 2, N)
+        return buf[:, :, :N]
+
+    def transposed(t):  # the same values, stored column-major
+        return t.t().contiguous().t()
+
+    for name, f in (("padded", padded), ("batched", batched), ("transposed", transposed)):
+        xv, dyv = f(x), f(dy)
+        _, y, r = kp.rms_norm([xv], w, 1e-6, N)
+        dx, dw = kp.rms_norm_backward([dyv], [xv], None, w, 1e-6, N)
+        torch.cuda.synchronize()
+        assert y.shape == xv.shape and dx.shape == xv.shape, name
+        assert torch.equal(y.reshape(M, N), y0) and torch.equal(r, r0), name
+        assert torch.equal(dx.reshape(M, N), dx0) and torch.equal(dw, dw0), name
