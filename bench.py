@@ -738,25 +738,31 @@ CONFIGS = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
 
 # ------------------------------------------------------------------ measure
 def measure_gpu(wl, steps, warmup):
-    """Two passes over the same K steps: the timed pass (wall clock and HIP
-    events around the whole loop, no per-kernel hooks) gives value and
-    ms_per_step; a second pass with the timing hook set gives the dominant
-    kernel's per-launch durations (events stamped at its own start / end)."""
+    """Three passes over K steps: the timed pass (wall clock between two
+    synchronisations, nothing else inside: recording even two HIP events in
+    it cost ~1-2 us per call at K = 20) gives value and ms_per_step; a
+    second pass with HIP events around the loop gives the GPU time per step;
+    a third with the timing hook set gives the dominant kernel's per-launch
+    durations (events stamped at its own start / end)."""
     import torch
     from kernelproblems_amd import _lib as L
     lib = L.lib()
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    for i in range(steps):
+        wl.step(warmup + i)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+
     t0e, t1e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
-    w0 = time.perf_counter()
     t0e.record()
     for i in range(steps):
         wl.step(warmup + i)
     t1e.record()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
     gpu_ms = t0e.elapsed_time(t1e)
 
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
