@@ -737,6 +737,21 @@ CONFIGS = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
 
 
 # ------------------------------------------------------------------ measure
+def warm_device(dev):
+    """~5 ms of plain device fills (32 x 1 GiB) before a workload's warmup
+    steps.  After an idle stretch (workload set-up, a CPU baseline) the
+    memory system needs a few ms of sustained traffic before it runs at full
+    rate; five warmup steps of a short call do not supply it, and the first
+    timed pass then runs slow (c3b: ~367 against ~355 us per call at K = 20,
+    the later passes ~355 either way).  Nothing of the workload runs here."""
+    import torch
+    buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    for _ in range(32):
+        buf.zero_()
+    torch.cuda.synchronize()
+    del buf
+
+
 def measure_gpu(wl, steps, warmup):
     """Three passes over K steps: the timed pass (wall clock between two
     synchronisations, nothing else inside: recording even two HIP events in
@@ -747,6 +762,7 @@ def measure_gpu(wl, steps, warmup):
     import torch
     from kernelproblems_amd import _lib as L
     lib = L.lib()
+    warm_device(wl.dev)
     for i in range(warmup):
         wl.step(i)
     torch.cuda.synchronize()
