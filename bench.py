@@ -738,18 +738,19 @@ CONFIGS = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
 
 # ------------------------------------------------------------------ measure
 def warm_device(dev):
-    """~5 ms of plain device fills (32 x 1 GiB) before a workload's warmup
+    """~5 ms of plain device copies (16 x 1 GiB) before a workload's warmup
     steps.  After an idle stretch (workload set-up, a CPU baseline) the
     memory system needs a few ms of sustained traffic before it runs at full
     rate; five warmup steps of a short call do not supply it, and the first
     timed pass then runs slow (c3b: ~367 against ~355 us per call at K = 20,
     the later passes ~355 either way).  Nothing of the workload runs here."""
     import torch
-    buf = torch.empty(1 << 28, dtype=torch.float32, device=dev)
-    for _ in range(32):
-        buf.zero_()
+    src = torch.empty(1 << 28, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(16):
+        dst.copy_(src)
     torch.cuda.synchronize()
-    del buf
+    del src, dst
 
 
 def measure_gpu(wl, steps, warmup):
