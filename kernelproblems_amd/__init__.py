@@ -7,6 +7,8 @@ vocabulary cross-entropy loss forward/backward.
 Layers:
   * ``include/kp.h`` + ``csrc/*.hip``  -- the C ABI and the HIP kernels;
   * ``_lib``      -- ctypes binding of ``libkp_hip.so`` (no fallback path);
+  * ``_kp_torch`` -- native torch extension (``csrc/kp_torch.cpp``): the
+    bodies of the tensor-level operations, calling the C ABI;
   * ``fused``     -- tensor-level fused operations over the C ABI;
   * ``aten``      -- drop-ins for the aten operators used by the fragments;
   * ``fragments`` -- ``kernel_function`` drop-ins for individual reference
