@@ -68,7 +68,17 @@ void need_gpu(const std::string& name, const Tensor& t, std::optional<at::Scalar
     fail(name + ": expected dtype " + dtype_name(*dt) + ", got " + dtype_name(t.scalar_type()));
 }
 
-void* stream_of(const Tensor& t) { return c10::hip::getCurrentHIPStream(t.device().index()).stream(); }
+// The tensor's device made current (HIP launches on the current device) and
+// that device's current stream.  Passed as a temporary in a C call's argument
+// list, so the device stays current until the call returns.
+struct DeviceStream {
+  c10::DeviceGuard guard;
+  void* stream;
+  explicit DeviceStream(const Tensor& t)
+      : guard(t.device()), stream(c10::hip::getCurrentHIPStream(t.device().index()).stream()) {}
+  operator void*() const { return stream; }
+};
+DeviceStream stream_of(const Tensor& t) { return DeviceStream(t); }
 
 void* ptr(const Tensor& t) { return t.defined() ? t.data_ptr() : nullptr; }
 
@@ -648,7 +658,7 @@ py::tuple rope(Tensor q, std::optional<Tensor> k, const std::optional<Tensor>& p
     for (int i = 0; i < 3; ++i) kos[i] = k_out.stride(i);
   const int mask = (q_f32 ? 1 : 0) | (k_out.defined() && k_f32 ? 2 : 0);
   int32_t* fl = flag_ptr(flag);
-  void* s = stream_of(q);
+  const DeviceStream s = stream_of(q);  // the device stays current to the end of the function
   if (copies) {
     Tensor q_copy = at::empty_like(q_out);
     Tensor k_copy = k_out.defined() ? at::empty_like(k_out) : Tensor();
