@@ -9,8 +9,8 @@ in the top-level fields and one block per configuration under "configs",
 each with its whole-call rate, roofline (dominant kernel), traffic, CPU
 baseline and the tensor-level drop-in's time per call.  When --steps is
 below 100, each block also carries a "steady" pass of 100 calls: the timed
-loop's fixed cost (first launch, closing synchronisation; ~20 us) spread over
-few steps inflates the per-call time of the small configurations.
+loop's fixed cost (first launch, closing synchronisation) spread over few
+steps inflates the per-call time of the small configurations.
 
 A step is one call of the fragment (one pass of the hot path over one batch
 of synthetic input, already resident in HBM).  Workloads are the
@@ -38,10 +38,12 @@ BASELINE.json configurations:
 Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 ~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
 find its operands in cache from the previous call.  The timed loop calls the
-C ABI directly through pre-bound ctypes arguments.  value = algorithmic
-bytes per call * steps / wall time of the timed loop (synchronised on both
-sides, no per-kernel instrumentation inside).  roofline.achieved = the
-dominant kernel's algorithmic bytes / its mean duration, from a second pass
+C ABI directly through pre-bound ctypes arguments, after ~5 ms of plain
+device copies (no part of the workload) and the W warmup steps.  value =
+algorithmic bytes per call * steps / wall time of the timed loop
+(synchronised on both sides, no instrumentation inside; the GPU time per
+step comes from a separate pass with HIP events).  roofline.achieved = the
+dominant kernel's algorithmic bytes / its mean duration, from a third pass
 over K steps with HIP events that the library has the runtime stamp at that
 kernel's own start and completion (kp_profile_dominant_kernel ->
 hipExtLaunchKernel), on the stream the kernel runs on.  roofline.ceiling is
