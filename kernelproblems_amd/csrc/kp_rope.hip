@@ -388,9 +388,10 @@ __global__ __launch_bounds__(kThreads) void rope_fast(RopeArgs a) {
 // (row_ror:8); interleaved pairs are the 4 (2i, 2i+1) pairs inside a chunk.
 // Theta mode evaluates the (cos, sin) of the tile's (at most 8) positions
 // once per block (threads f, f + 64, ... of position slot i / 64) into LDS
-// behind one barrier; table mode reads the position's row of the table
-// (L2-resident).  Arithmetic, rounding and angles are those of rope_fast, so
-// both give identical bits.
+// behind one barrier; rotate-half table mode copies the positions' table
+// rows there the same way; interleaved table mode reads the position's row
+// (L2-resident) per chunk.  Arithmetic, rounding and angles are those of
+// rope_fast, so both give identical bits.
 constexpr int kTileChunks = 2 * kThreads;
 constexpr int kTileGroups = kTileChunks / 64;  // 8
 constexpr int kTileMaxPos = kTileGroups;       // a position is >= 1 group
@@ -443,39 +444,44 @@ template <int PAIRING, bool TABLE>
 __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
   constexpr bool kHalf = PAIRING == KP_ROPE_HALF;
   constexpr int FPU = kHalf ? 8 : 4;  // angles per chunk
-  // Theta mode: per position slot cos, s' = sc sin and -s' (sc = -1 for conj),
-  // so that no lane multiplies its sines by a sign.
-  __shared__ float cs[TABLE ? 1 : kTileMaxPos][3][64];
+  // kStage: the block's angles go through LDS -- per position slot cos,
+  // s' = sc sin and -s' (sc = -1 for conj), so that no lane multiplies its
+  // sines by a sign -- evaluated in theta mode, copied from the table row in
+  // rotate-half table mode (with the slot's validity).  Interleaved table
+  // mode reads its 4 angles per chunk straight from the row (2 x 16 bytes,
+  // an L2 hit; staging them measured 0.8% slower there, while it takes
+  // rotate-half's 8 angles per chunk -- 4 x 16 bytes -- from 62 to 55 us at c4).
+  constexpr bool kStage = !TABLE || kHalf;
+  __shared__ float cs[kStage ? kTileMaxPos : 1][3][64];
+  __shared__ int slot_ok[TABLE && kStage ? kTileMaxPos : 1];
   const int lane = threadIdx.x & 63;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const bool second = blockIdx.x >= a.nb0;
   const TileTensor& T = a.t[second ? 1 : 0];
   const uint32_t g0 = (second ? blockIdx.x - a.nb0 : blockIdx.x) * kTileGroups;
   const uint32_t glast = T.groups - 1;
-  // Theta mode: everything the angles depend on -- the inverse frequency and
-  // the position ids of this thread's angle slots (vector loads) -- is
-  // requested before the data: vector loads complete in issue order, so
-  // waiting for these is not waiting for the data, and the sincos and the
-  // barrier overlap the data's latency instead of following it (c4: ids
-  // requested after the data cost ~2.5 us per call).
+  // Everything the angles depend on -- the position ids of this thread's
+  // angle items (vector loads) and the inverse frequency -- is requested
+  // before the data: vector loads complete in issue order, so waiting for
+  // these is not waiting for the data, and the angle work and the barrier
+  // overlap the data's latency instead of following it (c4: ids requested
+  // after the data cost ~2.5 us per call).  Item i (threads t and t + 256)
+  // is frequency i % 64 of position slot i / 64; a slot past the block's
+  // last reads the last one's id and leaves it unused.
   const uint32_t ps0 = div32(g0, T.gpp);
+  const uint32_t gl = g0 + kTileGroups - 1 < glast ? g0 + kTileGroups - 1 : glast;
+  const int npos = (int)(div32(gl, T.gpp) - ps0) + 1;  // <= kTileMaxPos
   float inv = 0.f;
-  int npos = 0;
-  // theta: the positions of angle items t and t + 256 (slot clamped to the
-  // block's last, whose id is then unused); table: those of groups u = 0, 1
+  if constexpr (!TABLE) inv = a.inv_freq[lane];
   uint32_t pps[2];
   PosWords pw[2];
-  if constexpr (!TABLE) {
-    inv = a.inv_freq[lane];
-    const uint32_t gl = g0 + kTileGroups - 1 < glast ? g0 + kTileGroups - 1 : glast;
-    npos = (int)(div32(gl, T.gpp) - ps0) + 1;
+  if constexpr (kStage) {
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int slot = ((int)threadIdx.x + k * kThreads) >> 6;  // npos * 64 <= 2 * kThreads
       pps[k] = ps0 + (uint32_t)(slot < npos ? slot : npos - 1);
+      pw[k] = tile_pos_words(a, pps[k]);
     }
-#pragma unroll
-    for (int k = 0; k < 2; ++k) pw[k] = tile_pos_words(a, pps[k]);
   }
   __builtin_amdgcn_sched_barrier(0);
   // Groups past the tensor's end (last tile only) re-read the last group and store nothing.
@@ -486,9 +492,9 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     v[u] = ld16_stream(T.x + ((size_t)(g < glast ? g : glast) * 64 + lane) * 8);
   }
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (TABLE) {
-    // table mode: a group's id is wave-uniform, a scalar load whose wait
-    // (lgkmcnt) is independent of the data's (vmcnt), so it follows the data
+  if constexpr (!kStage) {
+    // interleaved table mode: a group's id is wave-uniform, a scalar load
+    // whose wait (lgkmcnt) is independent of the data's (vmcnt)
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const uint32_t g = g0 + wave + 4 * u;
@@ -496,51 +502,50 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
       pw[u] = tile_pos_words(a, pps[u]);
     }
   }
-
-  if constexpr (!TABLE) {
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int i = (int)threadIdx.x + k * kThreads;
-      if (i < npos * 64) {
-        float sn, cn;
-        sincosf((float)tile_pos_value(a, pw[k], pps[k]) * inv, &sn, &cn);
-        const float sp = a.conj ? -sn : sn;
-        cs[i >> 6][0][lane] = cn;
-        cs[i >> 6][1][lane] = sp;
-        cs[i >> 6][2][lane] = -sp;
+  for (int k = 0; k < 2; ++k) {
+    const int i = (int)threadIdx.x + k * kThreads;
+    if (kStage && i < npos * 64) {
+      const int slot = i >> 6;
+      const int64_t p = tile_pos_value(a, pw[k], pps[k]);
+      float sn, cn;
+      if constexpr (TABLE) {
+        // the row's complex entry `lane` (an out-of-range id reads row 0: its outputs are zeroed)
+        const bool ok = p >= 0 && p < a.frows;
+        const f32x2 t = *reinterpret_cast<const f32x2*>(a.freqs + 2 * ((ok ? p : 0) * a.frs + lane));
+        cn = t[0];
+        sn = t[1];
+        if (lane == 0) {
+          slot_ok[slot] = ok ? 1 : 0;
+          if (!ok && a.err) *a.err = 1;
+        }
+      } else {
+        sincosf((float)p * inv, &sn, &cn);
       }
+      const float sp = a.conj ? -sn : sn;
+      cs[slot][0][lane] = cn;
+      cs[slot][1][lane] = sp;
+      cs[slot][2][lane] = -sp;
     }
-    __syncthreads();
   }
+  if constexpr (kStage) __syncthreads();
   const int c = lane & 15;
   const int f0 = (kHalf ? (c & 7) : c) * FPU;
   const bool lo = c < 8;
   // Rotate-half, lane holding x1 (lo): x1 c - x2 s; holding x2: x2 c + x1 s --
-  // both fma(own, c, partner * s') with s' = -s or s, the same roundings as
-  // rot()'s two outputs (the negation is exact).  conj flips s' again.
-  const float sgn = (a.conj ? -1.f : 1.f) * ((kHalf && lo) ? -1.f : 1.f);
+  // both fma(own, c, partner * s') with s' = -s or s (the table row picked
+  // by the lane), the same roundings as rot()'s two outputs (the negation is
+  // exact).  conj flips s' again.
+  const int srow = (kHalf && lo) ? 2 : 1;
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
     const uint32_t g = g0 + wave + 4 * u;
     const uint32_t ps = div32(g < glast ? g : glast, T.gpp);
-    float cv[FPU], sv[FPU];
+    const int slot = (int)(ps - ps0);
     bool ok = true;
-    if constexpr (TABLE) {
-      const int64_t p = tile_pos_value(a, pw[u], pps[u]);
-      ok = p >= 0 && p < a.frows;
-      if (!ok && lane == 0 && a.err) *a.err = 1;
-      const float* frow = a.freqs + 2 * ((ok ? p : 0) * a.frs + f0);
-#pragma unroll
-      for (int q = 0; q < FPU / 2; ++q) {
-        const f32x4 t = *reinterpret_cast<const f32x4*>(frow + 4 * q);
-        cv[2 * q] = t[0];
-        sv[2 * q] = t[1];
-        cv[2 * q + 1] = t[2];
-        sv[2 * q + 1] = t[3];
-      }
-    } else {
-      const int slot = (int)(ps - ps0);
-      const int srow = (kHalf && lo) ? 2 : 1;  // the sign sgn below, taken from the table
+    float cv[FPU], sv[FPU];
+    if constexpr (kStage) {
+      if constexpr (TABLE) ok = slot_ok[slot] != 0;
 #pragma unroll
       for (int e = 0; e < FPU; e += 4) {
         const f32x4 cq = *reinterpret_cast<const f32x4*>(&cs[slot][0][f0 + e]);
@@ -551,10 +556,20 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
           sv[e + j] = sq[j];
         }
       }
-    }
-    if constexpr (TABLE) {
+    } else {
+      const int64_t p = tile_pos_value(a, pw[u], pps[u]);
+      ok = p >= 0 && p < a.frows;
+      if (!ok && lane == 0 && a.err) *a.err = 1;
+      const float* frow = a.freqs + 2 * ((ok ? p : 0) * a.frs + f0);
+      const float sc = a.conj ? -1.f : 1.f;  // interleaved: the conjugate's sign alone
 #pragma unroll
-      for (int e = 0; e < FPU; ++e) sv[e] = sgn * sv[e];
+      for (int q = 0; q < FPU / 2; ++q) {
+        const f32x4 t = *reinterpret_cast<const f32x4*>(frow + 4 * q);
+        cv[2 * q] = t[0];
+        sv[2 * q] = sc * t[1];
+        cv[2 * q + 1] = t[2];
+        sv[2 * q + 1] = sc * t[3];
+      }
     }
     float own[8], o[8];
     unpack8(v[u], own);

@@ -175,12 +175,29 @@ def test_rope_tile_fp32_output(gpu, table):
     assert torch.equal(q32.to(torch.bfloat16), qb) and torch.equal(k32.to(torch.bfloat16), kb)
 
 
-def test_rope_tile_path_out_of_table_position(gpu):
-    """An id outside the table in the tile kernel: its rows are zero and the flag is raised."""
+@pytest.mark.parametrize("pairing", ["interleaved", "half"])
+def test_rope_tile_path_out_of_table_position(gpu, pairing):
+    """An id outside the table in the tile kernel (rotate-half stages the
+    rows through LDS, interleaved reads them per chunk): the flag is raised,
+    and with checking off that position's rows are zero while the others
+    equal the in-range result."""
     x = torch.ones((1, 6, 4, 128), dtype=torch.bfloat16, device=gpu)
-    freqs = torch.ones((3, 64), dtype=torch.complex64, device=gpu)
+    freqs = torch.complex(torch.rand(3, 64), torch.rand(3, 64)).to(gpu)
+    pos = torch.tensor([0, 1, 2, 3, 1, 0], device=gpu)
     with pytest.raises(IndexError):
-        kp.rope(x, positions=torch.tensor([0, 1, 2, 3, 1, 0], device=gpu), freqs_cis=freqs, pairing="interleaved")
+        kp.rope(x, positions=pos, freqs_cis=freqs, pairing=pairing)
+    kp.set_index_checking(False)
+    try:
+        out, _ = kp.rope(x, positions=pos, freqs_cis=freqs, pairing=pairing)
+        ref, _ = kp.rope(x, positions=torch.tensor([0, 1, 2, 0, 1, 0], device=gpu), freqs_cis=freqs, pairing=pairing)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(out[0, 3]) == 0
+        keep = [0, 1, 2, 4, 5]
+        assert torch.equal(out[0, keep], ref[0, keep])
+    finally:
+        with pytest.raises(IndexError):
+            kp.check_indices()
+        kp.set_index_checking(True)
 
 
 @pytest.mark.parametrize("tile", [True, False])
