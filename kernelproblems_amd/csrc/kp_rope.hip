@@ -419,6 +419,23 @@ struct TileArgs {
   float inv_freq[64];
 };
 
+// The block's tensor, its fields selected from both tensors' values: all
+// of them are loaded at fixed argument offsets in one batch (the empty asm
+// takes them together), so that no load waits for `second` -- indexing
+// a.t[second] made the compiler load each field from a computed address, a
+// chain of dependent scalar loads ahead of the block's first data load.
+__device__ __forceinline__ TileTensor pick_tensor(bool second, const TileTensor& A, const TileTensor& B) {
+  uint64_t ax = (uint64_t)A.x, bx = (uint64_t)B.x, ao = (uint64_t)A.out, bo = (uint64_t)B.out;
+  uint64_t a2 = (uint64_t)A.out2, b2 = (uint64_t)B.out2;
+  uint32_t ag = A.groups, bg = B.groups, am = A.gpp.m, bm = B.gpp.m, al = A.gpp.l, bl = B.gpp.l;
+  uint32_t ad = A.gpp.d, bd = B.gpp.d, af = (uint32_t)A.out_f32, bf = (uint32_t)B.out_f32;
+  asm volatile("" : "+s"(ax), "+s"(bx), "+s"(ao), "+s"(bo), "+s"(a2), "+s"(b2), "+s"(ag), "+s"(bg), "+s"(am),
+               "+s"(bm), "+s"(al), "+s"(bl), "+s"(ad), "+s"(bd), "+s"(af), "+s"(bf));
+  return TileTensor{reinterpret_cast<const uint16_t*>(second ? bx : ax), reinterpret_cast<void*>(second ? bo : ao),
+                    second ? bg : ag, Div32{second ? bm : am, second ? bl : al, second ? bd : ad},
+                    (int)(second ? bf : af), reinterpret_cast<void*>(second ? b2 : a2)};
+}
+
 // Position id of flattened position ps = b S + s (ps < 2^31), in two steps so
 // that its load can be issued early and waited for late: tile_pos_words
 // loads the id's 32-bit words without a branch on the id type (an int32 id
@@ -457,7 +474,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
   const int lane = threadIdx.x & 63;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const bool second = blockIdx.x >= a.nb0;
-  const TileTensor& T = a.t[second ? 1 : 0];
+  const TileTensor T = pick_tensor(second, a.t[0], a.t[1]);
   const uint32_t g0 = (second ? blockIdx.x - a.nb0 : blockIdx.x) * kTileGroups;
   const uint32_t glast = T.groups - 1;
   // Everything the angles depend on -- the position ids of this thread's
