@@ -419,23 +419,6 @@ struct TileArgs {
   float inv_freq[64];
 };
 
-// The block's tensor, its fields selected from both tensors' values: all
-// of them are loaded at fixed argument offsets in one batch (the empty asm
-// takes them together), so that no load waits for `second` -- indexing
-// a.t[second] made the compiler load each field from a computed address, a
-// chain of dependent scalar loads ahead of the block's first data load.
-__device__ __forceinline__ TileTensor pick_tensor(bool second, const TileTensor& A, const TileTensor& B) {
-  uint64_t ax = (uint64_t)A.x, bx = (uint64_t)B.x, ao = (uint64_t)A.out, bo = (uint64_t)B.out;
-  uint64_t a2 = (uint64_t)A.out2, b2 = (uint64_t)B.out2;
-  uint32_t ag = A.groups, bg = B.groups, am = A.gpp.m, bm = B.gpp.m, al = A.gpp.l, bl = B.gpp.l;
-  uint32_t ad = A.gpp.d, bd = B.gpp.d, af = (uint32_t)A.out_f32, bf = (uint32_t)B.out_f32;
-  asm volatile("" : "+s"(ax), "+s"(bx), "+s"(ao), "+s"(bo), "+s"(a2), "+s"(b2), "+s"(ag), "+s"(bg), "+s"(am),
-               "+s"(bm), "+s"(al), "+s"(bl), "+s"(ad), "+s"(bd), "+s"(af), "+s"(bf));
-  return TileTensor{reinterpret_cast<const uint16_t*>(second ? bx : ax), reinterpret_cast<void*>(second ? bo : ao),
-                    second ? bg : ag, Div32{second ? bm : am, second ? bl : al, second ? bd : ad},
-                    (int)(second ? bf : af), reinterpret_cast<void*>(second ? b2 : a2)};
-}
-
 // Position id of flattened position ps = b S + s (ps < 2^31), in two steps so
 // that its load can be issued early and waited for late: tile_pos_words
 // loads the id's 32-bit words without a branch on the id type (an int32 id
@@ -444,7 +427,13 @@ __device__ __forceinline__ TileTensor pick_tensor(bool second, const TileTensor&
 struct PosWords {
   uint32_t lo, hi;
 };
-__device__ __forceinline__ PosWords tile_pos_words(const TileArgs& a, uint32_t ps) {
+struct PosArgs {
+  const void* pos;
+  int pb;
+  int64_t psb, pss;
+  Div32 S;
+};
+__device__ __forceinline__ PosWords tile_pos_words(const PosArgs& a, uint32_t ps) {
   if (a.pos == nullptr) return PosWords{0u, 0u};
   const uint32_t b = div32(ps, a.S), s = ps - b * a.S.d;
   const int64_t i = (int64_t)b * a.psb + (int64_t)s * a.pss;
@@ -452,9 +441,37 @@ __device__ __forceinline__ PosWords tile_pos_words(const TileArgs& a, uint32_t p
   const uint32_t* w = static_cast<const uint32_t*>(a.pos) + (wide ? 2 * i : i);
   return PosWords{w[0], w[wide ? 1 : 0]};
 }
-__device__ __forceinline__ int64_t tile_pos_value(const TileArgs& a, PosWords w, uint32_t ps) {
+__device__ __forceinline__ int64_t tile_pos_value(const PosArgs& a, PosWords w, uint32_t ps) {
   if (a.pos == nullptr) return ps - div32(ps, a.S) * a.S.d;
   return a.pb == 8 ? (int64_t)(((uint64_t)w.hi << 32) | w.lo) : (int64_t)(int32_t)w.lo;
+}
+
+// The block's scalar arguments in one batch: its tensor (q or k, picked by
+// block index) and the position arguments.  The empty asm takes every value
+// at once, so they are all loaded at fixed argument offsets together and
+// the tensor's fields are then selected; indexing a.t[second] made the
+// compiler load each field from a computed address -- with the position
+// arguments, a chain of dependent scalar loads ahead of the block's first
+// data load.
+__device__ __forceinline__ void tile_prologue(const TileArgs& a, bool& second, uint32_t& tile, TileTensor& T,
+                                              PosArgs& P) {
+  const TileTensor& A = a.t[0];
+  const TileTensor& B = a.t[1];
+  uint64_t ax = (uint64_t)A.x, bx = (uint64_t)B.x, ao = (uint64_t)A.out, bo = (uint64_t)B.out;
+  uint64_t a2 = (uint64_t)A.out2, b2 = (uint64_t)B.out2;
+  uint32_t ag = A.groups, bg = B.groups, am = A.gpp.m, bm = B.gpp.m, al = A.gpp.l, bl = B.gpp.l;
+  uint32_t ad = A.gpp.d, bd = B.gpp.d, af = (uint32_t)A.out_f32, bf = (uint32_t)B.out_f32;
+  uint32_t nb0 = a.nb0, pb = (uint32_t)a.pb, Sm = a.S.m, Sl = a.S.l, Sd = a.S.d;
+  uint64_t pos = (uint64_t)a.pos, psb = (uint64_t)a.psb, pss = (uint64_t)a.pss;
+  asm volatile("" : "+s"(ax), "+s"(bx), "+s"(ao), "+s"(bo), "+s"(a2), "+s"(b2), "+s"(ag), "+s"(bg), "+s"(am),
+               "+s"(bm), "+s"(al), "+s"(bl), "+s"(ad), "+s"(bd), "+s"(af), "+s"(bf), "+s"(nb0), "+s"(pb), "+s"(Sm),
+               "+s"(Sl), "+s"(Sd), "+s"(pos), "+s"(psb), "+s"(pss));
+  second = blockIdx.x >= nb0;
+  tile = second ? blockIdx.x - nb0 : blockIdx.x;  // the block's tile within its tensor
+  T = TileTensor{reinterpret_cast<const uint16_t*>(second ? bx : ax), reinterpret_cast<void*>(second ? bo : ao),
+                 second ? bg : ag, Div32{second ? bm : am, second ? bl : al, second ? bd : ad},
+                 (int)(second ? bf : af), reinterpret_cast<void*>(second ? b2 : a2)};
+  P = PosArgs{reinterpret_cast<const void*>(pos), (int)pb, (int64_t)psb, (int64_t)pss, Div32{Sm, Sl, Sd}};
 }
 
 template <int PAIRING, bool TABLE>
@@ -473,9 +490,12 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
   __shared__ int slot_ok[TABLE && kStage ? kTileMaxPos : 1];
   const int lane = threadIdx.x & 63;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const bool second = blockIdx.x >= a.nb0;
-  const TileTensor T = pick_tensor(second, a.t[0], a.t[1]);
-  const uint32_t g0 = (second ? blockIdx.x - a.nb0 : blockIdx.x) * kTileGroups;
+  bool second;
+  uint32_t tile;
+  TileTensor T;
+  PosArgs pa;
+  tile_prologue(a, second, tile, T, pa);
+  const uint32_t g0 = tile * kTileGroups;
   const uint32_t glast = T.groups - 1;
   // Everything the angles depend on -- the position ids of this thread's
   // angle items (vector loads) and the inverse frequency -- is requested
@@ -497,7 +517,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     for (int k = 0; k < 2; ++k) {
       const int slot = ((int)threadIdx.x + k * kThreads) >> 6;  // npos * 64 <= 2 * kThreads
       pps[k] = ps0 + (uint32_t)(slot < npos ? slot : npos - 1);
-      pw[k] = tile_pos_words(a, pps[k]);
+      pw[k] = tile_pos_words(pa, pps[k]);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -516,7 +536,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     for (int u = 0; u < 2; ++u) {
       const uint32_t g = g0 + wave + 4 * u;
       pps[u] = div32(g < glast ? g : glast, T.gpp);
-      pw[u] = tile_pos_words(a, pps[u]);
+      pw[u] = tile_pos_words(pa, pps[u]);
     }
   }
 #pragma unroll
@@ -524,7 +544,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
     const int i = (int)threadIdx.x + k * kThreads;
     if (kStage && i < npos * 64) {
       const int slot = i >> 6;
-      const int64_t p = tile_pos_value(a, pw[k], pps[k]);
+      const int64_t p = tile_pos_value(pa, pw[k], pps[k]);
       float sn, cn;
       if constexpr (TABLE) {
         // the row's complex entry `lane` (an out-of-range id reads row 0: its outputs are zeroed)
@@ -574,7 +594,7 @@ __global__ __launch_bounds__(kThreads) void rope_tile(TileArgs a) {
         }
       }
     } else {
-      const int64_t p = tile_pos_value(a, pw[u], pps[u]);
+      const int64_t p = tile_pos_value(pa, pw[u], pps[u]);
       ok = p >= 0 && p < a.frows;
       if (!ok && lane == 0 && a.err) *a.err = 1;
       const float* frow = a.freqs + 2 * ((ok ? p : 0) * a.frs + f0);
