@@ -274,8 +274,6 @@ __global__ __launch_bounds__(kThreads) void xent_bwd_vec(BwdArgs a) {
   const int64_t row = (int64_t)((int)blockIdx.x / a.bpr);
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & (kWave - 1);
   const int64_t g0 = (int64_t)((int)blockIdx.x - (int)row * a.bpr) * kBwdBlockGroups + (int64_t)wave * 128;
-  float sum;
-  const int64_t t = row_target(a, row, g0 == 0 && lane == 0, sum);
   const int64_t gpr = a.V / 4;
   const f32x4* p = reinterpret_cast<const f32x4*>(a.lsm + row * a.rs);
   u32x2* q = reinterpret_cast<u32x2*>(a.out + row * a.ors);
@@ -288,6 +286,12 @@ __global__ __launch_bounds__(kThreads) void xent_bwd_vec(BwdArgs a) {
     ok[h] = gi[h] < gpr;
     v[h] = __builtin_nontemporal_load(p + (ok[h] ? gi[h] : 0));
   }
+  // The row's target after the data loads: its scalar load (lgkmcnt) is
+  // waited for independently of the data (vmcnt), whereas ahead of them it
+  // held every block's data loads back by a chain of scalar round trips.
+  __builtin_amdgcn_sched_barrier(0);
+  float sum;
+  const int64_t t = row_target(a, row, g0 == 0 && lane == 0, sum);
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
     const bool has = (t >> 2) == gi[h];  // t = -1 for rows without a target column
