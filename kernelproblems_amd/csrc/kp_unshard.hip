@@ -3,7 +3,10 @@
 //
 // One-shot grid: every block copies one 4 KiB chunk (256 threads x 16 B) of
 // one shard row of one segment, the launch shape that streams fastest on
-// gfx950.  Chunks are enumerated segment-major, then shard row, then column.
+// gfx950.  Chunks are enumerated shard row first, then the segments' chunks
+// in row order, so consecutive blocks read one source row front to back.
+#include <algorithm>
+
 #include "kp_common.hpp"
 #include "kp_internal.hpp"
 
@@ -16,28 +19,38 @@ constexpr int64_t kChunkElems = kThreads * 8;  // bf16 elements per block
 
 struct UnshardArgs {
   const uint16_t* src;
-  int64_t shards, stride;
-  int n_seg;
-  int64_t off[kMaxSeg], len[kMaxSeg], nchunk[kMaxSeg], first_block[kMaxSeg + 1];
+  int64_t stride;
+  Div32 per_row;           // chunks per shard row, over all kept segments
+  int32_t first[kMaxSeg];  // first chunk of each segment within a row; INT32_MAX past the last
+  int64_t off[kMaxSeg], len[kMaxSeg];
   uint16_t* dst[kMaxSeg];
 };
 
 template <bool VEC>
 __global__ __launch_bounds__(kThreads) void unshard_kernel(UnshardArgs a) {
-  const int64_t b = blockIdx.x;
+  const uint32_t b = blockIdx.x;
+  const uint32_t row = div32(b, a.per_row);
+  const int32_t cc = (int32_t)(b - row * a.per_row.d);
+  // The chunk's segment as a count over fixed argument slots, which the
+  // compiler fetches in one batch of scalar loads; a search loop would wait
+  // for one load per segment before the block's first data load.
   int s = 0;
-  while (s + 1 < a.n_seg && b >= a.first_block[s + 1]) ++s;
-  const int64_t local = b - a.first_block[s];
-  const int64_t row = local / a.nchunk[s], chunk = local % a.nchunk[s];
-  if (row >= a.shards) return;
-  const uint16_t* sp = a.src + row * a.stride + a.off[s];
-  uint16_t* dp = a.dst[s] + row * a.len[s];
-  const int64_t c0 = chunk * kChunkElems;
+  int32_t start = 0;
+#pragma unroll
+  for (int k = 1; k < kMaxSeg; ++k) {
+    const bool in = cc >= a.first[k];
+    s = in ? k : s;
+    start = in ? a.first[k] : start;
+  }
+  const uint16_t* sp = a.src + (int64_t)row * a.stride + a.off[s];
+  const int64_t len = a.len[s];
+  uint16_t* dp = a.dst[s] + (int64_t)row * len;
+  const int64_t c0 = (int64_t)(cc - start) * kChunkElems;
   if constexpr (VEC) {
     const int64_t c = c0 + (int64_t)threadIdx.x * 8;
-    if (c < a.len[s]) st16(dp + c, ld16_stream(sp + c));
+    if (c < len) st16(dp + c, ld16_stream(sp + c));
   } else {
-    for (int64_t c = c0 + threadIdx.x; c < min(a.len[s], c0 + kChunkElems); c += kThreads) dp[c] = sp[c];
+    for (int64_t c = c0 + threadIdx.x; c < min(len, c0 + kChunkElems); c += kThreads) dp[c] = sp[c];
   }
 }
 
@@ -55,11 +68,9 @@ extern "C" int kp_unshard_bf16(const void* src, int64_t shards, int64_t shard_st
     return fail(KP_EINVAL, "%s: NULL pointer or negative size", who);
   UnshardArgs a{};
   a.src = static_cast<const uint16_t*>(src);
-  a.shards = shards;
   a.stride = shard_stride;
-  a.n_seg = n_seg;
   bool vec = aligned16(src) && (shard_stride % 8) == 0;
-  int64_t blocks = 0;
+  int64_t per_row = 0;
   for (int s = 0; s < n_seg; ++s) {
     if (col_off[s] < 0 || col_len[s] < 0 || (col_len[s] > 0 && dst[s] == nullptr))
       return fail(KP_EINVAL, "%s: bad segment %d", who, s);
@@ -68,14 +79,17 @@ extern "C" int kp_unshard_bf16(const void* src, int64_t shards, int64_t shard_st
     a.off[s] = col_off[s];
     a.len[s] = col_len[s];
     a.dst[s] = static_cast<uint16_t*>(dst[s]);
-    a.nchunk[s] = ceil_div(col_len[s], kChunkElems);
-    a.first_block[s] = blocks;
-    blocks += a.nchunk[s] * shards;
+    a.first[s] = (int32_t)std::min<int64_t>(per_row, INT32_MAX);
+    per_row += ceil_div(col_len[s], kChunkElems);
     vec = vec && (col_off[s] % 8) == 0 && (col_len[s] % 8) == 0 && aligned16(dst[s]);
   }
-  a.first_block[n_seg] = blocks;
-  if (blocks == 0) return KP_OK;
-  if (blocks > 0x7fffffffLL) return fail(KP_EUNSUPPORTED, "%s: too many blocks", who);
+  for (int s = n_seg; s < kMaxSeg; ++s) a.first[s] = INT32_MAX;
+  if (per_row == 0) return KP_OK;
+  // Every block index (row * per_row + chunk) stays below 2^31, which
+  // div32 requires.
+  if (per_row > 0x7fffffffLL / shards) return fail(KP_EUNSUPPORTED, "%s: too many blocks", who);
+  const int64_t blocks = per_row * shards;
+  a.per_row = make_div32((uint32_t)per_row);
   hipStream_t s = as_stream(stream);
   if (vec) KP_LAUNCH_DOMINANT(unshard_kernel<true>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);
   else KP_LAUNCH_DOMINANT(unshard_kernel<false>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a);

@@ -31,6 +31,21 @@ def test_unshard_matches_split_clone(gpu, splits, keep):
         assert torch.equal(o, e)
 
 
+@pytest.mark.parametrize("shards", [1, 3])
+def test_unshard_sixteen_segments_empty_ends(gpu, shards):
+    """All 16 argument slots in use, empty first / middle / last segments and
+    a segment of exactly one chunk, at shard counts other than 8."""
+    splits = (0, 2056, 8, 0, 4096, 2048, 24, 4104, 8, 8, 16, 8, 8, 8, 2040, 0)
+    keep = tuple(range(16))
+    g = torch.Generator(device=gpu).manual_seed(11 + shards)
+    L = sum(splits)
+    flat = torch.randn(shards * L, dtype=torch.bfloat16, device=gpu, generator=g)
+    outs = kp.unshard(flat, shards, splits, keep)
+    exp = _expected(flat.view(shards, L), splits, keep)
+    for o, e in zip(outs, exp):
+        assert o.shape == e.shape and torch.equal(o, e)
+
+
 def test_unshard_row_strided_view(gpu):
     """A [shards, L] view whose rows are further apart than L (stride > L)."""
     g = torch.Generator(device=gpu).manual_seed(5)
