@@ -10,7 +10,11 @@ each with its whole-call rate, roofline (dominant kernel), traffic, CPU
 baseline and the tensor-level drop-in's time per call.  When --steps is
 below 100, each block also carries a "steady" pass of 100 calls: the timed
 loop's fixed cost (first launch, closing synchronisation) spread over few
-steps inflates the per-call time of the small configurations.
+steps inflates the per-call time of the small configurations.  The default run also times the canonical
+drop-in of each fragment family (CORE_FRAGMENTS: RMSNorm, embedding, RoPE and
+the norm -> embedding-backward chain) through its kernel_function at the
+reference's own shape, under "fragment_drop_ins", each beside the reference's
+record of that fragment on its H100 (--fragments: every distinct drop-in).
 
 A step is one call of the fragment (one pass of the hot path over one batch
 of synthetic input, already resident in HBM).  Workloads are the
@@ -353,7 +357,8 @@ class EmbBwd(Workload):
                           f"read {T * D * 2 / 1e6:.1f} MB + write {V * D * 4 / 1e6:.1f} MB")
         uniq = int(torch.unique(self.ids).numel())
         self.description = (f"C3 embedding backward: grad [{B},{S},{D}] bf16, ids Zipf(1.1) ({uniq} distinct) -> "
-                            f"dense fp32 [{V},{D}], sort-and-segment, each row written once")
+                            f"dense fp32 [{V},{D}], sort-and-segment, every row written (touched rows of the "
+                            f"top zero shares twice)")
         R = self.rotations(self.bytes_per_call)
         gd, idd = self.grad.to(dev), self.ids.to(dev)
         fn = L.lib().kp_embedding_bwd_bf16
@@ -973,14 +978,33 @@ def _view_bytes(ts):
     return total
 
 
-def measure_fragments(dev, steps, warmup):
-    """Every distinct fragment drop-in (kernelproblems_amd.fragments) at its
-    reference shape: kernel_function on rotating get_inputs sets (>= 1 GiB of
-    inputs or 2 sets), K calls timed with synchronisation on both sides.
-    moved_bytes = every input view and every distinct output once (an upper
-    bound where a fragment reads part of an input, e.g. the y of a saved
-    (y, rstd) tuple).  ref = the reference's own record of the fragment (its
-    eager time and fastest passing candidate on its H100), where it has one."""
+# The canonical drop-in of each hot-path fragment family, timed at its
+# reference shape in every default run (--fragments times all of them).
+CORE_FRAGMENTS = (
+    "v7/59f786beb25f",  # RMSNorm forward, y + rstd
+    "v7/215dd2e6a519",  # RMSNorm forward, strided FSDP weight view
+    "v8/7884328a5557",  # residual add + RMSNorm forward
+    "v7/45990c83cfd6",  # RMSNorm backward, dw to fp32
+    "v8/d8f596b3df34",  # gradient adds -> RMSNorm backward -> residual add
+    "v8/3c6c589cdf81",  # residual add recomputed + RMSNorm backward
+    "v7/1e49beb8a123",  # embedding forward from a flat-buffer table
+    "v7/a12a160cb11b",  # embedding dense backward -> fp32
+    "v7/e29b92927600",  # RoPE forward (interleaved, table)
+    "v8/c8c60d8f7015",  # RoPE q + k forward with the position gather
+    "v7/5c65f62b0422",  # RoPE backward (conjugate table)
+    "v6/0b493aad68f0",  # chain: RMSNorm forward + backward -> embedding backward
+)
+
+
+def measure_fragments(dev, steps, warmup, ids=None):
+    """Fragment drop-ins (kernelproblems_amd.fragments) at their reference
+    shapes -- `ids`, or every distinct one: kernel_function on rotating
+    get_inputs sets (>= 1 GiB of inputs or 2 sets), K calls timed with
+    synchronisation on both sides.  moved_bytes = every input view and every
+    distinct output once (an upper bound where a fragment reads part of an
+    input, e.g. the y of a saved (y, rstd) tuple).  ref = the reference's own
+    record of the fragment (its eager time and fastest passing candidate on
+    its H100), where it has one."""
     import torch
     from kernelproblems_amd import fragments as fr
     try:
@@ -988,7 +1012,8 @@ def measure_fragments(dev, steps, warmup):
     except (OSError, ValueError):
         ref = {}
     out = {}
-    ids = [f for f in fr.FRAGMENTS if f not in fr.SAME_AS and f not in fr.EQUIVALENT]
+    if ids is None:
+        ids = [f for f in fr.FRAGMENTS if f not in fr.SAME_AS and f not in fr.EQUIVALENT]
     for fid in ids:
         mod = fr.load(fid)
         first = mod.get_inputs(device=dev, generator=torch.Generator(device=dev).manual_seed(1))
@@ -1151,7 +1176,9 @@ def main():
                          "configuration (c1, c2, c3f, c3b, c4, c5f, c5b) gets a block under 'configs'")
     ap.add_argument("--all", action="store_true", help="also measure every other workload (no CPU baseline)")
     ap.add_argument("--fragments", action="store_true",
-                    help="also time every distinct fragment drop-in at its reference shape (GPU only)")
+                    help="time every distinct fragment drop-in at its reference shape (by default only the "
+                         "canonical drop-in of each family, CORE_FRAGMENTS)")
+    ap.add_argument("--no-fragments", action="store_true", help="time no fragment drop-ins")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--no-probe", action="store_true", help="skip the streaming-ceiling probe")
     ap.add_argument("--no-dropin", action="store_true", help="skip timing the tensor-level drop-ins")
@@ -1313,6 +1340,8 @@ def main():
         line["fragments"] = frags
     if args.fragments:
         line["fragment_drop_ins"] = measure_fragments(dev, args.steps, args.warmup)
+    elif not args.no_fragments and not args.solo:
+        line["fragment_drop_ins"] = measure_fragments(dev, args.steps, args.warmup, CORE_FRAGMENTS)
     print(json.dumps(line), flush=True)
     return 0
 

@@ -38,6 +38,7 @@ extern "C" {
 #define KP_EUNSUPPORTED 2  /* valid call outside what this build implements (message via kp_last_error_message) */
 #define KP_EHIP 3          /* a HIP runtime call or launch failed */
 #define KP_EWORKSPACE 4    /* workspace_bytes smaller than the matching *_workspace_size() */
+#define KP_EBUSY 5         /* kp_rmsnorm_bwd_bf16_noalloc: an unfinished call on another stream holds the scratch */
 
 #define KP_DTYPE_F32 0
 #define KP_DTYPE_BF16 1
@@ -133,13 +134,20 @@ int kp_rmsnorm_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, 
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): the same computation and arguments as
  * kp_rmsnorm_bwd_bf16, with the weight-gradient partial rows kept in a static
- * device array of kp_rmsnorm_bwd_noalloc_max_bytes() bytes (8 MiB: 256 row
- * blocks of up to 8192 fp32 columns, enough for every configuration here) that
- * each GPU holds until the process ends.  A shape whose partial rows do not
- * fit returns KP_EUNSUPPORTED before launching anything.  Every call on one
- * GPU shares that GPU's array, so calls that overlap on one GPU (different
- * streams, no ordering) race; calls ordered on one stream do not.  No
- * hipMalloc, hipFree or hipMemset is made.
+ * device array of kp_rmsnorm_bwd_noalloc_max_bytes() bytes (8 MiB) that each
+ * GPU holds until the process ends.  The partial rows take one fp32 row of N
+ * per row block, and the row-block count is the device's CU count times the
+ * blocks per CU (1 by default; the KP_RMS_BWD_BPC tuning knob raises it): on
+ * a 256-CU MI355X at the default that is room for N <= 8192, every
+ * configuration here.  A shape whose partial rows do not fit returns
+ * KP_EUNSUPPORTED before launching anything.  Every call on one GPU shares
+ * that GPU's array: calls ordered on one stream are safe; a call on a
+ * different stream while the previous call on that GPU has not finished
+ * returns KP_EBUSY and launches nothing (the library records an event after
+ * each call's launches and queries it; the first call on a device creates
+ * that event and looks up the array's address).  A stream under graph
+ * capture is not guarded: the caller orders captured calls.  No hipMalloc,
+ * hipFree or hipMemset is made.
  */
 size_t kp_rmsnorm_bwd_noalloc_max_bytes(void);
 int kp_rmsnorm_bwd_bf16_noalloc(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,

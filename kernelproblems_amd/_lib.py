@@ -23,6 +23,7 @@ KP_EINVAL = 1
 KP_EUNSUPPORTED = 2
 KP_EHIP = 3
 KP_EWORKSPACE = 4
+KP_EBUSY = 5
 KP_DTYPE_F32 = 0
 KP_DTYPE_BF16 = 1
 KP_ROPE_HALF = 0
@@ -35,6 +36,7 @@ _STATUS = {
     KP_EUNSUPPORTED: "unsupported",
     KP_EHIP: "HIP error",
     KP_EWORKSPACE: "workspace too small",
+    KP_EBUSY: "scratch busy on another stream",
 }
 
 

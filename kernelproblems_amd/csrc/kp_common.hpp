@@ -10,6 +10,7 @@
 #include <stdint.h>
 
 #include "../../include/kp.h"
+#include "kp_div32.hpp"
 
 namespace kp {
 
@@ -118,22 +119,5 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 
 __host__ __device__ __forceinline__ int64_t ceil_div_dev(int64_t a, int64_t b) { return (a + b - 1) / b; }
-
-// Division of 32-bit n < 2^31 by a divisor d (1 <= d < 2^31) fixed for a
-// launch, without a divide sequence: with l = ceil(log2 d) and
-// m = floor(2^32 (2^l - d) / d) + 1 (< 2^32), n / d = (mulhi(n, m) + n) >> l
-// (Granlund & Montgomery, "Division by invariant integers using
-// multiplication", PLDI 1994, section 4; the multiplier's 2^32 term is the
-// "+ n", which cannot overflow since mulhi(n, m) < n < 2^31).  The host
-// computes (m, l) once; in a kernel a wave-uniform n takes two scalar ops.
-struct Div32 {
-  uint32_t m, l, d;
-};
-inline Div32 make_div32(uint32_t d) {
-  uint32_t l = 0;
-  while ((1ull << l) < d) ++l;
-  return Div32{(uint32_t)(((1ull << 32) * ((1ull << l) - d)) / d + 1), l, d};
-}
-__device__ __forceinline__ uint32_t div32(uint32_t n, const Div32& q) { return (__umulhi(n, q.m) + n) >> q.l; }
 
 }  // namespace kp

@@ -296,7 +296,7 @@ struct FwdOut {
 size_t bwd_workspace_size(int64_t M, int64_t N) {
   if (M <= 0 || N <= 0) return 16;
   // Partial rows: at most one per row block; the block count never exceeds 4 per
-  // CU.  Rows are padded to whole 32-column chunks.
+  // CU.  Rows are padded to whole 16-column chunks (kPartChunk).
   const int64_t blocks = (int64_t)cu_count() * 4;
   const int64_t rows = M < blocks ? M : blocks;
   return (size_t)(rows * ceil_div(N, kPartChunk) * kPartChunk * (int64_t)sizeof(float));
@@ -451,32 +451,53 @@ int rms_bwd_impl(const char* who, const void* const* dy_terms, const int64_t* dy
 // ------------------------------------------------------------ allocation-free
 // kp_rmsnorm_bwd_bf16_noalloc keeps the weight-gradient partial rows in a
 // fixed device array instead of a caller workspace: one copy per GPU, held
-// until the process ends, shared by every call on that GPU (calls that overlap
-// on one GPU race on it).  Nothing in it needs clearing: each call's row
-// blocks write their whole partial rows before the finalize reads them.  The
-// array's name is a host-side stand-in in host code, never a device address:
-// scratch_ptr() looks the address up once per device (that device current)
-// with hipGetSymbolAddress, and launches take that pointer.
+// until the process ends, shared by every call on that GPU.  Nothing in it
+// needs clearing: each call's row blocks write their whole partial rows
+// before the finalize reads them.  The array's name is a host-side stand-in
+// in host code, never a device address: the per-device set-up looks the
+// address up once (that device current) with hipGetSymbolAddress, and
+// launches take that pointer.
+//
+// Overlap guard: the set-up also creates one event per device, recorded on
+// the calling stream after each call's launches.  A call on a different
+// stream from the previous call on that GPU first asks whether that event
+// has completed; while it has not, the call returns KP_EBUSY and launches
+// nothing (two unordered calls would race on the array).  Calls on one
+// stream are ordered by the stream and pass straight through.  A stream
+// under graph capture is not guarded (an event query there would end the
+// capture): a captured call records nothing and checks nothing.
 constexpr size_t kScratchBytes = (size_t)8 << 20;  // 256 row blocks x 8192 fp32 columns
 __device__ __align__(256) uint8_t scratch[kScratchBytes];
 
 constexpr int kMaxScratchDevices = 64;
-std::mutex g_scratch_mu;
-void* g_scratch[kMaxScratchDevices];
+struct ScratchState {
+  void* ptr = nullptr;         // device address of this GPU's copy of `scratch`
+  hipEvent_t done = nullptr;   // recorded after the previous uncaptured call's launches
+  hipStream_t last = nullptr;  // that call's stream
+  bool used = false;
+};
+std::mutex g_scratch_mu;  // guards g_scratch and serialises guarded calls (check, launch, record)
+ScratchState g_scratch[kMaxScratchDevices];
 
-int scratch_ptr(const char* who, void** out) {
+// Per-device set-up (first call on the device, that device current).
+// Caller holds g_scratch_mu.
+int scratch_state(const char* who, ScratchState** out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxScratchDevices)
     return fail(KP_EHIP, "%s: no current HIP device (or device %d beyond %d)", who, dev, kMaxScratchDevices);
-  std::lock_guard<std::mutex> lock(g_scratch_mu);
-  if (g_scratch[dev] == nullptr) {
+  ScratchState& st = g_scratch[dev];
+  if (st.ptr == nullptr) {
     void* p = nullptr;
-    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess || p == nullptr)
       return fail(KP_EHIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev, hipGetErrorString(e));
-    g_scratch[dev] = p;
+    hipEvent_t ev = nullptr;
+    e = hipEventCreateWithFlags(&ev, hipEventDisableTiming);
+    if (e != hipSuccess) return fail(KP_EHIP, "%s: hipEventCreateWithFlags on device %d: %s", who, dev, hipGetErrorString(e));
+    st.ptr = p;
+    st.done = ev;
   }
-  *out = g_scratch[dev];
+  *out = &st;
   return KP_OK;
 }
 }  // namespace
@@ -620,20 +641,38 @@ int kp_rmsnorm_bwd_bf16_noalloc(const void* const* dy_terms, const int64_t* dy_s
                                 int64_t dxr_stride, void* dx, int64_t dx_stride, float* dw_f32, void* dw_bf16,
                                 int dw_f32_round_bf16, int64_t M, int64_t N, float eps, void* stream) {
   static const char* who = "kp_rmsnorm_bwd_bf16_noalloc";
-  void* ws = nullptr;
-  if ((dw_f32 != nullptr || dw_bf16 != nullptr) && M > 0) {
-    const int st = scratch_ptr(who, &ws);
-    if (st != KP_OK) return st;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  ScratchState* ss = nullptr;
+  int st = scratch_state(who, &ss);
+  if (st != KP_OK) return st;
+  hipStream_t s = as_stream(stream);
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(s, &cap);
+  if (e != hipSuccess) return fail(KP_EHIP, "%s: hipStreamIsCapturing: %s", who, hipGetErrorString(e));
+  const bool guarded = cap == hipStreamCaptureStatusNone;
+  if (guarded && ss->used && s != ss->last) {
+    e = hipEventQuery(ss->done);
+    if (e == hipErrorNotReady)
+      return fail(KP_EBUSY,
+                  "%s: the previous call on this GPU (another stream) has not finished; calls on different "
+                  "streams share the static scratch and must be ordered by the caller",
+                  who);
+    if (e != hipSuccess) return fail(KP_EHIP, "%s: hipEventQuery: %s", who, hipGetErrorString(e));
   }
-  const int st = rms_bwd_impl(who, dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, rstd, weight, w_seg_len,
-                              w_seg_stride, dx_residual, dxr_stride, dx, dx_stride, dw_f32, dw_bf16,
-                              dw_f32_round_bf16, M, N, eps, ws, kScratchBytes, nullptr, stream);
+  st = rms_bwd_impl(who, dy_terms, dy_strides, n_dy, x_terms, x_strides, n_x, rstd, weight, w_seg_len, w_seg_stride,
+                    dx_residual, dxr_stride, dx, dx_stride, dw_f32, dw_bf16, dw_f32_round_bf16, M, N, eps, ss->ptr,
+                    kScratchBytes, nullptr, stream);
   if (st == KP_EWORKSPACE)  // rejected before any launch
     return fail(KP_EUNSUPPORTED,
                 "%s: M=%lld, N=%lld needs more weight-gradient partial rows than its %zu bytes of static scratch "
                 "hold (one fp32 row of N per row block); use kp_rmsnorm_bwd_bf16 with a workspace",
                 who, (long long)M, (long long)N, kScratchBytes);
-  return st;
+  if (st != KP_OK || !guarded) return st;
+  e = hipEventRecord(ss->done, s);
+  if (e != hipSuccess) return fail(KP_EHIP, "%s: hipEventRecord: %s", who, hipGetErrorString(e));
+  ss->last = s;
+  ss->used = true;
+  return KP_OK;
 }
 
 int kp_rmsnorm_fwd_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,

@@ -498,7 +498,7 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   if (rloc == 0) {
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      // 8 consecutive columns, 8-aligned: inside one 32-column chunk
+      // 8 consecutive columns, 8-aligned: inside one 16-column chunk
       float* pp = a.partial + part_index(col + i * 512, blockIdx.x, gridDim.x);
       *reinterpret_cast<f32x4*>(pp) = f32x4{acc[i * 8], acc[i * 8 + 1], acc[i * 8 + 2], acc[i * 8 + 3]};
       *reinterpret_cast<f32x4*>(pp + 4) = f32x4{acc[i * 8 + 4], acc[i * 8 + 5], acc[i * 8 + 6], acc[i * 8 + 7]};

@@ -207,7 +207,9 @@ def embedding_dense_backward(
     round_to_bf16: bool = False,
 ) -> torch.Tensor:
     """Dense [num_weights, D] gradient of an embedding, fp32 accumulation,
-    deterministic sort-and-segment, every row written once."""
+    deterministic sort-and-segment.  Every row is written; the rows at the top
+    of the vocabulary that the early launches zero unconditionally are written
+    a second time when an id touches them."""
     if out_dtype not in (torch.float32, torch.bfloat16):
         raise RuntimeError(f"embedding_dense_backward: unsupported out_dtype {out_dtype}")
     flag = _flag(grad_output.device) if grad_output.is_cuda else None

@@ -4,7 +4,8 @@ same dx and weight gradient (the same row kernel, block count and
 fixed-order finalize), on two calls in a row whose second is smaller (the
 static scratch keeps the first call's partial rows, which must not leak into
 the second), and a clean rejection of a shape whose partial rows exceed the
-scratch, before anything is launched."""
+scratch, before anything is launched; a call on a second stream while the
+previous call is pending is refused with KP_EBUSY."""
 import ctypes as C
 
 import pytest
@@ -63,12 +64,62 @@ def test_noalloc_rejects_oversized_before_launch(gpu):
     print("[no_alloc] oversized shape is rejected", flush=True)
     lib = L.lib()
     M, N = 4096, 16384  # generic kernel, 2 blocks per CU: 512 x 16384 fp32 partial rows = 32 MiB
-    x = torch.zeros((M, N), dtype=torch.bfloat16, device=gpu)
-    w = torch.ones(N, dtype=torch.bfloat16, device=gpu)
-    dx = torch.zeros((M, N), dtype=torch.bfloat16, device=gpu)
-    dw = torch.zeros(N, dtype=torch.float32, device=gpu)
-    st = _call(lib, "kp_rmsnorm_bwd_bf16_noalloc", x, x, None, w, dx, dw, M, N)
+    g = gen(15)
+    x, dy = randn_bf16((M, N), g).to(gpu), randn_bf16((M, N), g).to(gpu)
+    w = randn_bf16(N, g, 1.0, 0.02).to(gpu)
+    # had anything run, dx and dw (finite inputs) would no longer be all NaN
+    dx = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+    dw = torch.full((N,), float("nan"), dtype=torch.float32, device=gpu)
+    st = _call(lib, "kp_rmsnorm_bwd_bf16_noalloc", dy, x, None, w, dx, dw, M, N)
     assert st == L.KP_EUNSUPPORTED
     assert b"static scratch" in lib.kp_last_error_message()
     torch.cuda.synchronize()
-    assert int(torch.count_nonzero(dx)) == 0, "nothing may be launched for a rejected shape"
+    assert bool(torch.isnan(dx).all()), "nothing may be launched for a rejected shape"
+    assert bool(torch.isnan(dw).all()), "nothing may be launched for a rejected shape"
+
+
+def test_noalloc_busy_on_another_stream(gpu):
+    """A call on a second stream while the previous call (first stream) is
+    still pending returns KP_EBUSY and launches nothing; once that call has
+    finished, the second stream's call runs and matches the workspace entry.
+    Pending is established, not assumed: a torch event recorded on the first
+    stream ahead of its call must still be incomplete after the second call
+    has returned (the library's event comes later on that stream)."""
+    print("[no_alloc] overlap guard across two streams", flush=True)
+    lib = L.lib()
+    M, N = 8192, 4096
+    g = gen(16)
+    x, dy = randn_bf16((M, N), g).to(gpu), randn_bf16((M, N), g).to(gpu)
+    w = randn_bf16(N, g, 1.0, 0.02).to(gpu)
+    big_src = torch.empty(1 << 31, dtype=torch.bfloat16, device=gpu)  # 4 GiB
+    big_dst = torch.empty_like(big_src)
+    sa, sb = torch.cuda.Stream(gpu), torch.cuda.Stream(gpu)
+    dx_a = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device=gpu)
+    dw_a = torch.full((N,), float("nan"), dtype=torch.float32, device=gpu)
+    dx_b, dw_b = torch.full_like(dx_a, float("nan")), torch.full_like(dw_a, float("nan"))
+    before = torch.cuda.Event()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(sa):
+        for _ in range(8):  # ~15 ms of copies queued ahead of the call on stream a
+            big_dst.copy_(big_src)
+        before.record(sa)
+        assert _call(lib, "kp_rmsnorm_bwd_bf16_noalloc", dy, x, None, w, dx_a, dw_a, M, N) == 0
+    with torch.cuda.stream(sb):
+        st = _call(lib, "kp_rmsnorm_bwd_bf16_noalloc", dy, x, None, w, dx_b, dw_b, M, N)
+    pending = not before.query()
+    assert pending, "stream a's queued copies finished before the second call: the guard was not exercised"
+    assert st == L.KP_EBUSY, f"expected KP_EBUSY, got {st}: {lib.kp_last_error_message().decode()}"
+    assert b"has not finished" in lib.kp_last_error_message()
+    sa.synchronize()
+    torch.cuda.synchronize()
+    del big_src, big_dst
+    assert bool(torch.isnan(dx_b).all()) and bool(torch.isnan(dw_b).all()), "the refused call launched work"
+    with torch.cuda.stream(sb):
+        assert _call(lib, "kp_rmsnorm_bwd_bf16_noalloc", dy, x, None, w, dx_b, dw_b, M, N) == 0
+    torch.cuda.synchronize()
+    ws = torch.empty(int(lib.kp_rmsnorm_bwd_workspace_size(M, N)), dtype=torch.uint8, device=gpu)
+    dx_r, dw_r = torch.empty_like(dx_a), torch.empty_like(dw_a)
+    assert _call(lib, "kp_rmsnorm_bwd_bf16", dy, x, None, w, dx_r, dw_r, M, N, ws) == 0
+    torch.cuda.synchronize()
+    for dx, dw in ((dx_a, dw_a), (dx_b, dw_b)):
+        assert torch.equal(dx, dx_r) and torch.equal(dw, dw_r)
