@@ -279,6 +279,57 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride,
                           int32_t* error_flag, void* stream);
 
 /* ------------------------------------------------------------------------
+ * RMSNorm backward (optionally with its forward) whose residual-epilogue
+ * output feeds the dense embedding backward of the same tokens, without that
+ * output ever reaching HBM.
+ *
+ * Replaces the _fused_rms_norm(_backward) -> add.Tensor(add_220, dx) ->
+ * embedding_dense_backward -> _to_copy chains of
+ *   v6/0b493aad68f0/problem.py:16-71   (forward + backward; y returned as 3 views)
+ *   v5/118d525f44e0/problem.py:16-80   (the same over a flat-buffer weight view)
+ *   v8/f6251e84e3fa/problem.py:10-57   (backward from the saved rstd)
+ * where add_tensor_2 = add_220 + dx is an intermediate, not an output.
+ *
+ * Norm: every argument has its kp_rmsnorm_bwd_bf16 meaning with one x term
+ *   (x, x_stride) and dx_residual required: g = bf16(dx_residual + bf16(dx)).
+ *   rstd: fp32 [M], or NULL to recompute it from x with eps; with rstd ==
+ *   NULL the same pass may also write the forward's y (bf16 [M, N], row
+ *   stride y_stride, may be NULL) and rstd_out (fp32 [M], may be NULL).
+ * Embedding: row t of g is token t with id indices[t] (index_bytes 4 or 8);
+ *   grad_table [V, N] (out_dtype KP_DTYPE_F32 or _BF16, out_round_bf16 as in
+ *   kp_embedding_bwd_bf16) = for each id the fp32 sum of its tokens' g rows
+ *   in ascending token order (rows of ids no token has are zero), the same
+ *   bits as kp_embedding_bwd_bf16 of a stored g; ids equal to padding_idx or
+ *   outside [0, V) contribute nothing (out-of-range ids set *error_flag).
+ *   There is no scale_grad_by_freq (the chains pass False).
+ * One row pass walks each run of equal ids in sorted order and sums g into
+ * registers; rows of skipped ids still count for y and the weight gradient.
+ * The weight gradient is deterministic (a fixed grouping of rows into partial
+ * rows, then a fixed-order sum) but groups rows differently from
+ * kp_rmsnorm_bwd_bf16, so its last bits may differ from that entry's.
+ * Supported: N = 2048, 4096 or 8192, 1..3 dy terms, rows 16-byte aligned with
+ * strides a multiple of 8, a 16-byte aligned weight with segment length and
+ * stride multiples of 8, a 16-byte aligned grad_table, V < 2^21, M < 2^31;
+ * anything else returns KP_EUNSUPPORTED (run the norm entry point and then
+ * kp_embedding_bwd_bf16).
+ * workspace: at least kp_rmsnorm_embedding_bwd_workspace_size(M, N, V) bytes,
+ * 16-byte aligned.
+ */
+size_t kp_rmsnorm_embedding_bwd_workspace_size(int64_t M, int64_t N, int64_t V);
+int kp_rmsnorm_embedding_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy,
+                                  const void* x, int64_t x_stride,
+                                  const float* rstd,
+                                  const void* weight, int64_t w_seg_len, int64_t w_seg_stride,
+                                  const void* dx_residual, int64_t dxr_stride,
+                                  void* y, int64_t y_stride, float* rstd_out,
+                                  float* dw_f32, void* dw_bf16, int dw_f32_round_bf16,
+                                  int64_t M, int64_t N, float eps,
+                                  const void* indices, int index_bytes, int64_t V, int64_t padding_idx,
+                                  void* grad_table, int out_dtype, int out_round_bf16,
+                                  void* workspace, size_t workspace_bytes,
+                                  int32_t* error_flag, void* stream);
+
+/* ------------------------------------------------------------------------
  * Rotary position embedding on up to two tensors (q and k) in one launch.
  *
  * Replaces the _to_copy f32 -> view_as_complex -> mul -> view_as_real ->

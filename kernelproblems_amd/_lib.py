@@ -94,6 +94,12 @@ SIGNATURES = {
         i32,
         [vp, i64, vp, i32, i64, i64, i64, i64, i32, vp, i32, i32, vp, sz, vp, vp],
     ),
+    "kp_rmsnorm_embedding_bwd_workspace_size": (sz, [i64, i64, i64]),
+    "kp_rmsnorm_embedding_bwd_bf16": (
+        i32,
+        [pvp, pi64, i32, vp, i64, vp, vp, i64, i64, vp, i64, vp, i64, vp, vp, vp, i32, i64, i64, f32,
+         vp, i32, i64, i64, vp, i32, i32, vp, sz, vp, vp],
+    ),
     "kp_rope_bf16": (
         i32,
         [vp, vp, i64, pi64, pi64, vp, vp, i64, pi64, pi64, i64, i64, i64, vp, i32, i64, i64,

@@ -43,6 +43,7 @@
 
 #include "kp_common.hpp"
 #include "kp_internal.hpp"
+#include "kp_rmsnorm_kernels.hpp"
 
 namespace kp {
 namespace {
@@ -527,6 +528,266 @@ __global__ __launch_bounds__(kThreads) void emb_combine(EmbBwdArgs a, int comb_b
   }
 }
 
+// ---- Fused chain: RMSNorm backward -> embedding backward ------------------
+// The norm's row pass walks each window's sorted positions ((id, token) order)
+// instead of token order, so the rows g = dx_residual + dx of a run are summed
+// into the run's fp32 accumulators as they are made -- ascending token order,
+// the sums K3 forms from a stored g -- and g never reaches HBM.  Block
+// b < nwin: window b (kWin positions), one row per step with the next
+// position's loads in flight, in the row layout of the RMSNorm backward
+// kernel for the same N (WPR waves of VPL chunks; wave w owns columns
+// [w * SEG, (w + 1) * SEG)), so every row's reductions, y and g are bitwise
+// those of that kernel.  Blocks [nwin, nwin + nb2): the norm rows of tokens the
+// embedding skips (padding or out-of-range id), which hold no sorted
+// position; their g is dropped.  Every block writes one weight-gradient
+// partial row -- a fixed grouping (windows, then token ranges) -- and the
+// RMSNorm finalize sums them.  Pieces of runs that span windows go to the
+// same piece rows as K3's, for K4.
+struct ChainArgs {
+  int64_t nwin;    // window blocks
+  int64_t nb2;     // norm-only blocks
+  int64_t tpb2;    // tokens per norm-only block
+  float* partial;  // [ceil(N / 16)][nwin + nb2][16] fp32, or nullptr (no weight gradient)
+};
+
+constexpr int64_t kChainTokens = 128;  // tokens per norm-only block
+
+// 8 consecutive values (fp32 or bf16) at column c of table row r; write-back
+// stores (a lane's 32 fp32 bytes are two 16-byte stores that L2 merges).
+__device__ __forceinline__ void store_out8(const EmbBwdArgs& a, int64_t r, int64_t c, const float* v) {
+  if (a.out_bf16) {
+    st16(static_cast<uint16_t*>(a.out) + r * a.D + c, pack8(v));
+  } else {
+    float t[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) t[j] = a.round_bf16 ? round_bf(v[j]) : v[j];
+    st32f(static_cast<float*>(a.out) + r * a.D + c, t);
+  }
+}
+
+// Rows in flight: RB positions of the block's window per step, one per group
+// of WPR waves (rloc r takes position w0 + k RB + r).  The groups r > 0 pass
+// their g rows through LDS to group 0, which adds them to the run in
+// position order -- the order K3 sums a stored g in -- and emits finished
+// runs.  Positions past the window's end run as a masked row (row M: its
+// loads re-read row M - 1, nothing is stored), so every wave meets the row
+// reduction's barriers equally often.
+template <int WPR>
+struct ChainShape {
+  static constexpr int NW = WPR > 4 ? WPR : 4;  // waves per block
+  static constexpr int RB = NW / WPR;           // positions per step
+};
+
+template <int VPL, int WPR, int NDY, bool FWD>
+__global__ __launch_bounds__(ChainShape<WPR>::NW * 64) void rms_emb_window(rms::RmsBwdArgs a, EmbBwdArgs e,
+                                                                           ChainArgs c) {
+  constexpr int NW = ChainShape<WPR>::NW, RB = ChainShape<WPR>::RB, SEG = 512 * VPL;
+  __shared__ float red[2][NW][2];
+  // g chunks of groups 1..RB-1 for group 0, two steps deep
+  __shared__ u32x4 gx[2][RB > 1 ? RB - 1 : 1][WPR][VPL][64];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int part = wave % WPR, rloc = wave / WPR;
+  const int64_t col = (int64_t)part * SEG + lane * 8;
+  float wf[VPL * 8];
+  {
+    u32x4 wv[VPL];
+    rms::load_weight<VPL>(wv, a.w, a.w_seg_len, a.w_seg_stride, col);
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) unpack8(wv[i], wf + i * 8);
+  }
+  float acc[VPL * 8];
+#pragma unroll
+  for (int j = 0; j < VPL * 8; ++j) acc[j] = 0.f;
+  int it = 0;
+  const int64_t b = blockIdx.x;
+  const int64_t nwb = c.nwin;  // window blocks
+  if (b < nwb) {
+    const int n_valid = (int)min((int64_t)max(e.hdr->n_valid, 0), e.T);
+    const int w0 = (int)(b * kWin);
+    const int w1 = min(n_valid, w0 + kWin);
+    const int np = w1 - w0;
+    if (np > 0) {
+      // Lane i < np holds position w0 + i's token, run bounds and id; the
+      // loop reads them as scalars (readlane), with no dependent load.
+      const int li = min(lane, np - 1);
+      const int tok_l = (int)token_of(e, w0 + li);
+      const int lo_l = clamp_pos(e.run_lo[w0 + li], n_valid);
+      const int hi_l = clamp_pos(e.run_hi[w0 + li], n_valid);
+      const int id_l = (int)e.sid[w0 + li];
+      const int steps = (np + RB - 1) / RB;
+      float racc[VPL * 8];
+#pragma unroll
+      for (int j = 0; j < VPL * 8; ++j) racc[j] = 0.f;
+      int lo = w0, hi = w0;  // hi == w0: a run starts at the first position
+      rms::RawRow<VPL, 1> x0, x1;
+      rms::RawRow<VPL, NDY> d0, d1;
+      rms::RawRow<VPL, 1> r0, r1;
+      float q0, q1;
+      // Position q of the window (offset from w0) into the run: group 0 only.
+      auto add_pos = [&](int q, const u32x4 (&gq)[VPL]) {
+        const int p = w0 + q;
+        if (p == hi) {
+          lo = min(__builtin_amdgcn_readlane(lo_l, q), p);
+          hi = max(__builtin_amdgcn_readlane(hi_l, q), p + 1);
+#pragma unroll
+          for (int j = 0; j < VPL * 8; ++j) racc[j] = 0.f;
+        }
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+          float f[8];
+          unpack8(gq[i], f);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) racc[i * 8 + j] += f[j];
+        }
+        if (p + 1 == hi || p + 1 == w1) {
+          if (lo >= w0 && hi <= w0 + kWin) {
+            const int64_t row = (int64_t)(uint32_t)__builtin_amdgcn_readlane(id_l, lo - w0);
+            if (row < e.V)
+#pragma unroll
+              for (int i = 0; i < VPL; ++i) store_out8(e, row, col + i * 512, racc + i * 8);
+          } else {
+            float* pr = e.pieces + (2 * b + (lo < w0 ? 0 : 1)) * e.D + col;
+#pragma unroll
+            for (int i = 0; i < VPL; ++i) st32f(pr + i * 512, racc + i * 8);
+          }
+        }
+      };
+#define KP_POS(k) ((k) * RB + rloc)
+#define KP_ROWK(k) (KP_POS(k) < np ? (int64_t)__builtin_amdgcn_readlane(tok_l, KP_POS(k)) : a.M)
+#define KP_LOAD(S, k)                                                                                  \
+  rms::bwd_load<VPL, 1, NDY, true, FWD>(x##S, d##S, r##S, q##S, a, rms::clamp_row(KP_ROWK(k), a.M), col); \
+  __builtin_amdgcn_sched_barrier(0)
+#define KP_PROC(S, k)                                                                                              \
+  {                                                                                                                \
+    u32x4 gv[VPL];                                                                                                 \
+    rms::bwd_row<VPL, WPR, 1, NDY, true, NW, FWD, true>(a, x##S, d##S, r##S, q##S, wf, acc, red, KP_ROWK(k), col,  \
+                                                        lane, wave, rloc, it, gv);                                \
+    if constexpr (RB > 1) {                                                                                        \
+      if (rloc > 0) {                                                                                              \
+        _Pragma("unroll") for (int i = 0; i < VPL; ++i) gx[it & 1][rloc - 1][part][i][lane] = gv[i];             \
+      }                                                                                                            \
+      __syncthreads();                                                                                             \
+    }                                                                                                              \
+    if (rloc == 0) {                                                                                               \
+      if ((k) * RB < np) add_pos((k) * RB, gv);                                                                    \
+      _Pragma("unroll") for (int r = 1; r < RB; ++r) {                                                            \
+        if ((k) * RB + r < np) {                                                                                   \
+          u32x4 gr[VPL];                                                                                           \
+          _Pragma("unroll") for (int i = 0; i < VPL; ++i) gr[i] = gx[it & 1][r - 1][part][i][lane];              \
+          add_pos((k) * RB + r, gr);                                                                               \
+        }                                                                                                          \
+      }                                                                                                            \
+    }                                                                                                              \
+    ++it;                                                                                                          \
+  }
+      int k = 0;
+      KP_LOAD(0, 0);
+      for (; k + 2 < steps; k += 2) {
+        KP_LOAD(1, k + 1);
+        KP_PROC(0, k);
+        KP_LOAD(0, k + 2);
+        KP_PROC(1, k + 1);
+      }
+      if (k + 1 < steps) {
+        KP_LOAD(1, k + 1);
+        KP_PROC(0, k);
+        KP_PROC(1, k + 1);
+      } else {
+        KP_PROC(0, k);
+      }
+#undef KP_POS
+#undef KP_ROWK
+#undef KP_LOAD
+#undef KP_PROC
+    }
+  } else if (b < nwb + c.nb2) {
+    // Tokens [t0, t1): a row whose id K1 rejected (out of range or the
+    // padding index) still belongs to the norm (y, rstd, weight gradient).
+    // The ballot is the same in every wave (same ids), so the block agrees;
+    // each such row is processed by the rloc 0 waves (the others run a
+    // masked row to meet the barriers).
+    const int64_t t0 = (b - nwb) * c.tpb2;
+    const int64_t t1 = min(e.T, t0 + c.tpb2);
+    for (int64_t tb = t0; tb < t1; tb += 64) {
+      const int64_t t = tb + lane;
+      bool skipped = false;
+      if (t < t1) {
+        const int64_t id = load_index(e.idx, e.ib, t);
+        skipped = !(id >= 0 && id < e.V) || id == e.padding_idx;
+      }
+      uint64_t m = __ballot(skipped);
+      while (m != 0) {
+        const int64_t row = rloc == 0 ? tb + __builtin_ctzll(m) : a.M;
+        m &= m - 1;
+        rms::RawRow<VPL, 1> xr;
+        rms::RawRow<VPL, NDY> dr;
+        rms::RawRow<VPL, 1> rr;
+        float rq;
+        rms::bwd_load<VPL, 1, NDY, true, FWD>(xr, dr, rr, rq, a, rms::clamp_row(row, a.M), col);
+        u32x4 gv[VPL];
+        rms::bwd_row<VPL, WPR, 1, NDY, true, NW, FWD, true>(a, xr, dr, rr, rq, wf, acc, red, row, col, lane, wave,
+                                                            rloc, it, gv);
+        ++it;
+      }
+    }
+  }
+  // One partial row per block: the RB row groups' column sums combined in a
+  // fixed order (rloc 0 + rloc 1 + ...) through LDS, then stored by rloc 0.
+  if (c.partial != nullptr) {
+    if constexpr (RB > 1) {
+      __shared__ float comb[RB - 1][WPR][SEG];
+      if (rloc > 0) {
+#pragma unroll
+        for (int j = 0; j < VPL * 8; j += 4)
+          *reinterpret_cast<f32x4*>(&comb[rloc - 1][part][(j / 8) * 512 + lane * 8 + (j % 8)]) =
+              f32x4{acc[j], acc[j + 1], acc[j + 2], acc[j + 3]};
+      }
+      __syncthreads();
+      if (rloc == 0) {
+#pragma unroll
+        for (int r = 0; r < RB - 1; ++r)
+#pragma unroll
+          for (int j = 0; j < VPL * 8; ++j) acc[j] += comb[r][part][(j / 8) * 512 + lane * 8 + (j % 8)];
+      }
+    }
+    if (rloc == 0) {
+      const int64_t P = nwb + c.nb2;
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        float* pp = c.partial + rms::part_index(col + i * 512, b, P);  // 8 columns inside one 16-column chunk
+        *reinterpret_cast<f32x4*>(pp) = f32x4{acc[i * 8], acc[i * 8 + 1], acc[i * 8 + 2], acc[i * 8 + 3]};
+        *reinterpret_cast<f32x4*>(pp + 4) = f32x4{acc[i * 8 + 4], acc[i * 8 + 5], acc[i * 8 + 6], acc[i * 8 + 7]};
+      }
+    }
+  }
+}
+
+typedef void (*ChainKernel)(rms::RmsBwdArgs, EmbBwdArgs, ChainArgs);
+
+template <int VPL, int WPR>
+ChainKernel chain_kernel_for(int n_dy, bool fwd) {
+  switch (n_dy * 2 + (fwd ? 1 : 0)) {
+    case 2: return rms_emb_window<VPL, WPR, 1, false>;
+    case 3: return rms_emb_window<VPL, WPR, 1, true>;
+    case 4: return rms_emb_window<VPL, WPR, 2, false>;
+    case 5: return rms_emb_window<VPL, WPR, 2, true>;
+    case 6: return rms_emb_window<VPL, WPR, 3, false>;
+    case 7: return rms_emb_window<VPL, WPR, 3, true>;
+  }
+  return nullptr;
+}
+// Row widths with a fused kernel and their row layout: the RMSNorm
+// backward's default shape for that N (VPL chunks x WPR waves per row).
+// *nw gets the block's waves, *rb its rows per step.
+ChainKernel chain_kernel(int64_t N, int n_dy, bool fwd, int* nw, int* rb) {
+  switch (N) {
+    case 2048: *nw = ChainShape<1>::NW; *rb = ChainShape<1>::RB; return chain_kernel_for<4, 1>(n_dy, fwd);
+    case 4096: *nw = ChainShape<2>::NW; *rb = ChainShape<2>::RB; return chain_kernel_for<4, 2>(n_dy, fwd);
+    case 8192: *nw = ChainShape<8>::NW; *rb = ChainShape<8>::RB; return chain_kernel_for<2, 8>(n_dy, fwd);
+  }
+  return nullptr;
+}
+
 // ------------------------------------------------------------- workspace
 struct Layout {
   size_t hdr, keys_chunk, chunk_valid, sid, stok, run_lo, run_hi, bitmap, pieces, total;
@@ -577,6 +838,26 @@ int64_t share_rows(const char* env, int64_t dflt_mb, int64_t row_bytes, int64_t 
   const int64_t rows = mb <= 0 ? 0 : ((mb << 20) + row_bytes - 1) / row_bytes;
   return rows < cap_rows ? rows : cap_rows;
 }
+
+// Workspace of the fused chain: the embedding backward's layout, then the
+// weight-gradient partial rows of its window and norm-only blocks.
+struct ChainLayout {
+  Layout emb;
+  int64_t nwin, nb2;
+  size_t partial, total;
+};
+ChainLayout make_chain_layout(int64_t T, int64_t V, int64_t D) {
+  ChainLayout L{};
+  L.emb = make_layout(T, V, D);
+  L.nwin = ceil_div(T, kWin);
+  L.nb2 = ceil_div(T, kChainTokens);
+  L.partial = L.emb.total;
+  L.total = align256(L.partial + (size_t)(L.nwin + L.nb2) * (size_t)(ceil_div(D, rms::kPartChunk) * rms::kPartChunk) *
+                                     sizeof(float));
+  return L;
+}
+
+bool rows16(const void* p, int64_t stride) { return aligned16(p) && (stride & 7) == 0; }
 
 }  // namespace
 }  // namespace kp
@@ -696,6 +977,153 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   if (vec) KP_LAUNCH_SPAN(false, true, emb_combine<true>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
   else KP_LAUNCH_SPAN(false, true, emb_combine<false>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
   return check_launch(who);
+}
+
+size_t kp_rmsnorm_embedding_bwd_workspace_size(int64_t M, int64_t N, int64_t V) {
+  if (M < 0 || N <= 0 || V <= 0) return 0;
+  return make_chain_layout(M, V, N).total;
+}
+
+int kp_rmsnorm_embedding_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strides, int n_dy, const void* x,
+                                  int64_t x_stride, const float* rstd, const void* weight, int64_t w_seg_len,
+                                  int64_t w_seg_stride, const void* dx_residual, int64_t dxr_stride, void* y,
+                                  int64_t y_stride, float* rstd_out, float* dw_f32, void* dw_bf16,
+                                  int dw_f32_round_bf16, int64_t M, int64_t N, float eps, const void* indices,
+                                  int index_bytes, int64_t V, int64_t padding_idx, void* grad_table, int out_dtype,
+                                  int out_round_bf16, void* workspace, size_t workspace_bytes, int32_t* error_flag,
+                                  void* stream) {
+  static const char* who = "kp_rmsnorm_embedding_bwd_bf16";
+  if (M < 0 || N <= 0 || V <= 0) return fail(KP_EINVAL, "%s: need M >= 0, N > 0, V > 0", who);
+  if (dy_terms == nullptr || dy_strides == nullptr || n_dy < 1 || n_dy > 3)
+    return fail(KP_EINVAL, "%s: dy needs 1..3 terms", who);
+  if (grad_table == nullptr) return fail(KP_EINVAL, "%s: grad_table is NULL", who);
+  if (M > 0) {
+    for (int i = 0; i < n_dy; ++i)
+      if (dy_terms[i] == nullptr || dy_strides[i] < 0) return fail(KP_EINVAL, "%s: dy term %d is NULL or has a negative stride", who, i);
+    if (x == nullptr || x_stride < 0 || dx_residual == nullptr || dxr_stride < 0 || indices == nullptr)
+      return fail(KP_EINVAL, "%s: NULL x, dx_residual or indices (or a negative stride)", who);
+  }
+  if (index_bytes != 4 && index_bytes != 8) return fail(KP_EINVAL, "%s: index_bytes must be 4 or 8", who);
+  if (out_dtype != KP_DTYPE_F32 && out_dtype != KP_DTYPE_BF16) return fail(KP_EINVAL, "%s: bad out_dtype", who);
+  const bool want_dw = dw_f32 != nullptr || dw_bf16 != nullptr;
+  if (want_dw && weight == nullptr) return fail(KP_EINVAL, "%s: a weight gradient needs a weight", who);
+  if (weight != nullptr && (w_seg_len <= 0 || w_seg_stride < 0))
+    return fail(KP_EINVAL, "%s: weight segment length must be > 0", who);
+  if (rstd != nullptr && (y != nullptr || rstd_out != nullptr))
+    return fail(KP_EINVAL, "%s: y / rstd_out are the forward's outputs: pass rstd = NULL to compute them", who);
+  if (y != nullptr && y_stride < 0) return fail(KP_EINVAL, "%s: negative y stride", who);
+  // The fused row pass: N = 2048, 4096 or 8192, 16-byte rows, one x term,
+  // the residual epilogue, the sort's limits.  Anything else: KP_EUNSUPPORTED
+  // (the caller runs the norm and then kp_embedding_bwd_bf16).
+  const bool fwd = y != nullptr || rstd_out != nullptr;
+  int nw = 4, rb = 1;  // rb: rows per step, documented by the kernel's shape
+  const ChainKernel kern = chain_kernel(N, n_dy, fwd, &nw, &rb);
+  (void)rb;
+  bool ok = kern != nullptr && V <= kMaxVocab && M <= 0x7fffffffLL && rows16(x, x_stride) &&
+            rows16(dx_residual, dxr_stride) && (y == nullptr || rows16(y, y_stride)) &&
+            (weight == nullptr || (aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0)) &&
+            aligned16(grad_table);
+  for (int i = 0; ok && i < n_dy; ++i) ok = rows16(dy_terms[i], dy_strides[i]);
+  if (!ok)
+    return fail(KP_EUNSUPPORTED, "%s: no fused row pass for this shape or layout (N=%lld, %d dy terms, V=%lld)", who,
+                (long long)N, n_dy, (long long)V);
+  const ChainLayout CL = make_chain_layout(M, V, N);
+  if (workspace == nullptr || workspace_bytes < CL.total || !aligned16(workspace))
+    return fail(KP_EWORKSPACE, "%s: workspace needs %zu bytes, 16-byte aligned (got %zu)", who, CL.total,
+                workspace_bytes);
+  const Layout& L = CL.emb;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  EmbBwdArgs e{};
+  e.grad = nullptr;
+  e.grs = N;
+  e.idx = indices;
+  e.ib = index_bytes;
+  e.T = M;
+  e.V = V;
+  e.D = N;
+  e.padding_idx = padding_idx;
+  e.scale = 0;
+  e.out = grad_table;
+  e.out_bf16 = out_dtype == KP_DTYPE_BF16;
+  e.round_bf16 = out_round_bf16 ? 1 : 0;
+  e.nchunks = (int)L.nchunks;
+  e.err = error_flag;
+  e.hdr = reinterpret_cast<EmbHeader*>(ws + L.hdr);
+  e.keys_chunk = reinterpret_cast<uint32_t*>(ws + L.keys_chunk);
+  e.chunk_valid = reinterpret_cast<int32_t*>(ws + L.chunk_valid);
+  e.sid = reinterpret_cast<uint32_t*>(ws + L.sid);
+  e.stok = reinterpret_cast<uint32_t*>(ws + L.stok);
+  e.run_lo = reinterpret_cast<int32_t*>(ws + L.run_lo);
+  e.run_hi = reinterpret_cast<int32_t*>(ws + L.run_hi);
+  e.bitmap = reinterpret_cast<uint32_t*>(ws + L.bitmap);
+  e.pieces = reinterpret_cast<float*>(ws + L.pieces);
+
+  rms::RmsBwdArgs a{};
+  for (int i = 0; i < n_dy; ++i) {
+    a.dy[i] = static_cast<const uint16_t*>(dy_terms[i]);
+    a.dys[i] = dy_strides[i];
+  }
+  a.n_dy = n_dy;
+  a.x[0] = static_cast<const uint16_t*>(x);
+  a.xs[0] = x_stride;
+  a.n_x = 1;
+  a.rstd = rstd;
+  a.w = static_cast<const uint16_t*>(weight);
+  a.w_seg_len = weight ? w_seg_len : N;
+  a.w_seg_stride = weight ? w_seg_stride : N;
+  a.dxr = static_cast<const uint16_t*>(dx_residual);
+  a.dxrs = dxr_stride;
+  a.y = static_cast<uint16_t*>(y);
+  a.ys = y_stride;
+  a.rstd_out = rstd_out;
+  a.M = M;
+  a.N = N;
+  a.eps = eps;
+  ChainArgs c{CL.nwin, CL.nb2, kChainTokens, want_dw ? reinterpret_cast<float*>(ws + CL.partial) : nullptr};
+
+  hipStream_t s = as_stream(stream);
+  const int64_t nq = ceil_div(N, kColStep);
+  const int64_t row_bytes = N * (out_dtype == KP_DTYPE_BF16 ? 2 : 4);
+  // Zero fill: K1 and K2 carry unconditional shares from the top of the
+  // vocabulary and K4 a conditional one, as in kp_embedding_bwd_bf16; the
+  // rest of the untouched rows go to K3's zero blocks, launched with no
+  // window blocks after the fused row pass (whose registers would hold zero
+  // blocks sharing its launch to a few per CU).
+  const int64_t z1 = share_rows("KP_EMB_ZERO_MB_SORT", 128, row_bytes, V / 4);
+  const int64_t z2 = share_rows("KP_EMB_ZERO_MB_RANK", 128, row_bytes, V / 4);
+  const int64_t z4 = share_rows("KP_EMB_ZERO_MB_COMBINE", 96, row_bytes, V / 4);
+  const ZeroShare zs1{V - z1, V, 0};
+  const ZeroShare zs2{V - z1 - z2, V - z1, 0};
+  const ZeroShare zs4{V - z1 - z2 - z4, V - z1 - z2, 1};
+  const ZeroShare zs3{0, V - z1 - z2 - z4, 1};
+  const int64_t total_keys = L.nchunks * kChunk;
+  const int64_t rank_blocks = ceil_div(total_keys, kThreads);
+  const int comb_blocks = cu_count() * 4;
+  const int64_t g1 = L.nchunks + z1 * nq, g2 = rank_blocks + z2 * nq, g3 = zs3.hi * nq, g4 = comb_blocks + z4 * nq;
+  if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL || g3 > 0x7fffffffLL || g4 > 0x7fffffffLL)
+    return fail(KP_EUNSUPPORTED, "%s: V * N too large for one launch", who);
+  int st;
+  KP_LAUNCH_SPAN(true, false, emb_sort_chunks<true>, dim3((unsigned)g1), dim3(kThreads), 0, s, e, zs1);
+  if ((st = check_launch(who)) != KP_OK) return st;
+  hipLaunchKernelGGL(emb_rank<true>, dim3((unsigned)g2), dim3(kThreads), 0, s, e, (int)rank_blocks, zs2);
+  if ((st = check_launch(who)) != KP_OK) return st;
+  const int64_t nblocks = CL.nwin + CL.nb2;  // window blocks, then norm-only blocks
+  if (nblocks > 0) {
+    hipLaunchKernelGGL(kern, dim3((unsigned)nblocks), dim3(nw * 64), 0, s, a, e, c);
+    if ((st = check_launch(who)) != KP_OK) return st;
+  }
+  if (g3 > 0) {
+    hipLaunchKernelGGL(emb_dense<true>, dim3((unsigned)g3), dim3(kThreads), 0, s, e, (int64_t)0, zs3);
+    if ((st = check_launch(who)) != KP_OK) return st;
+  }
+  KP_LAUNCH_SPAN(false, true, emb_combine<true>, dim3((unsigned)g4), dim3(kThreads), 0, s, e, comb_blocks, zs4);
+  if ((st = check_launch(who)) != KP_OK) return st;
+  // The weight gradient: the partial rows in block order (none when M == 0:
+  // zeros).
+  if (want_dw)
+    return rms_dw_finalize_launch(c.partial, (int)nblocks, N, dw_f32, static_cast<uint16_t*>(dw_bf16),
+                                  dw_f32_round_bf16, s, who);
+  return KP_OK;
 }
 
 }  // extern "C"

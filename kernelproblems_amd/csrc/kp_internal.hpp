@@ -26,6 +26,12 @@ hipEvent_t prof_stop_event();
 // kernel's own start and completion, so they time that kernel alone.
 void launch_dominant_raw(const void* fn, dim3 grid, dim3 block, void** args, size_t shmem, hipStream_t s);
 
+// Sums P fp32 weight-gradient partial rows (the row kernels' layout,
+// [ceil(N / 16)][P][16]) into dw in a fixed order (kp_rmsnorm.hip), for
+// other row passes that write the same partial rows.
+int rms_dw_finalize_launch(const float* partial, int P, int64_t N, float* dw_f32, uint16_t* dw_bf16, int round_f32,
+                           hipStream_t s, const char* who);
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }

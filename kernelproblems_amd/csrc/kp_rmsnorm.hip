@@ -501,6 +501,14 @@ int scratch_state(const char* who, ScratchState** out) {
   return KP_OK;
 }
 }  // namespace
+
+int rms_dw_finalize_launch(const float* partial, int P, int64_t N, float* dw_f32, uint16_t* dw_bf16, int round_f32,
+                           hipStream_t s, const char* who) {
+  hipLaunchKernelGGL(rms_dw_finalize, dim3((unsigned)ceil_div(N, kPartChunk)), dim3(kThreads), 0, s, partial, P, N,
+                     dw_f32, dw_bf16, round_f32);
+  return check_launch(who);
+}
+
 }  // namespace kp
 
 using namespace kp;

@@ -338,11 +338,15 @@ __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& 
 // loaded), and the forward's outputs are stored from it as well -- y =
 // bf16(xhat * w), the same expression as the forward kernel, h when there are
 // several x terms, rstd -- so the chain's x is read once for both passes.
-template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD>
+//
+// KEEP: the row's dx (with the residual epilogue) is handed back in gout[]
+// (the same packed bf16 chunks the store would write) instead of stored, for
+// a consumer in the same kernel (the embedding backward of the chain).
+template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD, bool KEEP = false>
 __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, NX>& xr, const RawRow<VPL, NDY>& dr,
                                         const RawRow<VPL, 1>& rr, float rq, const float (&wf)[VPL * 8],
                                         float (&acc)[VPL * 8], float (&red)[2][NW][2], int64_t row, int64_t col,
-                                        int lane, int wave, int rloc, int it) {
+                                        int lane, int wave, int rloc, int it, u32x4* gout = nullptr) {
   const bool valid = row < a.M;
   const float inv_n = 1.0f / (float)a.N;
   const bool have_rstd = !FWD && a.rstd != nullptr;
@@ -404,7 +408,7 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
       }
       if (a.rstd_out != nullptr && wave % WPR == 0 && lane == 0) a.rstd_out[row] = r;
     }
-    uint16_t* dxrow = a.dx + row * a.dxs + col;
+    uint16_t* dxrow = KEEP ? nullptr : a.dx + row * a.dxs + col;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       float o[8];
@@ -418,7 +422,11 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
       }
       u32x4 ov = pack8(o);
       if constexpr (RES) ov = add_bf8(rr.v[0][i], ov);
-      st16_stream(dxrow + i * 512, ov);
+      if constexpr (KEEP) {
+        gout[i] = ov;
+      } else {
+        st16_stream(dxrow + i * 512, ov);
+      }
     }
   }
 }

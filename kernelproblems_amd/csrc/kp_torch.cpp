@@ -378,6 +378,70 @@ Tensor embedding_dense_backward(const Tensor& grad_output, const Tensor& indices
   return out;
 }
 
+// The RMSNorm backward (with its forward when rstd is None) whose residual
+// output g = dx_residual + dx feeds the dense embedding backward of the same
+// tokens: one row pass that sums g straight into the table
+// (kp_rmsnorm_embedding_bwd_bf16).  Layouts without a fused kernel run the
+// norm entry point and then the embedding backward of its stored g (same y,
+// g and table bits; the weight gradient groups its rows differently).
+// Returns (y or None, dw or None, table).
+py::tuple rms_norm_embedding_backward(const std::vector<Tensor>& dy_terms, const Tensor& x,
+                                      const std::optional<Tensor>& rstd, const std::optional<Tensor>& weight,
+                                      double eps, int64_t n, const Tensor& dx_residual, bool want_y,
+                                      const std::optional<std::string>& dw, const Tensor& indices,
+                                      int64_t num_weights, int64_t padding_idx, bool out_f32, bool round_to_bf16,
+                                      const std::optional<Tensor>& flag) {
+  const std::string who = "rms_norm_embedding_backward";
+  BwdOperands o;
+  bwd_operands(who, dy_terms, {x}, weight, n, dx_residual, o);
+  if (rstd && want_y) fail(who + ": y is the forward's output: pass rstd=None to compute it");
+  Tensor rstd_t;
+  if (rstd) {
+    need_gpu(who + " rstd", *rstd, at::kFloat);
+    if (rstd->numel() != o.m)
+      fail(who + ": rstd has " + std::to_string(rstd->numel()) + " values, expected " + std::to_string(o.m));
+    rstd_t = rstd->contiguous();
+  }
+  Tensor idx;
+  int ib = 0;
+  index_info(indices, idx, ib);
+  if (idx.numel() != o.m)
+    fail(who + ": " + std::to_string(idx.numel()) + " indices for " + std::to_string(o.m) + " rows");
+  const Tensor& dy0 = dy_terms[0];
+  const auto bf = dy0.options().dtype(at::kBFloat16);
+  Tensor y = want_y ? at::empty(x.sizes(), bf) : Tensor();
+  Tensor dw_f32, dw_bf16;
+  dw_outputs(who, dw, weight.has_value(), n, bf, dw_f32, dw_bf16);
+  Tensor table = at::empty({num_weights, n}, dy0.options().dtype(out_f32 ? at::kFloat : at::kBFloat16));
+  const size_t ws_bytes = kp_rmsnorm_embedding_bwd_workspace_size(o.m, n, num_weights);
+  Tensor wsp = at::empty({(int64_t)std::max<size_t>(ws_bytes, 16)}, bf.dtype(at::kByte));
+  const int st = kp_rmsnorm_embedding_bwd_bf16(
+      o.dyp, o.dys, o.n_dy, o.xp[0], o.xs[0], static_cast<const float*>(ptr(rstd_t)), ptr(o.ws.w), o.ws.len,
+      o.ws.stride, ptr(o.res), o.res_s, ptr(y), n, nullptr, static_cast<float*>(ptr(dw_f32)), ptr(dw_bf16),
+      (dw && *dw == "f32_bf16") ? 1 : 0, o.m, n, (float)eps, idx.data_ptr(), ib, num_weights, padding_idx,
+      table.data_ptr(), out_f32 ? KP_DTYPE_F32 : KP_DTYPE_BF16, round_to_bf16 ? 1 : 0, wsp.data_ptr(), ws_bytes,
+      flag_ptr(flag), stream_of(dy0));
+  if (st == KP_EUNSUPPORTED) {  // no fused row pass for this layout: the norm, then the embedding backward of g
+    wsp = Tensor();
+    Tensor g;
+    py::object dwo;
+    if (rstd) {
+      py::tuple r = rms_norm_backward(dy_terms, {x}, rstd, weight, eps, n, dx_residual, true, dw);
+      g = r[0].cast<Tensor>();
+      dwo = r[1];
+    } else {
+      py::tuple r = rms_norm_forward_backward(dy_terms, {x}, weight, eps, n, dx_residual, dw, false, false);
+      if (want_y) y = r[0].cast<Tensor>();
+      g = r[1].cast<Tensor>();
+      dwo = r[2];
+    }
+    Tensor t = embedding_dense_backward(g, indices, num_weights, padding_idx, false, out_f32, round_to_bf16, flag);
+    return py::make_tuple(opt(y), dwo, t);
+  }
+  check("kp_rmsnorm_embedding_bwd_bf16", st);
+  return py::make_tuple(opt(y), opt(dw_view(dw_f32, dw_bf16, weight)), table);
+}
+
 // ------------------------------------------------------------- FSDP unshard
 std::vector<Tensor> unshard(Tensor flat, int64_t shards, const std::vector<int64_t>& split_sizes,
                             const std::vector<int64_t>& keep) {
@@ -725,6 +789,7 @@ PYBIND11_MODULE(_kp_torch, m) {
   m.def("embedding", &embedding);
   m.def("embedding_rms_norm", &embedding_rms_norm);
   m.def("embedding_dense_backward", &embedding_dense_backward);
+  m.def("rms_norm_embedding_backward", &rms_norm_embedding_backward);
   m.def("rope", &rope);
   m.def("rope_complex", &rope_complex);
   m.def("unshard", &unshard);

@@ -3,10 +3,11 @@ residual epilogue, then the token-embedding backward of the result, the saved
 forward passed as a tuple: v8/f6251e84e3fa/problem.py:10-57.
 
 rstd = _fused_rms_norm_recomputed[1]; dy = bf16(bf16(mm_670 + mm_672) +
-mm_674); g = bf16(add_220 + dx) in the norm's row kernel; dw is the bf16 weight
-gradient widened to fp32; the [128256, 4096] table gradient is the dense
-embedding backward of g (fp32 accumulation, one bf16 rounding as the eager bf16
-table, stored fp32).  The reference's own get_inputs hands a 0-dim tensor where
+mm_674); g = bf16(add_220 + dx) is made in the norm's row pass, which walks the
+tokens in (id, token) order and sums each id's g rows into its table row in
+registers (fp32 accumulation, one bf16 rounding as the eager bf16 table, stored
+fp32), so g never reaches HBM; dw is the bf16 weight gradient widened to
+fp32.  The reference's own get_inputs hands a 0-dim tensor where
 the graph passes the tuple (v8/f6251e84e3fa/benchmark.json records the index
 error); get_inputs here builds the tuple."""
 import torch
@@ -29,8 +30,7 @@ def get_inputs(device="cuda", generator=None):
 def kernel_function(_fused_rms_norm_recomputed, mm_670, mm_672, mm_674, embedding, _unsafe_view_432, add_220,
                     arg583_1):
     n = embedding.shape[-1]
-    g, dw = F.rms_norm_backward([mm_670, mm_672, mm_674], [embedding], _fused_rms_norm_recomputed[1],
-                                _unsafe_view_432, EPS, n, dx_residual=add_220, dw="f32_bf16")
-    table = F.embedding_dense_backward(g, arg583_1, NUM_WEIGHTS, -1, False, out_dtype=torch.float32,
-                                       round_to_bf16=True)
+    _, dw, table = F.rms_norm_embedding_backward([mm_670, mm_672, mm_674], embedding, _fused_rms_norm_recomputed[1],
+                                                 _unsafe_view_432, EPS, n, add_220, arg583_1, NUM_WEIGHTS, -1,
+                                                 dw="f32_bf16", out_dtype=torch.float32, round_to_bf16=True)
     return dw, table

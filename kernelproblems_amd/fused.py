@@ -220,6 +220,46 @@ def embedding_dense_backward(
     return out
 
 
+def rms_norm_embedding_backward(
+    dy_terms: Sequence[torch.Tensor],
+    x: torch.Tensor,
+    rstd: Optional[torch.Tensor],
+    weight: Optional[torch.Tensor],
+    eps: float,
+    n: int,
+    dx_residual: torch.Tensor,
+    indices: torch.Tensor,
+    num_weights: int,
+    padding_idx: int = -1,
+    *,
+    want_y: bool = False,
+    dw: Optional[str] = "f32",
+    out_dtype: torch.dtype = torch.float32,
+    round_to_bf16: bool = False,
+):
+    """The RMSNorm backward whose residual output g = bf16(dx_residual + dx)
+    feeds embedding_dense_backward of the same tokens, as one row pass that
+    sums g into the table without storing it (the _fused_rms_norm_backward ->
+    add -> embedding_dense_backward chains of v6/0b493aad68f0/problem.py:45-71,
+    v5/118d525f44e0/problem.py:50-80, v8/f6251e84e3fa/problem.py:37-57).
+
+    rstd=None recomputes rstd from x (and with want_y the same pass writes the
+    forward's y = bf16(x * rstd * w)); otherwise rstd is the saved forward's.
+    The table is what embedding_dense_backward(g, indices, num_weights,
+    padding_idx) returns (no scale_grad_by_freq); the weight gradient is that
+    of rms_norm_backward, summed in a different (fixed) grouping of rows.
+    Returns (y or None, dw or None, table)."""
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise RuntimeError(f"rms_norm_embedding_backward: unsupported out_dtype {out_dtype}")
+    flag = _flag(x.device) if x.is_cuda else None
+    out = _native().rms_norm_embedding_backward(dy_terms, x, rstd, weight, float(eps), int(n), dx_residual,
+                                                bool(want_y), dw, indices, int(num_weights),
+                                                -1 if padding_idx is None else int(padding_idx),
+                                                out_dtype == torch.float32, bool(round_to_bf16), flag)
+    _raise_if_flagged(flag, "rms_norm_embedding_backward")
+    return out
+
+
 # ---------------------------------------------------------------- RoPE
 _PAIRING = {"half": L.KP_ROPE_HALF, "interleaved": L.KP_ROPE_INTERLEAVED}
 

@@ -166,6 +166,26 @@ def test_cross_entropy_fwd_bwd_validation(lib):
                                              0, None) == L.KP_OK
 
 
+def test_rmsnorm_embedding_bwd_validation(lib):
+    fn = "kp_rmsnorm_embedding_bwd_bf16"
+    dy, st = L.ptr_array([16]), L.i64_array([4096])
+    M, N, V = 8192, 4096, 128256
+
+    def call(status, n_dy=1, x_stride=N, rstd=None, y=None, n=N, ib=8, out_dtype=L.KP_DTYPE_F32, ws=None, wsb=0):
+        _expect(lib, status, fn, dy, st, n_dy, 32, x_stride, rstd, 48, n, n, 64, n, y, n, None, 80, None, 1, M, n,
+                1e-5, 96, ib, V, -1, 112, out_dtype, 1, ws, wsb, None, None)
+
+    call(L.KP_EINVAL, n_dy=0)                      # no dy terms
+    call(L.KP_EINVAL, ib=3)                        # 3-byte ids
+    call(L.KP_EINVAL, out_dtype=7)                 # unknown table dtype
+    call(L.KP_EINVAL, rstd=128, y=144)             # y is the forward's: not with a saved rstd
+    call(L.KP_EUNSUPPORTED, n=1000)                # no fused row pass for N = 1000
+    call(L.KP_EUNSUPPORTED, x_stride=N + 4)        # rows not 16-byte aligned
+    need = lib.kp_rmsnorm_embedding_bwd_workspace_size(M, N, V)
+    assert need > lib.kp_embedding_bwd_workspace_size(M, V, N)  # + the weight-gradient partial rows
+    call(L.KP_EWORKSPACE, ws=256, wsb=need - 1)    # one byte short
+
+
 def test_embedding_rmsnorm_validation(lib):
     fn = "kp_embedding_rmsnorm_fwd_bf16"
     _expect(lib, L.KP_EINVAL, fn, 16, 100, 64, 32, 3, 8, None, 64, 64, None, 64, 48, 64, None, 64, 1e-5, None, None)
