@@ -38,6 +38,9 @@ BASELINE.json configurations:
   cefb cross-entropy fwd+bwd  logits [8192, 128256] bf16, targets -> bf16 grad, one pass (v5/fb5b36393cbd)
   nfb  RMSNorm fwd + bwd      x, 3 dy, res [8192, 4096] -> y, g, dw in one row pass (v6/0b493aad68f0)
   nfb2 the same as the forward kernel then the backward kernel (the composition nfb replaces)
+  nec  RMSNorm fwd + bwd -> embedding bwd  x, 3 dy, res [8192, 4096], ids [8192] -> y, dw, table fp32 [128256, 4096],
+       g summed into the table in registers (v6/0b493aad68f0)
+  nec2 the same as the norm's row pass writing g, then the embedding backward reading it (what nec replaces)
 
 Each step uses one of R rotating copies of its inputs/outputs (R * bytes >=
 ~1 GiB, several times the 256 MiB Infinity Cache) so that a call does not
@@ -697,7 +700,102 @@ class NormFwdBwd(Workload):
         torch_ref.rms_norm_bwd(self.x, dy, self.w, 1e-5)
 
 
+class NormEmbChain(Workload):
+    """The whole chain of v6/0b493aad68f0 (problem.py:16-71) at its shape: the
+    RMSNorm forward + backward of x [8192, 4096] with three gradient terms and
+    the residual, and the dense embedding backward of g = add_220 + dx over
+    ids [8192] drawn from 100 values (the fragment's get_inputs) into an fp32
+    [128256, 4096] table.  fused=True: kp_rmsnorm_embedding_bwd_bf16 (the ids
+    sorted first, the norm's row pass summing g into the table in registers:
+    g never stored); fused=False: kp_rmsnorm_fwd_bwd_bf16 writing g, then
+    kp_embedding_bwd_bf16 reading it back.  bytes_per_call is the fragment's
+    algorithmic bytes for both (2 x 67 MB less than the composition moves)."""
+
+    def __init__(self, dev, M=8192, N=4096, V=128256, fused=True, name="nec"):
+        super().__init__(dev)
+        import torch
+        from kernelproblems_amd import _lib as L
+        self.name = name
+        g = _gen(0)
+        self.x = _randn((M, N), g)
+        self.dys = [_randn((M, N), g) for _ in range(3)]
+        self.res = _randn((M, N), g)
+        self.w = _randn(N, g, 1.0, 0.02)
+        self.ids = torch.randint(0, 100, (M,), generator=g)
+        eps = 1e-5
+        nb = M * N * 2
+        self.bytes_per_call = 6 * nb + V * N * 4 + M * 8 + N * 2 + N * 4
+        # the timing hook spans the embedding pipeline's first to last launch (the fused
+        # row pass included for nec); for nec2 the norm pass runs ahead of that span
+        self.dominant_bytes = self.bytes_per_call - N * 4 if fused else V * N * 4 + nb + M * 8
+        self.dominant_kernel = ("sort .. row pass .. combine (span)" if fused
+                                else "embedding backward of the stored g (span)")
+        self.probe_mix = None
+        self.description = (f"RMSNorm fwd + bwd -> embedding bwd chain of v6/0b493aad68f0: x, 3 dy terms, residual "
+                            f"[{M},{N}] bf16, ids [{M}] in [0, 100) -> y bf16, dw fp32, table fp32 [{V},{N}]; "
+                            + ("one row pass over sorted-id windows, g kept in registers" if fused
+                               else "norm row pass writing g, then the embedding backward reading it"))
+        lib = L.lib()
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        R = max(2, math.ceil(MIN_ROTATION_BYTES / (6 * nb)))  # rotate the row inputs; the tables are 2.1 GB each
+        xd, wd, rd, idd = self.x.to(dev), self.w.to(dev), self.res.to(dev), self.ids.to(dev)
+        dyd = [d.to(dev) for d in self.dys]
+        tables = [torch.empty((V, N), dtype=torch.float32, device=dev) for _ in range(2)]
+        if fused:
+            ws_bytes = int(lib.kp_rmsnorm_embedding_bwd_workspace_size(M, N, V))
+        else:
+            ws_bytes = int(lib.kp_rmsnorm_fwd_bwd_workspace_size(M, N))
+            ews_bytes = int(lib.kp_embedding_bwd_workspace_size(M, V, N))
+        for r in range(R):
+            xs, rs, ids = xd.clone(), rd.clone(), idd.clone()
+            dys = [d.clone() for d in dyd]
+            y = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+            dw = torch.empty(N, dtype=torch.float32, device=dev)
+            table = tables[r % 2]
+            ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+            dpa, dsa = L.ptr_array([d.data_ptr() for d in dys]), L.i64_array([N] * 3)
+            keep = (xs, rs, ids, dys, y, dw, table, ws, dpa, dsa, wd)
+            if fused:
+                args = (dpa, dsa, 3, xs.data_ptr(), N, None, wd.data_ptr(), N, N, rs.data_ptr(), N, y.data_ptr(), N,
+                        None, dw.data_ptr(), None, 1, M, N, eps, ids.data_ptr(), 8, V, -1, table.data_ptr(),
+                        L.KP_DTYPE_F32, 1, ws.data_ptr(), ws_bytes, None, stream)
+                self.sets.append((lib.kp_rmsnorm_embedding_bwd_bf16, args, keep))
+            else:
+                gout = torch.empty((M, N), dtype=torch.bfloat16, device=dev)
+                ews = torch.empty(ews_bytes, dtype=torch.uint8, device=dev)
+                xpa, xsa = L.ptr_array([xs.data_ptr()]), L.i64_array([N])
+                na = (dpa, dsa, 3, xpa, xsa, 1, wd.data_ptr(), N, N, None, N, y.data_ptr(), N, None,
+                      rs.data_ptr(), N, gout.data_ptr(), N, dw.data_ptr(), None, 1, M, N, eps, ws.data_ptr(),
+                      ws_bytes, stream)
+                ea = (gout.data_ptr(), N, ids.data_ptr(), 8, M, V, N, -1, 0, table.data_ptr(), L.KP_DTYPE_F32, 1,
+                      ews.data_ptr(), ews_bytes, None, stream)
+
+                def both(na=na, ea=ea):
+                    st = lib.kp_rmsnorm_fwd_bwd_bf16(*na)
+                    return st if st != 0 else lib.kp_embedding_bwd_bf16(*ea)
+                both.__name__ = "kp_rmsnorm_fwd_bwd_bf16 + kp_embedding_bwd_bf16"
+                self.sets.append((both, (), keep + (gout, ews, xpa, xsa)))
+        self.cpu_rows = 256
+        self.cpu_bytes = self.cpu_rows * 6 * N * 2
+        self.cpu_sample = (f"the norm forward + backward of {self.cpu_rows} of the {M} rows and their table "
+                           f"rows' segment sums (rate from the sample's own row bytes)")
+
+    def cpu_run(self):
+        import torch
+        from oracle import torch_ref
+        k = self.cpu_rows
+        torch_ref.rms_norm_fwd(self.x[:k], self.w, 1e-5)
+        dy = self.dys[0][:k] + self.dys[1][:k] + self.dys[2][:k]
+        dx, _ = torch_ref.rms_norm_bwd(self.x[:k], dy, self.w, 1e-5)
+        g = (self.res[:k].float() + dx.float()).to(torch.bfloat16)
+        torch.zeros(100, g.shape[1]).index_add_(0, self.ids[:k], g.float())
+
+
 def make_workload(name, dev):
+    if name == "nec":
+        return NormEmbChain(dev, fused=True, name="nec")
+    if name == "nec2":
+        return NormEmbChain(dev, fused=False, name="nec2")
     if name == "nfb":
         return NormFwdBwd(dev, one_pass=True, name="nfb")
     if name == "nfb2":
@@ -738,7 +836,7 @@ def make_workload(name, dev):
 
 
 ALL = ["c1", "c2", "c3f", "c3b", "c3n", "c4", "c64r", "c5f", "c5b", "swf", "swb", "silu", "swfb", "cef", "ceb",
-       "cefb", "nfb", "nfb2"]
+       "cefb", "nfb", "nfb2", "nec", "nec2"]
 # The BASELINE.json configurations: every default run measures each of them.
 CONFIGS = ["c1", "c2", "c3f", "c3b", "c4", "c5f", "c5b"]
 
