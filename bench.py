@@ -221,6 +221,7 @@ class RmsBwd(Workload):
         self.bytes_per_call = self.dominant_bytes + N * 4
         self.dominant_kernel = "rms_bwd_vec"
         self.probe_mix = (n_in, 1, M * N * 2, M * N * 2, f"{n_in} reads + 1 write of {M * N * 2 / 1e6:.1f} MB")
+        self.timeline = True  # the row kernel records a block timeline (kp_debug_block_trace)
         if residual:
             self.description = (f"C5 residual add + RMSNorm backward: x, res, dy [{M},{N}] bf16 -> dx bf16, dw fp32 "
                                 f"(h, rstd recomputed; eps={eps})")
@@ -912,6 +913,72 @@ def measure_gpu(wl, steps, warmup):
     }
 
 
+def measure_timeline(wl, calls=5, warmup=10):
+    """Where the RMSNorm backward's row kernel spends its time, from the block
+    timeline hook (kp_debug_block_trace): each of `calls` calls, amid
+    untraced back-to-back calls, records every row block's start, the end of
+    its rows and the store of its weight-gradient partial row (constant 100
+    MHz clock), and the kernel's own start and end (HIP events stamped by the
+    launch, the hook of measure_gpu).  Per call: rows_done_us (median / max
+    over blocks, from the first block's start), tail_us = max - median,
+    partial_us (the last partial row stored), launch_drain_us = kernel time
+    minus the blocks' span (dispatch before the first block, completion after
+    the last).  Each field is the median over the calls."""
+    import statistics
+    import torch
+    from kernelproblems_amd import _lib as L
+    lib = L.lib()
+    if not getattr(wl, "timeline", False):
+        return None
+    nb = 4096
+    bufs = [torch.zeros(nb * 4, dtype=torch.int64, device=wl.dev) for _ in range(calls)]
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(calls)]
+    for a, b in ev:
+        a.record()
+        b.record()
+    warm_device(wl.dev)
+    i = 0
+    for c in range(calls):
+        for _ in range(warmup):
+            wl.step(i)
+            i += 1
+        lib.kp_debug_block_trace(bufs[c].data_ptr(), nb * 32)
+        lib.kp_profile_dominant_kernel(ev[c][0].cuda_event, ev[c][1].cuda_event)
+        wl.step(i)
+        i += 1
+        lib.kp_profile_dominant_kernel(None, None)
+        lib.kp_debug_block_trace(None, 0)
+    torch.cuda.synchronize()
+    per = []
+    for c in range(calls):
+        rec = bufs[c].view(nb, 4).cpu().tolist()
+        rec = [r for r in rec if r[0] != 0]
+        t0 = min(r[0] for r in rec)
+        rows = sorted((r[1] - t0) / 100.0 for r in rec)
+        ends = [(r[2] - t0) / 100.0 for r in rec]
+        kernel_us = ev[c][0].elapsed_time(ev[c][1]) * 1e3
+        xcc = {}
+        for r in rec:
+            xcc.setdefault(int(r[3]), []).append((r[1] - t0) / 100.0)
+        med = statistics.median(rows)
+        per.append({
+            "blocks": len(rec),
+            "start_spread_us": (max(r[0] for r in rec) - t0) / 100.0,
+            "rows_done_median_us": med,
+            "rows_done_max_us": rows[-1],
+            "tail_us": rows[-1] - med,
+            "partial_stored_max_us": max(ends),
+            "kernel_us": kernel_us,
+            "launch_drain_us": kernel_us - max(ends),
+            "rows_done_mean_by_xcc_us": {str(k): statistics.mean(v) for k, v in sorted(xcc.items())},
+        })
+    out = {k: round(statistics.median(p[k] for p in per), 2) for k in per[0] if k != "rows_done_mean_by_xcc_us"}
+    out["rows_done_mean_by_xcc_us"] = {k: round(statistics.median(p["rows_done_mean_by_xcc_us"][k] for p in per), 2)
+                                       for k in per[0]["rows_done_mean_by_xcc_us"]}
+    out["calls"] = calls
+    return out
+
+
 def measure_dropin(wl, steps, warmup):
     """The tensor-level drop-in (fused.*) on the same rotating inputs: what a
     caller of the reference's boundary pays per call, with outputs and
@@ -1319,6 +1386,13 @@ def main():
             st = measure_gpu(wl, STEADY_STEPS, args.warmup)
             r["steady"] = {"steps": STEADY_STEPS, "us_per_call": round(st["ms_per_step"] * 1e3, 3),
                            "GBps": round(st["value"], 1), "kernel_us": round(st["dominant_ms"] * 1e3, 3)}
+        r["timeline"] = measure_timeline(wl)
+        if r["timeline"]:
+            t = r["timeline"]
+            print(f"[bench] {name}: block timeline (median of {t['calls']} calls): rows done median "
+                  f"{t['rows_done_median_us']:.1f} us, max {t['rows_done_max_us']:.1f} us (tail {t['tail_us']:.1f}), "
+                  f"partial rows stored {t['partial_stored_max_us']:.1f} us, kernel {t['kernel_us']:.1f} us "
+                  f"(launch + drain {t['launch_drain_us']:.1f})", file=sys.stderr, flush=True)
         r["dropin"] = None if args.no_dropin else measure_dropin(wl, args.steps, args.warmup)
         if r["dropin"]:
             d = r["dropin"]
@@ -1369,6 +1443,7 @@ def main():
             "bytes_per_call": wl.bytes_per_call,
             "roofline": roofline(name, wl, r),
             "steady": r["steady"],
+            "timeline": r["timeline"],
             "dropin": r["dropin"],
             "cpu_baseline": cpu,
         }

@@ -67,6 +67,18 @@ const char* kp_last_error_message(void);
  * Pass NULL, NULL to clear.  Per calling thread. */
 void kp_profile_dominant_kernel(void* start_event, void* stop_event);
 
+/* Block timeline hook (measurement only; no counterpart in the reference).
+ * While set, the vectorized RMSNorm backward row kernel (the dominant kernel
+ * of kp_rmsnorm_bwd_bf16, its allocation-free form and kp_rmsnorm_fwd_bwd_bf16
+ * on 16-byte rows of N a multiple of 512) writes, for each row block b below
+ * bytes / 32, four 64-bit words starting at word 4 b of buf: the device's
+ * constant 100 MHz clock (s_memrealtime) when the block
+ * starts, when its last row's stores have completed, and when its
+ * weight-gradient partial row has been stored, then the XCC id the block ran
+ * on.  buf is device memory; pass NULL (or bytes < 32) to clear.  Per calling
+ * thread, like kp_profile_dominant_kernel. */
+void kp_debug_block_trace(void* buf, size_t bytes);
+
 /* ------------------------------------------------------------------------
  * RMSNorm forward, optionally fused with the residual add in front of it.
  *

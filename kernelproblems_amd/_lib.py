@@ -66,6 +66,7 @@ SIGNATURES = {
     "kp_last_hip_error": (i32, []),
     "kp_last_error_message": (C.c_char_p, []),
     "kp_profile_dominant_kernel": (None, [vp, vp]),
+    "kp_debug_block_trace": (None, [vp, sz]),
     "kp_rmsnorm_fwd_bf16": (
         i32,
         [pvp, pi64, i32, vp, i64, i64, vp, i64, vp, i64, vp, i64, i64, f32, vp],

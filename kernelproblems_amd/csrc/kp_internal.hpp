@@ -21,6 +21,12 @@ int cu_count();
 hipEvent_t prof_start_event();
 hipEvent_t prof_stop_event();
 
+// Block timeline hook (kp_debug_block_trace): the caller's buffer, or nullptr,
+// and how many blocks' records (kBlockTraceWords 64-bit words each) it holds.
+constexpr int kBlockTraceWords = 4;
+unsigned long long* block_trace_buf();
+int block_trace_blocks();
+
 // Launches an entry point's dominant kernel.  With timing events set, the
 // launch goes through hipExtLaunchKernel, which stamps the events at the
 // kernel's own start and completion, so they time that kernel alone.

@@ -410,6 +410,8 @@ int rms_bwd_impl(const char* who, const void* const* dy_terms, const int64_t* dy
   a.dx = static_cast<uint16_t*>(dx);
   a.dxs = dx_stride;
   a.partial = want_dw ? static_cast<float*>(workspace) : nullptr;
+  a.trace = block_trace_buf();
+  a.trace_blocks = a.trace ? block_trace_blocks() : 0;
   a.M = M;
   a.N = N;
   a.eps = eps;

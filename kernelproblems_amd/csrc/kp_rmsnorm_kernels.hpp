@@ -70,6 +70,10 @@ struct RmsBwdArgs {
   float* rstd_out;
   int64_t M, N;
   float eps;
+  // Block timeline (kp_debug_block_trace): 4 words per block for blocks below
+  // trace_blocks, or nullptr.
+  unsigned long long* trace;
+  int trace_blocks;
 };
 
 // Weight-gradient partials are stored column-chunk-major, [ceil(N/16)][P][16]
@@ -434,12 +438,30 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
 // Grid-stride over row groups with one group of loads in flight, in two named
 // register slots (see rms_fwd_vec).  NW waves per block (4 or 8): RB = NW / WPR
 // rows per block step; every block owns one weight-gradient partial row.
+// The block's timeline record (kp_debug_block_trace): start, rows done,
+// partial row stored (constant 100 MHz clock), XCC id; written by thread 0.
+__device__ __forceinline__ void trace_block(const RmsBwdArgs& a, unsigned long long t_start,
+                                            unsigned long long t_rows) {
+  __builtin_amdgcn_s_waitcnt(0);
+  const unsigned long long t_end = __builtin_amdgcn_s_memrealtime();
+  if (threadIdx.x == 0 && (int)blockIdx.x < a.trace_blocks) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    unsigned long long* d = a.trace + (size_t)blockIdx.x * 4;
+    d[0] = t_start;
+    d[1] = t_rows;
+    d[2] = t_end;
+    d[3] = xcc;
+  }
+}
+
 template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD>
 __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   constexpr int RB = NW / WPR;
   constexpr int SEG = 512 * VPL;
   extern __shared__ float smem[];  // [RB / 2][WPR][SEG] weight-gradient combine (only when a.partial)
   __shared__ float red[2][NW][2];
+  const unsigned long long t_start = a.trace != nullptr ? __builtin_amdgcn_s_memrealtime() : 0ull;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int part = wave % WPR, rloc = wave / WPR;
   const int64_t col = (int64_t)part * SEG + lane * 8;
@@ -491,8 +513,16 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
 #undef KP_ROW
 #undef KP_LOAD
 #undef KP_PROC
+  unsigned long long t_rows = 0;
+  if (a.trace != nullptr) {
+    __builtin_amdgcn_s_waitcnt(0);
+    t_rows = __builtin_amdgcn_s_memrealtime();
+  }
 
-  if (a.partial == nullptr) return;
+  if (a.partial == nullptr) {
+    if (a.trace != nullptr) trace_block(a, t_start, t_rows);
+    return;
+  }
   // Combine the column partials of the RB waves that share a column segment
   // with a fixed pairwise tree (level `step`: rloc r += rloc r + step), through
   // [RB / 2][WPR][SEG] floats of LDS, then write one partial row per block.
@@ -512,6 +542,7 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
       *reinterpret_cast<f32x4*>(pp + 4) = f32x4{acc[i * 8 + 4], acc[i * 8 + 5], acc[i * 8 + 6], acc[i * 8 + 7]};
     }
   }
+  if (a.trace != nullptr) trace_block(a, t_start, t_rows);
 }
 
 
