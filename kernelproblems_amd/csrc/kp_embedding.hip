@@ -382,10 +382,10 @@ __device__ __forceinline__ int64_t row_of(const EmbBwdArgs& a, int64_t r) { retu
 __device__ __forceinline__ int clamp_pos(int v, int n_valid) { return v < 0 ? 0 : (v > n_valid ? n_valid : v); }
 
 // Where a finished piece [p0, p1) of the run [lo, hi) inside window [w0, w1) goes.
-__device__ __forceinline__ void emit_piece(const EmbBwdArgs& a, int64_t w, int64_t w0, int64_t w1, int lo, int hi,
-                                           int64_t c, const f32x4& acc) {
+// `row` is the run's id (sid[lo]), read only when the run lies in the window.
+__device__ __forceinline__ void emit_piece_row(const EmbBwdArgs& a, int64_t w, int64_t w0, int64_t w1, int lo, int hi,
+                                               int64_t c, const f32x4& acc, int64_t row) {
   if (lo >= w0 && hi <= w1) {
-    const int64_t row = row_of(a, lo);
     if (row < a.V) store_out4(a, row, c, acc);
   } else {
     const int slot = lo < w0 ? 0 : 1;  // 0: continues from an earlier window; 1: run starts here
@@ -416,32 +416,47 @@ __device__ void emb_do_window(const EmbBwdArgs& a, int64_t w, int64_t q, int n_v
     constexpr int U = 16;
     const int64_t col = q * kColStep + threadIdx.x * 4;
     const bool on = col < a.D;
-    int lo = min(clamp_pos(a.run_lo[w0], n_valid), (int)w0);
-    int hi = max(clamp_pos(a.run_hi[w0], n_valid), (int)w0 + 1);
-    float cnt = (float)(hi - lo);
+    // Lane i < np holds position w0 + i's token, run bounds and id, fetched
+    // in one batch and read as scalars (readlane) by the loop: a window of
+    // many short runs would otherwise wait for one dependent load of its
+    // bounds (and one of its id) per run.
+    const int np = (int)(w1 - w0);  // 1..kWin
+    const int lane = threadIdx.x & 63;
+    const int64_t pl = w0 + (lane < np ? lane : np - 1);
+    const int tok_l = (int)token_of(a, pl);
+    const int lo_l = clamp_pos(a.run_lo[pl], n_valid);
+    const int hi_l = clamp_pos(a.run_hi[pl], n_valid);
+    const int id_l = (int)a.sid[pl];
+    int lo = (int)w0, hi = (int)w0;  // hi == w0: a run starts at the first position
+    float cnt = 1.f;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    for (int64_t r0 = w0; r0 < w1; r0 += U) {
+    for (int k0 = 0; k0 < np; k0 += U) {
       u32x2 v[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const bool have = r0 + u < w1;
-        const int64_t t = have ? token_of(a, r0 + u) : 0;
+        const bool have = k0 + u < np;
+        const int64_t t = have ? (int64_t)__builtin_amdgcn_readlane(tok_l, k0 + u) : 0;
         v[u] = (have && on) ? ld8_stream(a.grad + t * a.grs + col) : u32x2{0u, 0u};
       }
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int64_t r = r0 + u;
-        if (r < w1) {
+        const int k = k0 + u;
+        const int r = (int)w0 + k;
+        if (k < np) {
           if (r == hi) {  // a new run starts at r
-            lo = min(clamp_pos(a.run_lo[r], n_valid), (int)r);
-            hi = max(clamp_pos(a.run_hi[r], n_valid), (int)r + 1);
+            lo = min(__builtin_amdgcn_readlane(lo_l, k), r);
+            hi = max(__builtin_amdgcn_readlane(hi_l, k), r + 1);
             cnt = (float)(hi - lo);
             acc = f32x4{0.f, 0.f, 0.f, 0.f};
           }
           f32x4 f = {bf_lo(v[u][0]), bf_hi(v[u][0]), bf_lo(v[u][1]), bf_hi(v[u][1])};
           if (a.scale) f = f32x4{f[0] / cnt, f[1] / cnt, f[2] / cnt, f[3] / cnt};
           acc += f;
-          if ((r + 1 == hi || r + 1 == w1) && on) emit_piece(a, w, w0, w0 + kWin, lo, hi, col, acc);
+          if (r + 1 == hi || r + 1 == (int)w1) {
+            // the run's id: lane lo - w0 when the run starts in this window (a final row)
+            const int64_t row = lo >= w0 ? (int64_t)(uint32_t)__builtin_amdgcn_readlane(id_l, lo - (int)w0) : 0;
+            if (on) emit_piece_row(a, w, w0, w0 + kWin, lo, hi, col, acc, row);
+          }
         }
       }
     }

@@ -184,3 +184,37 @@ def test_row_layouts_give_the_contiguous_bits(gpu):
         assert y.shape == xv.shape and dx.shape == xv.shape, name
         assert torch.equal(y.reshape(M, N), y0) and torch.equal(r, r0), name
         assert torch.equal(dx.reshape(M, N), dx0) and torch.equal(dw, dw0), name
+
+
+@pytest.mark.parametrize("M, N, residual", [(8192, 4096, False), (4096, 8192, True), (1000, 4096, False)])
+def test_block_trace_hook_records_every_block_and_changes_nothing(gpu, M, N, residual):
+    """kp_debug_block_trace: with the hook set, every row block of the
+    backward's row kernel writes (start <= rows done <= partial stored, XCC id
+    < 8) and nothing past its records; dx and dw are bitwise those of an
+    untraced call."""
+    from kernelproblems_amd import _lib as L
+    print(f"[rmsnorm] block trace hook M={M} N={N} residual={residual}", flush=True)
+    g = gen(21)
+    x = randn_bf16((M, N), g).to(gpu)
+    dy = randn_bf16((M, N), g).to(gpu)
+    w = randn_bf16(N, g, 1.0, 0.02).to(gpu)
+    res = randn_bf16((M, N), g).to(gpu) if residual else None
+    dx0, dw0 = kp.rms_norm_backward([dy], [x], None, w, 1e-5, N, dx_residual=res)
+    cap = 4096
+    buf = torch.zeros(cap * 4 + 64, dtype=torch.int64, device=gpu)
+    lib = L.lib()
+    lib.kp_debug_block_trace(buf.data_ptr(), cap * 32)
+    try:
+        dx1, dw1 = kp.rms_norm_backward([dy], [x], None, w, 1e-5, N, dx_residual=res)
+    finally:
+        lib.kp_debug_block_trace(None, 0)
+    torch.cuda.synchronize()
+    assert torch.equal(dx0.view(torch.int16), dx1.view(torch.int16))
+    assert torch.equal(dw0.view(torch.int32), dw1.view(torch.int32))
+    rec = buf[: cap * 4].view(cap, 4).cpu()
+    n = int((rec[:, 0] != 0).sum())
+    assert n > 0 and bool((rec[:n, 0] != 0).all()) and bool((rec[n:] == 0).all()), "records must be the first n"
+    r = rec[:n]
+    assert bool((r[:, 0] <= r[:, 1]).all()) and bool((r[:, 1] <= r[:, 2]).all())
+    assert bool((r[:, 3] >= 0).all()) and bool((r[:, 3] < 8).all())
+    assert bool((buf[cap * 4:] == 0).all()), "nothing may be written past the records"
