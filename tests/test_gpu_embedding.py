@@ -10,7 +10,8 @@ from tests._util import bf, gen, randn_bf16, to_u16, ulp_bf16, zipf_ids
 pytestmark = pytest.mark.gpu
 
 
-@pytest.mark.parametrize("V,D,T", [(1000, 4096, 777), (50, 64, 300), (128256, 4096, 2048), (300, 100, 129)])
+@pytest.mark.parametrize("V,D,T", [(1000, 4096, 777), (50, 64, 300), (128256, 4096, 2048), (300, 100, 129),
+                                   (300, 4608, 257), (70, 8192, 65)])
 @pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
 def test_embedding_fwd_bit_exact(gpu, oracle_lib, V, D, T, idx_dtype):
     g = gen(V + D + T)
@@ -41,6 +42,32 @@ def test_embedding_fwd_out_of_range_flagged(gpu):
     ids = torch.tensor([1, 10, 3], device=gpu)
     with pytest.raises(IndexError):
         kp.embedding(table, ids)
+
+
+@pytest.mark.parametrize("D", [4096, 4608])
+@pytest.mark.parametrize("idx_dtype", [torch.int64, torch.int32])
+def test_embedding_fwd_out_of_range_rows_zero_vector_path(gpu, oracle_lib, D, idx_dtype):
+    """Out-of-range ids (negative, V, far above V) in the 16-byte path: those
+    rows come out zero, every other row bit-exact, and the id is recorded."""
+    g = gen(D + 5)
+    V, T = 500, 300
+    table = randn_bf16((V, D), g, 0.0, 0.02)
+    ids = zipf_ids(T, V, 1.1, g)
+    bad_pos = [0, 7, 150, T - 1]
+    ids[bad_pos[0]], ids[bad_pos[1]], ids[bad_pos[2]], ids[bad_pos[3]] = -1, V, V + 100000, -(2 ** 30)
+    kp.set_index_checking(False)
+    try:
+        kp.check_indices()
+        out = kp.embedding(table.to(gpu), ids.to(idx_dtype).to(gpu))
+        with pytest.raises(IndexError):
+            kp.check_indices()
+    finally:
+        kp.set_index_checking(True)
+    got = to_u16(out).reshape(T, D)
+    assert not got[bad_pos].any()
+    good = np.setdiff1d(np.arange(T), bad_pos)
+    exp, _ = oracle_lib.embedding_fwd(to_u16(table), ids.clamp(0, V - 1).numpy())
+    assert np.array_equal(got[good], exp[good])
 
 
 def test_out_of_range_recorded_without_checking_mode(gpu):
