@@ -133,6 +133,20 @@ __device__ __forceinline__ void load_raw(RawRow<VPL, NT>& r, const uint16_t* con
   }
 }
 
+// The same with cacheable loads, for gathered rows: Zipf-repeated ids re-read
+// the same table rows, which L2 / MALL then serve (at C3 the non-temporal
+// loads above took the fused gather + norm 42.3 us, these 34.1 us).
+template <int VPL, int NT>
+__device__ __forceinline__ void load_raw_cached(RawRow<VPL, NT>& r, const uint16_t* const (&base)[3],
+                                                const int64_t (&strides)[3], int64_t row, int64_t col) {
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    const uint16_t* p = base[t] + row * strides[t] + col;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) r.v[t][i] = ld16(p + i * 512);
+  }
+}
+
 // bf16 running sum of the terms, each add rounded as an eager bf16 add.Tensor.
 template <int VPL, int NT>
 __device__ __forceinline__ void sum_raw(u32x4 (&out)[VPL], const RawRow<VPL, NT>& r) {
@@ -217,11 +231,25 @@ __device__ __forceinline__ void fwd_row(const RmsFwdArgs& a, const RawRow<VPL, N
 // separate named variables, and the loop is unrolled two steps per pass so
 // that no slot is ever copied: an array of slots indexed by the step ends up
 // in scratch memory, and a slot copy makes the wave wait for the prefetch.
-// The source row of a gathered row: ids[row] when in [0, idx_rows), else row
-// 0 (always readable) with ok = false.  row is wave-uniform: a scalar load.
-__device__ __forceinline__ int64_t gather_src(const RmsFwdArgs& a, int64_t row, bool& ok) {
-  const int64_t id = a.idx_bytes == 8 ? static_cast<const int64_t*>(a.idx)[row]
-                                      : (int64_t) static_cast<const int32_t*>(a.idx)[row];
+// Gathered rows: lane j of a wave holds the id of the wave's row at step
+// kb + j (kb a multiple of 64), fetched by one vector load per 64 steps; a
+// step reads its id with readlane.  Read inside the row loop instead, the id
+// was a vector load (the loop's stores might alias it) whose wait drained the
+// other slot's prefetched row loads as well.
+__device__ __forceinline__ int64_t gather_fetch(const RmsFwdArgs& a, int64_t kb, int64_t nb, int64_t b, int64_t G,
+                                                int RB, int rloc, int lane) {
+  const int64_t k = kb + lane < nb ? kb + lane : nb - 1;
+  const int64_t row = clamp_row((b + k * G) * RB + rloc, a.M);
+  return a.idx_bytes == 8 ? static_cast<const int64_t*>(a.idx)[row]
+                          : (int64_t) static_cast<const int32_t*>(a.idx)[row];
+}
+// The source row of step k: the id when in [0, idx_rows), else row 0 (always
+// readable) with ok = false.
+__device__ __forceinline__ int64_t gather_src(const RmsFwdArgs& a, int64_t idl, int64_t k, bool& ok) {
+  const int j = (int)(k & 63);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)idl, j);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)idl >> 32), j);
+  const int64_t id = (int64_t)(((uint64_t)hi << 32) | lo);
   ok = id >= 0 && id < a.idx_rows;
   return ok ? id : 0;
 }
@@ -255,10 +283,15 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   bool s0ok = true, s1ok = true;
   int it = 0;
 #define KP_ROW(g) ((g) * RB + rloc)
-#define KP_LOAD(S, g)                                                                                 \
+#define KP_LOAD(S, g, kk)                                                                             \
   {                                                                                                   \
-    const int64_t row_ = clamp_row(KP_ROW(g), a.M);                                                   \
-    load_raw<VPL, NX>(S, a.x, a.xs, GATHER ? gather_src(a, row_, S##ok) : row_, col);                 \
+    int64_t src_ = clamp_row(KP_ROW(g), a.M);                                                         \
+    if constexpr (GATHER) {                                                                           \
+      if ((kk) > 0 && ((kk) & 63) == 0) idl = gather_fetch(a, (kk), nb, blockIdx.x, G, RB, rloc, lane); \
+      src_ = gather_src(a, idl, (kk), S##ok);                                                         \
+    }                                                                                                 \
+    if constexpr (GATHER) load_raw_cached<VPL, NX>(S, a.x, a.xs, src_, col);                          \
+    else load_raw<VPL, NX>(S, a.x, a.xs, src_, col);                                                  \
   }                                                                                                   \
   __builtin_amdgcn_sched_barrier(0)
 #define KP_PROC(S, g)                                                                               \
@@ -267,16 +300,18 @@ __global__ __launch_bounds__(kThreads) void rms_fwd_vec(RmsFwdArgs a) {
   // Exact trip count: the grid never exceeds the row-group count, so every
   // block owns nb >= 1 groups and nothing is prefetched past its last one.
   const int64_t nb = block_trips(ngroups, blockIdx.x, G);
+  int64_t idl = 0;
+  if constexpr (GATHER) idl = gather_fetch(a, 0, nb, blockIdx.x, G, RB, rloc, lane);
   int64_t g = blockIdx.x, k = 0;
-  KP_LOAD(s0, g);
+  KP_LOAD(s0, g, 0);
   for (; k + 2 < nb; k += 2, g += 2 * G) {
-    KP_LOAD(s1, g + G);
+    KP_LOAD(s1, g + G, k + 1);
     KP_PROC(s0, g);
-    KP_LOAD(s0, g + 2 * G);
+    KP_LOAD(s0, g + 2 * G, k + 2);
     KP_PROC(s1, g + G);
   }
   if (k + 1 < nb) {
-    KP_LOAD(s1, g + G);
+    KP_LOAD(s1, g + G, k + 1);
     KP_PROC(s0, g);
     KP_PROC(s1, g + G);
   } else {

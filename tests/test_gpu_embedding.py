@@ -266,6 +266,24 @@ def test_embedding_rms_norm_equals_the_two_launch_composition(gpu, V, D, T, idx_
     assert (ulp_bf16(to_u16(y), yo) <= 1).all()
 
 
+def test_embedding_rms_norm_long_block_walk(gpu):
+    """1.2M tokens of width 512: each block walks ~150 row steps, so the
+    ids it holds in lanes (64 steps at a time) are fetched again twice;
+    h, y and rstd bit for bit those of embedding() then rms_norm()."""
+    V, D, T = 1000, 512, 1_200_000
+    print(f"[emb+rms long] V={V} D={D} T={T}", flush=True)
+    g = torch.Generator().manual_seed(12)
+    table = (torch.randn(V, D, generator=g) * 0.5).to(torch.bfloat16).to(gpu)
+    w = (1 + 0.02 * torch.randn(D, generator=g)).to(torch.bfloat16).to(gpu)
+    ids = torch.randint(0, V, (T,), generator=g, dtype=torch.int32).to(gpu)
+    h, y, r = kp.embedding_rms_norm(table, ids, w, 1e-5, return_h=True)
+    emb = kp.embedding(table, ids)
+    assert torch.equal(h, emb)
+    del h
+    _, y2, r2 = kp.rms_norm([emb], w, 1e-5, D)
+    assert torch.equal(y, y2) and torch.equal(r, r2.view(r.shape))
+
+
 def test_embedding_rms_norm_fsdp_weight_and_bad_ids(gpu):
     """Weight as an [8, 512] row-strided view of a flat buffer; ids outside
     [0, V) give zero h / y rows and raise with index checking on."""
