@@ -91,8 +91,23 @@ __device__ __forceinline__ void combine_dpp(float& R, float& s) {
   combine(R, s, dpp_f<CTRL>(R), dpp_f<CTRL>(s));
 }
 
+// The row's target and the raw bf16 logit at it, requested by the row's wave
+// before its data loads: the target is then a scalar load ahead of any store,
+// and the logit's wait, at the end of the row, does not sit behind the row's
+// stores (loaded after them, the two formed a chain of full waits on the
+// kernel's last wave generation).  An id outside [0, V) reads column 0.
+struct FwdTarget {
+  int64_t t;
+  uint16_t xt;
+};
+__device__ __forceinline__ FwdTarget row_target(const FwdArgs& a, int64_t row) {
+  const int64_t t = target_at(a.targets, a.tbytes, row);
+  const bool in = t >= 0 && t < a.V;
+  return FwdTarget{t, a.logits[row * a.rs + (in ? t : 0)]};
+}
+
 // Row-wave epilogue: reduce the lanes' states, then lane 0 writes the row's loss.
-__device__ __forceinline__ void finish_row(const FwdArgs& a, int64_t row, float R, float s) {
+__device__ __forceinline__ void finish_row(const FwdArgs& a, int64_t row, FwdTarget rt, float R, float s) {
   combine_dpp<0xB1>(R, s);   // quad_perm [1,0,3,2]
   combine_dpp<0x4E>(R, s);   // quad_perm [2,3,0,1]
   combine_dpp<0x141>(R, s);  // row_half_mirror
@@ -105,13 +120,13 @@ __device__ __forceinline__ void finish_row(const FwdArgs& a, int64_t row, float 
   if ((threadIdx.x & (kWave - 1)) != 0) return;
   const double lse = ((double)r0 + log2((double)s0)) / (double)kLog2e;
   if (a.lse_out) a.lse_out[row] = (float)lse;
-  const int64_t t = target_at(a.targets, a.tbytes, row);
+  const int64_t t = rt.t;
   int valid = t != a.ignore;
   if (valid && (t < 0 || t >= a.V)) {
     valid = 0;
     if (a.err) a.err[0] = 1;
   }
-  a.row_loss[row] = valid ? lse - (double)bf_to_f(a.logits[row * a.rs + t]) : 0.0;
+  a.row_loss[row] = valid ? lse - (double)bf_to_f(rt.xt) : 0.0;
   a.row_valid[row] = valid;
 }
 
@@ -164,8 +179,9 @@ __device__ __forceinline__ void fwd_step(const u32x4* p, int64_t c0, int64_t cpr
 // of a step issued together.  Full steps carry no masks; the tail step's
 // chunks past the row end read the row's first chunk and count as -inf.
 __global__ __launch_bounds__(kThreads) void xent_fwd_vec(FwdArgs a) {
-  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
+  const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   if (row >= a.M) return;
+  const FwdTarget rt = row_target(a, row);
   const int lane = threadIdx.x & (kWave - 1);
   const u32x4* p = reinterpret_cast<const u32x4*>(a.logits + row * a.rs);
   const int64_t cpr = a.V / 8;
@@ -174,13 +190,14 @@ __global__ __launch_bounds__(kThreads) void xent_fwd_vec(FwdArgs a) {
   float R = -INFINITY, s = 0.0f;
   for (int64_t c0 = 0; c0 < full; c0 += kStep) fwd_step<false>(p, c0, cpr, lane, R, s);
   if (full < cpr) fwd_step<true>(p, full, cpr, lane, R, s);
-  finish_row(a, row, R, s);
+  finish_row(a, row, rt, R, s);
 }
 
 // Any row stride / alignment / V: lane l reads elements l, l + 64, ...
 __global__ __launch_bounds__(kThreads) void xent_fwd_scalar(FwdArgs a) {
   const int64_t row = (int64_t)blockIdx.x * kWavesPerBlock + (threadIdx.x >> 6);
   if (row >= a.M) return;
+  const FwdTarget rt = row_target(a, row);
   const int lane = threadIdx.x & (kWave - 1);
   const uint16_t* p = a.logits + row * a.rs;
   float R = -INFINITY, s = 0.0f;
@@ -193,7 +210,7 @@ __global__ __launch_bounds__(kThreads) void xent_fwd_scalar(FwdArgs a) {
     }
     online8(R, s, f);
   }
-  finish_row(a, row, R, s);
+  finish_row(a, row, rt, R, s);
 }
 
 // One block: loss = scale * sum(row_loss), total_weight = sum(row_valid), in a
