@@ -217,8 +217,9 @@ int kp_rmsnorm_fwd_bwd_bf16(const void* const* dy_terms, const int64_t* dy_strid
  * layer buffer).  table: bf16 [V, N] rows (row stride table_row_stride);
  * indices: T integers of index_bytes (4 or 8); weight as in
  * kp_rmsnorm_fwd_bf16; y / h_out: bf16 [T, N] with the given row strides;
- * rstd: fp32 [T] or NULL.  An index outside [0, V) reads nothing: its h and
- * y rows are zero and, when error_flag != NULL, *error_flag is set to 1.
+ * rstd: fp32 [T] or NULL.  An index outside [0, V) contributes nothing (row 0
+ * is read in its place and discarded): its h and y rows are zero and, when
+ * error_flag != NULL, *error_flag is set to 1.
  * Rows, strides and pointers must be 16-byte granular with N a fast-path row
  * length; otherwise KP_EUNSUPPORTED (compose kp_embedding_fwd_bf16 and
  * kp_rmsnorm_fwd_bf16 instead).
@@ -252,8 +253,11 @@ int kp_stream_probe(const void* const* in, int n_in, int64_t in_bytes, void* con
  * Replaces torch.ops.aten.embedding.default at v7/1e49beb8a123/problem.py:23
  * (table = [128256, 4096] view of an FSDP flat buffer, ids i64 [1, 8192]).
  * indices: T integers of index_bytes (4 or 8) each, contiguous.
- * An index outside [0, V) reads nothing: its output row is zero-filled and,
- * when error_flag != NULL, *error_flag is set to 1 (never cleared here).
+ * An index outside [0, V) gives a zero-filled output row (the 16-byte path
+ * reads table row 0 in its place and masks it away) and, when
+ * error_flag != NULL, sets *error_flag to 1 (never cleared here).
+ * One wave per token: T above 4 * (2^31 - 1) tokens on the 16-byte path
+ * returns KP_EUNSUPPORTED.
  */
 int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table_row_stride,
                           const void* indices, int index_bytes, int64_t T,
@@ -367,8 +371,8 @@ int kp_rmsnorm_embedding_bwd_bf16(const void* const* dy_terms, const int64_t* dy
  *   bf16, or as fp32 for tensor i when bit i of out_f32_mask is set (the
  *   fragment v7/0f38bc55457c/problem.py returns its q rotation in fp32);
  *   conj != 0 uses (c, -s) (the backward of the forward rotation).
- * With a table, a position outside [0, freq_rows) reads nothing: its output is
- *   zero and *error_flag (if non-NULL) is set to 1.
+ * With a table, a position outside [0, freq_rows) contributes nothing: its
+ *   output is zero and *error_flag (if non-NULL) is set to 1.
  */
 int kp_rope_bf16(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides, const int64_t* out0_strides,
                  const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,
@@ -409,8 +413,8 @@ int kp_rope_bf16_twice(const void* x0, void* out0, int64_t H0, const int64_t* x0
  *   [B, S, H_i, P] with strides {b, s, h} in complex elements and unit stride
  *   on P.  positions as in kp_rope_bf16 (NULL: position of (b, s) is s).
  *   freqs_cis: complex64 [freq_rows, >= P], row stride in complex elements.
- * A position outside [0, freq_rows) reads nothing: its output is zero and
- * *error_flag (if non-NULL) is set to 1.
+ * A position outside [0, freq_rows) contributes nothing: its output is zero
+ * and *error_flag (if non-NULL) is set to 1.
  */
 int kp_rope_c64(const void* x0, void* out0, int64_t H0, const int64_t* x0_strides, const int64_t* out0_strides,
                 const void* x1, void* out1, int64_t H1, const int64_t* x1_strides, const int64_t* out1_strides,

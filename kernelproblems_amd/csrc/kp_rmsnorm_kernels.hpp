@@ -29,7 +29,7 @@ struct RmsFwdArgs {
   int64_t xs[3];
   int n_x;
   // Gather variant: row r of term 0 is x[0] row idx[r] (idx_bytes 4 or 8);
-  // an id outside [0, idx_rows) reads nothing, gives a zero row and sets *err.
+  // an id outside [0, idx_rows) reads row 0 in its place, gives a zero row and sets *err.
   const void* idx;
   int idx_bytes;
   int64_t idx_rows;
