@@ -329,6 +329,7 @@ class EmbNorm(Workload):
         self.description = (f"embedding -> RMSNorm fused (v8/12545c1e9b06 region): table [{V},{D}] bf16, ids "
                             f"[{B},{S}] int64 Zipf(1.1) -> y [{B},{S},{D}] bf16 (eps=1e-5), no HBM intermediate")
         uniq = int(torch.unique(self.ids).numel())
+        self.unique_row_bytes = uniq * D * 2 + T * D * 2 + T * 8 + D * 2  # distinct rows read once (as c3f)
         R = max(2, math.ceil(MIN_ROTATION_BYTES / (uniq * D * 2 + T * D * 2)))
         tab_d, ids_d, w_d = self.table.to(dev), self.ids.to(dev), self.w.to(dev)
         fn = L.lib().kp_embedding_rmsnorm_fwd_bf16
@@ -1584,6 +1585,9 @@ def main():
                 "ceiling": _ceiling_json(r2),
                 "bytes_per_call": w2.bytes_per_call,
             }
+            ub = getattr(w2, "unique_row_bytes", None)
+            if ub:
+                frags[name]["unique_rows"] = {"bytes": ub, "GBps": round(ub / r2["dominant_ms"] / 1e6, 1)}
         line["fragments"] = frags
     if args.fragments:
         line["fragment_drop_ins"] = measure_fragments(dev, args.steps, args.warmup)
