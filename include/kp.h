@@ -267,8 +267,9 @@ int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table
 /* ------------------------------------------------------------------------
  * Embedding backward, dense: G[v, :] = sum over {t : indices[t] == v,
  * v != padding_idx} of grad[t, :] (divided by the id's count when
- * scale_grad_by_freq), accumulated in fp32, every row of G written exactly
- * once (rows without contributions are written as zeros).
+ * scale_grad_by_freq), accumulated in fp32; every row of G is written (rows
+ * without contributions as zeros; rows of the zero shares filled by the first
+ * two launches are written as zeros first, then their sums when touched).
  *
  * Replaces torch.ops.aten.embedding_dense_backward.default (+ _to_copy f32)
  * at v7/a12a160cb11b/problem.py:16-20, following the decomposition
@@ -283,8 +284,9 @@ int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table
  * grad_table: [V, D] contiguous, out_dtype KP_DTYPE_F32 or KP_DTYPE_BF16; with
  *   KP_DTYPE_F32 and out_round_bf16 != 0 every value is first rounded to bf16.
  * padding_idx < 0 means none.  Out-of-range ids are skipped and flagged.
- * Limits of this build: T <= 32768 and ceil(log2 V) + ceil(log2 T) <= 31
- *   (KP_EUNSUPPORTED otherwise).
+ * Limits of this build: T < 2^31 (KP_EUNSUPPORTED otherwise); any V -- the
+ *   sort keys hold ids below 2^21 - 1, so a larger vocabulary runs the
+ *   pipeline once per slab of that many rows, each pass writing its slab.
  */
 size_t kp_embedding_bwd_workspace_size(int64_t T, int64_t V, int64_t D);
 int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride,

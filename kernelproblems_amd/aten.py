@@ -95,7 +95,8 @@ def embedding_dense_backward(
 ) -> torch.Tensor:
     """aten.embedding_dense_backward(...) -> [num_weights, D] in grad_output's
     dtype (bf16), accumulated in fp32 (v7/a12a160cb11b/problem.py:16;
-    torch/_decomp/decompositions.py:1245-1275).  Any token count; the
-    vocabulary must stay below 2^21 ids (else KPError)."""
+    torch/_decomp/decompositions.py:1245-1275).  Any token count below 2^31
+    and any vocabulary (2^21 ids or more run one sort pass per slab of the
+    vocabulary)."""
     return fused.embedding_dense_backward(
         grad_output, indices, num_weights, padding_idx, scale_grad_by_freq, out_dtype=torch.bfloat16)

@@ -153,7 +153,10 @@ struct EmbBwdArgs {
   int64_t grs;
   const void* idx;
   int ib;
+  // V: rows of this pass's vocabulary slab [id_lo, id_lo + V) of the whole
+  // vocabulary [0, v_all); ids, rows, bitmap and out are slab-relative.
   int64_t T, V, D, padding_idx;
+  int64_t id_lo, v_all;
   int scale;  // scale_grad_by_freq
   void* out;
   int out_bf16;
@@ -284,10 +287,11 @@ __global__ __launch_bounds__(kThreads) void emb_sort_chunks(EmbBwdArgs a, ZeroSh
     const int64_t id = id8[e];
     uint32_t key = kSentinel;
     if (t < a.T) {
-      const bool in_range = id >= 0 && id < a.V;
+      const bool in_range = id >= 0 && id < a.v_all;
       bad |= !in_range;
-      if (in_range && id != a.padding_idx) {
-        key = ((uint32_t)id << kChunkBits) | (uint32_t)(e * kThreads + tid);
+      const int64_t rel = id - a.id_lo;  // ids of other slabs contribute nothing to this pass
+      if (in_range && rel >= 0 && rel < a.V && id != a.padding_idx) {
+        key = ((uint32_t)rel << kChunkBits) | (uint32_t)(e * kThreads + tid);
         ++nvalid;
       }
     }
@@ -949,7 +953,7 @@ int kp_embedding_fwd_bf16(const void* table, int64_t V, int64_t D, int64_t table
 
 size_t kp_embedding_bwd_workspace_size(int64_t T, int64_t V, int64_t D) {
   if (T < 0 || V <= 0 || D <= 0) return 0;
-  return make_layout(T, V, D).total;
+  return make_layout(T, V < kMaxVocab ? V : kMaxVocab, D).total;  // one slab's bitmap (see the entry point)
 }
 
 int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void* indices, int index_bytes, int64_t T,
@@ -963,10 +967,15 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   if (index_bytes != 4 && index_bytes != 8) return fail(KP_EINVAL, "%s: index_bytes must be 4 or 8", who);
   if (out_dtype != KP_DTYPE_F32 && out_dtype != KP_DTYPE_BF16) return fail(KP_EINVAL, "%s: bad out_dtype", who);
   if (T > 0 && grad_row_stride < D) return fail(KP_EINVAL, "%s: grad row stride must be >= D", who);
-  if (V > kMaxVocab || T > 0x7fffffffLL)
-    return fail(KP_EUNSUPPORTED, "%s: V=%lld, T=%lld outside this build's sort (V < 2^21, T < 2^31)", who,
-                (long long)V, (long long)T);
-  const Layout L = make_layout(T, V, D);
+  if (T > 0x7fffffffLL)
+    return fail(KP_EUNSUPPORTED, "%s: T=%lld outside this build's sort (T < 2^31)", who, (long long)T);
+  // The sort keys hold an id below 2^21 (kMaxVocab), so a larger vocabulary
+  // runs as one pass of the whole pipeline per slab of kMaxVocab rows: each
+  // pass sorts the ids of its slab (relative to the slab), writes the slab's
+  // rows (dense sums and zero fill) and ignores every other token.  The
+  // workspace holds one slab's bitmap; the passes reuse it in stream order.
+  const int64_t vs_max = V < kMaxVocab ? V : kMaxVocab;
+  const Layout L = make_layout(T, vs_max, D);
   if (workspace == nullptr || workspace_bytes < L.total || !aligned16(workspace))
     return fail(KP_EWORKSPACE, "%s: workspace needs %zu bytes, 16-byte aligned (got %zu)", who, L.total,
                 workspace_bytes);
@@ -978,9 +987,11 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   a.idx = indices;
   a.ib = index_bytes;
   a.T = T;
-  a.V = V;
+  a.V = vs_max;
   a.D = D;
   a.padding_idx = padding_idx;
+  a.id_lo = 0;
+  a.v_all = V;
   a.scale = scale_grad_by_freq ? 1 : 0;
   a.out = grad_table;
   a.out_bf16 = out_dtype == KP_DTYPE_BF16;
@@ -1002,39 +1013,50 @@ int kp_embedding_bwd_bf16(const void* grad, int64_t grad_row_stride, const void*
   hipStream_t s = as_stream(stream);
   const int64_t nq = ceil_div(D, kColStep);
   const int64_t row_bytes = D * (out_dtype == KP_DTYPE_BF16 ? 2 : 4);
-  // Zero-fill shares, taken from the top of the vocabulary down (high ids are
-  // the rarely touched ones under the usual frequency-ordered vocabularies):
-  // K1 [V - z1, V), K2 [V - z1 - z2, V - z1), K4 [r3, V - z1 - z2), K3 [0, r3).
-  const int64_t z1 = share_rows("KP_EMB_ZERO_MB_SORT", 128, row_bytes, V / 4);
-  const int64_t z2 = share_rows("KP_EMB_ZERO_MB_RANK", 128, row_bytes, V / 4);
-  const int64_t z4 = share_rows("KP_EMB_ZERO_MB_COMBINE", 96, row_bytes, V / 4);
-  const ZeroShare zs1{V - z1, V, 0};
-  const ZeroShare zs2{V - z1 - z2, V - z1, 0};
-  const ZeroShare zs4{V - z1 - z2 - z4, V - z1 - z2, 1};
-  const ZeroShare zs3{0, V - z1 - z2 - z4, 1};
   const int64_t nwin_blocks = L.nwin * nq;
   const int64_t total_keys = L.nchunks * kChunk;
   const int64_t rank_blocks = ceil_div(total_keys, kThreads);
   const int comb_blocks = cu_count() * 4;
-  const int64_t g1 = L.nchunks + z1 * nq, g2 = rank_blocks + z2 * nq, g3 = nwin_blocks + zs3.hi * nq,
-                g4 = comb_blocks + z4 * nq;
-  if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL || g3 > 0x7fffffffLL || g4 > 0x7fffffffLL)
-    return fail(KP_EUNSUPPORTED, "%s: V * D too large for one launch", who);
-  // With the timing hook set, the events span the whole pipeline (K1 start
-  // to K4 end): its zero fill is spread over all four launches.
-  int st;
-  if (vec) KP_LAUNCH_SPAN(true, false, emb_sort_chunks<true>, dim3((unsigned)g1), dim3(kThreads), 0, s, a, zs1);
-  else KP_LAUNCH_SPAN(true, false, emb_sort_chunks<false>, dim3((unsigned)g1), dim3(kThreads), 0, s, a, zs1);
-  if ((st = check_launch(who)) != KP_OK) return st;
-  if (vec) hipLaunchKernelGGL(emb_rank<true>, dim3((unsigned)g2), dim3(kThreads), 0, s, a, (int)rank_blocks, zs2);
-  else hipLaunchKernelGGL(emb_rank<false>, dim3((unsigned)g2), dim3(kThreads), 0, s, a, (int)rank_blocks, zs2);
-  if ((st = check_launch(who)) != KP_OK) return st;
-  if (vec) hipLaunchKernelGGL(emb_dense<true>, dim3((unsigned)g3), dim3(kThreads), 0, s, a, nwin_blocks, zs3);
-  else hipLaunchKernelGGL(emb_dense<false>, dim3((unsigned)g3), dim3(kThreads), 0, s, a, nwin_blocks, zs3);
-  if ((st = check_launch(who)) != KP_OK) return st;
-  if (vec) KP_LAUNCH_SPAN(false, true, emb_combine<true>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
-  else KP_LAUNCH_SPAN(false, true, emb_combine<false>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
-  return check_launch(who);
+  for (int64_t lo = 0; lo < V; lo += kMaxVocab) {
+    const int64_t Vs = V - lo < kMaxVocab ? V - lo : kMaxVocab;  // this pass's slab [lo, lo + Vs)
+    const bool first = lo == 0, last = lo + Vs >= V;
+    a.id_lo = lo;
+    a.V = Vs;
+    a.out = static_cast<uint8_t*>(grad_table) + lo * row_bytes;
+    // Zero-fill shares, taken from the top of the slab down (high ids are
+    // the rarely touched ones under the usual frequency-ordered vocabularies):
+    // K1 [Vs - z1, Vs), K2 [Vs - z1 - z2, Vs - z1), K4 [r3, Vs - z1 - z2), K3 [0, r3).
+    const int64_t z1 = share_rows("KP_EMB_ZERO_MB_SORT", 128, row_bytes, Vs / 4);
+    const int64_t z2 = share_rows("KP_EMB_ZERO_MB_RANK", 128, row_bytes, Vs / 4);
+    const int64_t z4 = share_rows("KP_EMB_ZERO_MB_COMBINE", 96, row_bytes, Vs / 4);
+    const ZeroShare zs1{Vs - z1, Vs, 0};
+    const ZeroShare zs2{Vs - z1 - z2, Vs - z1, 0};
+    const ZeroShare zs4{Vs - z1 - z2 - z4, Vs - z1 - z2, 1};
+    const ZeroShare zs3{0, Vs - z1 - z2 - z4, 1};
+    const int64_t g1 = L.nchunks + z1 * nq, g2 = rank_blocks + z2 * nq, g3 = nwin_blocks + zs3.hi * nq,
+                  g4 = comb_blocks + z4 * nq;
+    if (g1 > 0x7fffffffLL || g2 > 0x7fffffffLL || g3 > 0x7fffffffLL || g4 > 0x7fffffffLL)
+      return fail(KP_EUNSUPPORTED, "%s: V * D too large for one launch", who);
+    // With the timing hook set, the events span the whole pipeline (the first
+    // K1's start to the last K4's end): its zero fill is spread over all four
+    // launches.
+    int st;
+    if (vec) KP_LAUNCH_SPAN(first, false, emb_sort_chunks<true>, dim3((unsigned)g1), dim3(kThreads), 0, s, a, zs1);
+    else KP_LAUNCH_SPAN(first, false, emb_sort_chunks<false>, dim3((unsigned)g1), dim3(kThreads), 0, s, a, zs1);
+    if ((st = check_launch(who)) != KP_OK) return st;
+    if (vec) hipLaunchKernelGGL(emb_rank<true>, dim3((unsigned)g2), dim3(kThreads), 0, s, a, (int)rank_blocks, zs2);
+    else hipLaunchKernelGGL(emb_rank<false>, dim3((unsigned)g2), dim3(kThreads), 0, s, a, (int)rank_blocks, zs2);
+    if ((st = check_launch(who)) != KP_OK) return st;
+    if (vec) hipLaunchKernelGGL(emb_dense<true>, dim3((unsigned)g3), dim3(kThreads), 0, s, a, nwin_blocks, zs3);
+    else hipLaunchKernelGGL(emb_dense<false>, dim3((unsigned)g3), dim3(kThreads), 0, s, a, nwin_blocks, zs3);
+    if ((st = check_launch(who)) != KP_OK) return st;
+    if (vec)
+      KP_LAUNCH_SPAN(false, last, emb_combine<true>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
+    else
+      KP_LAUNCH_SPAN(false, last, emb_combine<false>, dim3((unsigned)g4), dim3(kThreads), 0, s, a, comb_blocks, zs4);
+    if ((st = check_launch(who)) != KP_OK) return st;
+  }
+  return KP_OK;
 }
 
 size_t kp_rmsnorm_embedding_bwd_workspace_size(int64_t M, int64_t N, int64_t V) {
@@ -1100,6 +1122,8 @@ int kp_rmsnorm_embedding_bwd_bf16(const void* const* dy_terms, const int64_t* dy
   e.V = V;
   e.D = N;
   e.padding_idx = padding_idx;
+  e.id_lo = 0;
+  e.v_all = V;
   e.scale = 0;
   e.out = grad_table;
   e.out_bf16 = out_dtype == KP_DTYPE_BF16;

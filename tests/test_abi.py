@@ -74,9 +74,13 @@ def test_rmsnorm_validation(lib):
 
 def test_embedding_validation(lib):
     _expect(lib, L.KP_EINVAL, "kp_embedding_fwd_bf16", 16, 10, 8, 8, 32, 3, 4, 48, 8, None, None)  # 3-byte ids
-    ws = lib.kp_embedding_bwd_workspace_size(100, 1 << 21, 64)
-    _expect(lib, L.KP_EUNSUPPORTED, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 100, 1 << 21, 64, -1, 0, 48,
-            L.KP_DTYPE_F32, 0, 64, max(ws, 1), None, None)  # a vocabulary past the sort key's 21 id bits
+    # any vocabulary: past the sort key's 21 id bits the pipeline runs once per
+    # slab of 2^21 - 1 rows, so the workspace holds one slab's bitmap
+    slab = (1 << 21) - 1
+    assert lib.kp_embedding_bwd_workspace_size(100, 1 << 30, 64) == lib.kp_embedding_bwd_workspace_size(100, slab, 64)
+    assert lib.kp_embedding_bwd_workspace_size(100, slab, 64) > lib.kp_embedding_bwd_workspace_size(100, slab - 4096, 64)
+    _expect(lib, L.KP_EUNSUPPORTED, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 1 << 31, 1 << 22, 64, -1, 0, 48,
+            L.KP_DTYPE_F32, 0, 64, 1 << 20, None, None)  # 2^31 tokens: past the sort's token count
     ws = lib.kp_embedding_bwd_workspace_size(65536, 128256, 64)
     _expect(lib, L.KP_EWORKSPACE, "kp_embedding_bwd_bf16", 16, 64, 32, 8, 65536, 128256, 64, -1, 0, 48,
             L.KP_DTYPE_F32, 0, 64, ws - 1, None, None)  # any token count: only the workspace bounds it

@@ -113,6 +113,53 @@ def _check_bwd(gpu, O, V, D, ids, grad, padding_idx=-1, scale=False):
     return out
 
 
+_SLAB = (1 << 21) - 1  # ids per pass of the backward's sort (21 id bits in its keys)
+
+
+@pytest.mark.parametrize("V,scale,pad", [(_SLAB + 1000, False, -1), (_SLAB + 1000, True, _SLAB + 7),
+                                         (2 * _SLAB + 3, False, _SLAB + 7)])
+def test_embedding_bwd_vocabulary_slabs(gpu, oracle_lib, V, scale, pad):
+    """A vocabulary past the sort key's 21 id bits runs the pipeline once per
+    slab of 2^21 - 1 rows: ids on both sides of every slab boundary, the last
+    row, a hot id at the first row of the second slab (a run spanning
+    windows), padding inside the second slab -- every touched row against the
+    oracle's fp64 rows within the fp32 summation bound, every other row 0."""
+    print(f"[emb bwd slabs] V={V} scale={scale} pad={pad}", flush=True)
+    D, T = 64, 6000
+    g = gen(V % 1000 + int(scale))
+    ids = torch.randint(0, V, (T,), generator=g)
+    special = [0, _SLAB - 1, _SLAB, _SLAB + 1, V - 1] + ([2 * _SLAB - 1, 2 * _SLAB] if V > 2 * _SLAB else [])
+    ids[:len(special)] = torch.tensor(special)
+    ids[100:180] = _SLAB
+    if pad >= 0:
+        ids[200:210] = pad
+    grad = randn_bf16((T, D), g)
+    out = _check_bwd(gpu, oracle_lib, V, D, ids, grad, padding_idx=pad, scale=scale)
+    if pad >= 0:
+        assert not out[pad].any()
+    again = kp.embedding_dense_backward(grad.to(gpu), ids.to(gpu), V, pad, scale)
+    assert torch.equal(out, again)  # bitwise repeatable
+
+
+def test_embedding_bwd_vocabulary_slabs_bad_ids(gpu):
+    """Out-of-range ids (negative, V, far above V) under the slab passes are
+    skipped and recorded; the in-range rows of both slabs are unchanged."""
+    V, D = _SLAB + 50, 32
+    ids = torch.tensor([3, _SLAB + 2, -1, V, V + (1 << 22), _SLAB + 2, 3])
+    grad = torch.ones((ids.numel(), D), dtype=torch.bfloat16)
+    kp.set_index_checking(False)
+    try:
+        kp.check_indices()
+        out = kp.embedding_dense_backward(grad.to(gpu), ids.to(gpu), V)
+        with pytest.raises(IndexError):
+            kp.check_indices()
+    finally:
+        kp.set_index_checking(True)
+    assert torch.equal(out[3], torch.full((D,), 2.0, device=gpu))
+    assert torch.equal(out[_SLAB + 2], torch.full((D,), 2.0, device=gpu))
+    assert float(out.abs().sum()) == 4.0 * D
+
+
 @pytest.mark.parametrize("V,D,T", [(1000, 4096, 777), (64, 128, 4000), (5000, 512, 2048), (37, 100, 250)])
 def test_embedding_bwd_matches_oracle(gpu, oracle_lib, V, D, T):
     g = gen(V * 3 + T)
