@@ -227,6 +227,23 @@ bool pick_vec(int64_t N, bool forward, int* vpl, int* wpr) {
   return false;
 }
 
+// Forward row shape for M rows: pick_vec's, except that rows of 4096 go to one
+// block of 4 waves each (the one-shot grid of one row per block) from
+// KP_RMS_FWD_BLOCK_ROWS (default 8192) rows on.  Measured on MI355X per call
+// (one wave per row -> one block per row): M = 4096 12.1 -> 13.5 us (c1),
+// 6144 18.9 both, 8192 25.0 -> 23.9, 12288 35.7 -> 34.0, 16384 46.3 -> 44.4,
+// 32768 90.9 -> 86.3.  0 turns the rule off (tuning knob).
+bool pick_fwd(int64_t M, int64_t N, int* vpl, int* wpr) {
+  if (!pick_vec(N, true, vpl, wpr)) return false;
+  static const int64_t from = env_int("KP_RMS_FWD_BLOCK_ROWS", 8192, 0, 1 << 30);
+  static const bool knobs = getenv("KP_RMS_VPL_MAX") != nullptr || getenv("KP_RMS_WPR_MIN") != nullptr;
+  if (!knobs && from > 0 && M >= from && N == 4096 && shape_ok(2, 4)) {
+    *vpl = 2;
+    *wpr = 4;
+  }
+  return true;
+}
+
 // Backward row shape: N = 8192 runs 8 waves per row with 2 chunks per lane in
 // 8-wave blocks (one row per block step; measured on MI355X at [16384, 8192]
 // with two x terms: 171.5 us against 175.5 us for 4 waves x 4 chunks in
@@ -548,7 +565,7 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
   a.eps = eps;
 
   int vpl = 0, wpr = 0;
-  bool vec = pick_vec(N, true, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) && aligned16(y) && (y_stride & 7) == 0;
+  bool vec = pick_fwd(M, N, &vpl, &wpr) && rows_vec_ok(x_terms, x_strides, n_x) && aligned16(y) && (y_stride & 7) == 0;
   if (vec && h_out) vec = aligned16(h_out) && (h_stride & 7) == 0;
   if (vec && weight) vec = aligned16(weight) && (w_seg_len & 7) == 0 && (w_seg_stride & 7) == 0;
   const FwdKernel fk = vec ? fwd_kernel(vpl, wpr, n_x) : nullptr;
@@ -611,6 +628,9 @@ int kp_embedding_rmsnorm_fwd_bf16(const void* table, int64_t V, int64_t table_ro
   a.eps = eps;
 
   int vpl = 0, wpr = 0;
+  // one wave per row whatever T: the gather's row-per-block form measured
+  // 39.3 against 34.2 us at C3 (cache-served table rows favour the
+  // persistent pipelined grid)
   bool vec = pick_vec(N, true, &vpl, &wpr) && aligned16(table) && (table_row_stride & 7) == 0 && aligned16(y) &&
              (y_stride & 7) == 0;
   if (vec && h_out) vec = aligned16(h_out) && (h_stride & 7) == 0;

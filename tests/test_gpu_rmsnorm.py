@@ -55,6 +55,27 @@ def test_rmsnorm_fwd_matches_oracle(gpu, oracle_lib, M, N, n_terms):
         assert_bf16_close(to_u16(y), y_o, what=f"y[{kind}]", max_ulp=1, min_exact=0.99)
 
 
+@pytest.mark.parametrize("n_terms", [1, 2])
+def test_rmsnorm_fwd_block_per_row_from_8192_rows(gpu, oracle_lib, n_terms):
+    """From 8192 rows of 4096 the forward runs one block of 4 waves per row
+    (the row's sum of squares split four ways): every rstd against fp64, h
+    bit-exact, and y of 64 sampled rows against the oracle."""
+    M, N = 8192, 4096
+    print(f"[rms fwd block-per-row] [{M},{N}] terms={n_terms}", flush=True)
+    g = gen(8192 + n_terms)
+    xs = [randn_bf16((M, N), g) for _ in range(n_terms)]
+    w = randn_bf16(N, g, 1.0, 0.02)
+    h, y, rstd = kp.rms_norm([x.to(gpu) for x in xs], w.to(gpu), 1e-6, N, return_h=True, return_rstd=True)
+    hh = xs[0].to(gpu) if n_terms == 1 else h
+    if n_terms > 1:
+        assert torch.equal(h, xs[0].to(gpu) + xs[1].to(gpu))
+    r64 = torch.rsqrt(hh.double().pow(2).mean(-1) + 1e-6)
+    assert float(((rstd.view(-1).double() - r64).abs() / r64).max()) < 1e-6
+    rows = torch.randperm(M, generator=torch.Generator().manual_seed(3))[:64].sort().values
+    _, y_o, _ = oracle_lib.rmsnorm_fwd([to_u16(x[rows]) for x in xs], to_u16(w), 1e-6, N)
+    assert_bf16_close(to_u16(y[rows.to(gpu)]), y_o, what="y", max_ulp=1, min_exact=0.99)
+
+
 def test_rmsnorm_fwd_vs_torch_eager(gpu):
     """The reference fragment's own op on this GPU (torch-ROCm eager _fused_rms_norm)."""
     g = gen(7)
