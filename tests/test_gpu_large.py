@@ -1,0 +1,147 @@
+"""Tensors of more than 2^31 elements (byte offsets past 4 GiB) on the GPU.
+
+Every kernel indexes rows or chunks with 64-bit byte offsets or with 32-bit
+chunk indices whose range the host checks; these tests run each family once
+past 2^31 elements and check the rows, positions or ids that lie past that
+point:
+  RMSNorm forward / backward  x, dy [262208, 8192] bf16 (2^31 + 2^19 elements)
+  SiLU                        a [262208, 8192] bf16
+  RoPE rotate-half            q [8, 32769, 64, 128] bf16 (2^31 + 65536 elements)
+  embedding fwd / bwd         table [262208, 8192] bf16, fp32 gradient table
+The inputs are drawn on the GPU from a seeded generator (drawing 2^31 values
+on the CPU takes longer than a test may).  Sampled rows are checked against
+the CPU oracle, elementwise results against torch-ROCm eager, and the weight
+gradient column by column against an fp64 sum taken in row chunks on the GPU.
+Samples of the large tensors are taken as slices (views), never by index
+tensors.  Each test holds at most ~22 GB of device memory and releases it at
+the end.
+"""
+import numpy as np
+import pytest
+import torch
+
+import kernelproblems_amd as kp
+import oracle
+from tests._util import to_u16, ulp_bf16
+
+pytestmark = pytest.mark.gpu
+
+M, N = 2**18 + 64, 8192  # rows 2^18 .. M - 1 start past element 2^31
+assert M * N > 2**31
+
+
+def _big(shape, seed, gpu, mean=0.0, std=1.0):
+    g = torch.Generator(device=gpu).manual_seed(seed)
+    t = torch.randn(shape, dtype=torch.bfloat16, device=gpu, generator=g)
+    if std != 1.0 or mean != 0.0:
+        t.mul_(std).add_(mean)
+    return t
+
+
+ROWS = [0, 1, 2**31 // N - 1, 2**31 // N, 2**31 // N + 1, M // 2 + 7, M - 3, M - 2, M - 1]
+assert all(0 <= r < M for r in ROWS)  # row 2^31 / N is the first to start past element 2^31
+
+
+def _take(t, idx):
+    """Rows idx of t (first dimension), gathered from views."""
+    return torch.cat([t[i:i + 1] for i in idx])
+
+
+def _release():
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def test_rmsnorm_forward_backward_past_2p31_elements(gpu):
+    print(f"[large] rmsnorm fwd / bwd [{M},{N}]", flush=True)
+    eps = 1e-5
+    x = _big((M, N), 31, gpu)
+    w = _big((N,), 32, gpu, 1.0, 0.02)
+    _, y, rstd = kp.rms_norm([x], w, eps, N)
+    _, yo, ro = oracle.rmsnorm_fwd([to_u16(_take(x, ROWS))], to_u16(w), eps, N)
+    assert ulp_bf16(to_u16(_take(y, ROWS)), yo).max() <= 1
+    assert np.allclose(_take(rstd.view(-1), ROWS).cpu().numpy(), ro, rtol=2e-6)
+    del y, rstd
+    _release()
+
+    dy = _big((M, N), 33, gpu)
+    dx, dw = kp.rms_norm_backward([dy], [x], None, w, eps, N)
+    dxo, _, _ = oracle.rmsnorm_bwd([to_u16(_take(dy, ROWS))], [to_u16(_take(x, ROWS))], None, to_u16(w), eps, N)
+    u = ulp_bf16(to_u16(_take(dx, ROWS)), dxo)
+    assert (u <= 2).all() and (u == 0).mean() > 0.9
+    del dx
+    _release()
+    # the weight gradient against an fp64 column sum over all rows, in chunks
+    dw64 = torch.zeros(N, dtype=torch.float64, device=gpu)
+    mag = torch.zeros_like(dw64)
+    for i in range(0, M, 16384):
+        xc = x[i:i + 16384].double()
+        r = torch.rsqrt(xc.pow(2).mean(1) + eps)
+        t = dy[i:i + 16384].double() * xc * r[:, None]
+        dw64 += t.sum(0)
+        mag += t.abs().sum(0)
+        del xc, t
+    assert bool(((dw.double() - dw64).abs() <= 2.0**-20 * mag + 1e-6).all())
+    del x, dy, dw, dw64, mag
+    _release()
+
+
+def test_silu_past_2p31_elements(gpu):
+    print(f"[large] silu [{M},{N}]", flush=True)
+    a = _big((M, N), 41, gpu, 0.0, 3.0)
+    out = kp.silu(a)
+    assert torch.equal(_take(out, ROWS), torch.nn.functional.silu(_take(a, ROWS)))
+    tail = slice(M - 64, M)  # the last 64 rows whole
+    assert torch.equal(out[tail], torch.nn.functional.silu(a[tail]))
+    del a, out
+    _release()
+
+
+def test_rope_past_2p31_elements(gpu):
+    B, S, H, D, theta = 8, 32769, 64, 128, 500000.0
+    assert B * S * H * D > 2**31
+    print(f"[large] rope q [{B},{S},{H},{D}]", flush=True)
+    q = _big((B, S, H, D), 51, gpu)
+    pos = torch.arange(S, dtype=torch.int64, device=gpu).expand(B, S).contiguous()
+    qo, _ = kp.rope(q, None, positions=pos, theta=theta)
+    for b in range(B):
+        assert torch.equal(qo[b, 0], q[b, 0])  # position 0 is the identity
+    # positions whose elements lie past 2^31 and a few others (element
+    # (b S + s) H D of position (b, s) is 2^31 or more from (7, 32761) on)
+    for b, s in ((0, 1), (3, 16384), (7, 0), (7, 20000), (7, 32760), (7, 32761), (7, 32762), (7, S - 1)):
+        e = oracle.rope(to_u16(q[b:b + 1, s:s + 1]), np.array([[s]]), pairing="half", theta=theta)
+        assert ulp_bf16(to_u16(qo[b:b + 1, s:s + 1]), e).max() <= 1, (b, s)
+    del q, qo, pos
+    _release()
+
+
+def test_embedding_past_2p31_elements(gpu):
+    V, D = M, N
+    print(f"[large] embedding table [{V},{D}] fwd / bwd", flush=True)
+    table = _big((V, D), 61, gpu, 0.0, 0.02)
+    gi = torch.Generator().manual_seed(62)
+    ids_l = [V - 1, V - 2, 0, 2**31 // D, 2**31 // D - 1, V - 1] + torch.randint(0, V, (4090,), generator=gi).tolist()
+    assert all(0 <= i < V for i in ids_l)
+    ids = torch.tensor(ids_l).view(4, 1024).to(gpu)
+    out = kp.embedding(table, ids)
+    assert torch.equal(out.view(-1, D), _take(table, ids_l))  # bit-exact gather
+    del out, table
+    _release()
+
+    grad = _big((4, 1024, D), 63, gpu)
+    dense = kp.embedding_dense_backward(grad, ids, V)  # fp32 [V, D]: 2^31 + 2^19 elements
+    flat = ids.view(-1)
+    uniq, inv = torch.unique(flat, return_inverse=True)
+    ref = torch.zeros(uniq.numel(), D, dtype=torch.float64, device=gpu).index_add_(0, inv, grad.view(-1, D).double())
+    absr = torch.zeros_like(ref).index_add_(0, inv, grad.view(-1, D).double().abs())
+    cnt = torch.bincount(inv).double()[:, None]
+    got = _take(dense, uniq.tolist())
+    assert bool(((got.double() - ref).abs() <= (cnt + 1) * 2.0**-24 * absr).all())
+    # every other row is written as zeros, the last rows included
+    touched = torch.zeros(V, dtype=torch.bool, device=gpu)
+    touched[uniq] = True
+    for i in range(0, V, 16384):
+        blk = dense[i:i + 16384]
+        assert not blk[~touched[i:i + 16384]].any(), f"nonzero untouched row in [{i}, {i + 16384})"
+    del dense, grad, ref, absr, got
+    _release()
