@@ -8,6 +8,8 @@ point:
   SiLU                        a [262208, 8192] bf16
   RoPE rotate-half            q [8, 32769, 64, 128] bf16 (2^31 + 65536 elements)
   embedding fwd / bwd         table [262208, 8192] bf16, fp32 gradient table
+  cross-entropy               logits [16800, 128256] bf16 (fwd, fwd + bwd) and
+                              its fp32 log-softmax (bwd)
 The inputs are drawn on the GPU from a seeded generator (drawing 2^31 values
 on the CPU takes longer than a test may).  Sampled rows are checked against
 the CPU oracle, elementwise results against torch-ROCm eager, and the weight
@@ -144,4 +146,55 @@ def test_embedding_past_2p31_elements(gpu):
         blk = dense[i:i + 16384]
         assert not blk[~touched[i:i + 16384]].any(), f"nonzero untouched row in [{i}, {i + 16384})"
     del dense, grad, ref, absr, got
+    _release()
+
+
+def test_cross_entropy_past_2p31_elements(gpu):
+    Mx, V = 16800, 128256
+    first = -(-2**31 // V)  # the first row that starts past element 2^31
+    rows = [0, 1, first - 1, first, first + 1, Mx - 2, Mx - 1]
+    assert Mx * V > 2**31 and all(0 <= r < Mx for r in rows)
+    print(f"[large] cross-entropy logits [{Mx},{V}] fwd, fwd + bwd, bwd", flush=True)
+    x = _big((Mx, V), 71, gpu, 0.0, 2.0)
+    t = torch.randint(0, V, (Mx,), generator=torch.Generator().manual_seed(72))
+    t[::4] = -100
+    td = t.to(gpu)
+    ts = t[rows].numpy()
+    xs = to_u16(_take(x, rows))
+    gl = 1 / 8192
+    # forward: the sampled rows' logsumexp against the oracle, the loss against
+    # an fp64 sum over every row taken in chunks on the GPU
+    loss, tw, lse = kp.cross_entropy_loss(x, td, scale=gl, return_lse=True)
+    _, _, e_lse, bad = oracle.cross_entropy_fwd(xs, ts, scale=gl)
+    assert bad == 0
+    np.testing.assert_allclose(_take(lse, rows).cpu().double().numpy(), e_lse, rtol=2.0**-24, atol=2e-6)
+    ref, cnt = 0.0, 0
+    for i in range(0, Mx, 512):
+        xc = x[i:i + 512].double()
+        tc = td[i:i + 512]
+        ok = tc != -100
+        xt = xc.gather(1, tc.clamp(min=0)[:, None])[:, 0]
+        ref += float(((torch.logsumexp(xc, dim=1) - xt) * ok).sum())
+        cnt += int(ok.sum())
+        del xc
+    assert float(tw) == cnt
+    assert float(loss) == pytest.approx(ref * gl, rel=2e-6)
+    del lse
+    _release()
+    # forward + backward from the logits: sampled rows against the oracle
+    out = kp.cross_entropy_forward_backward(x, td, gl)
+    eo, bad = oracle.cross_entropy_fwd_bwd(xs, ts, gl)
+    assert bad == 0 and ulp_bf16(to_u16(_take(out, rows)), eo).max() <= 1
+    del out
+    _release()
+    # backward from a saved fp32 log-softmax (2^31 + ... fp32 elements)
+    L = torch.empty((Mx, V), dtype=torch.float32, device=gpu)
+    for i in range(0, Mx, 512):
+        L[i:i + 512] = torch.log_softmax(x[i:i + 512].float(), dim=1)
+    del x
+    _release()
+    out = kp.cross_entropy_backward(L, td, gl)
+    eo, bad = oracle.cross_entropy_bwd(_take(L, rows).cpu().numpy(), ts, gl)
+    assert bad == 0 and ulp_bf16(to_u16(_take(out, rows)), eo).max() <= 1
+    del out, L
     _release()
