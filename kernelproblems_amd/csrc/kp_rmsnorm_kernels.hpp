@@ -381,7 +381,7 @@ __device__ __forceinline__ void bwd_load(RawRow<VPL, NX>& xr, RawRow<VPL, NDY>& 
 // KEEP: the row's dx (with the residual epilogue) is handed back in gout[]
 // (the same packed bf16 chunks the store would write) instead of stored, for
 // a consumer in the same kernel (the embedding backward of the chain).
-template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD, bool KEEP = false>
+template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD, bool KEEP = false, bool UNCOND = false>
 __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, NX>& xr, const RawRow<VPL, NDY>& dr,
                                         const RawRow<VPL, 1>& rr, float rq, const float (&wf)[VPL * 8],
                                         float (&acc)[VPL * 8], float (&red)[2][NW][2], int64_t row, int64_t col,
@@ -428,6 +428,31 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
   const float r = have_rstd ? rq : 1.0f / sqrtf(ss / (float)a.N + a.eps);
   // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
   const float cN = (r * sxg) * inv_n;
+  if constexpr (UNCOND && !FWD && !KEEP) {
+    // The stores are not under a branch (see rms_bwd_vec): a row past M --
+    // only in a block's last group -- was read as row M - 1, so its dx is row
+    // M - 1's bit for bit and is stored there again; only its weight-gradient
+    // contribution is dropped, by a select.
+    const int64_t srow = valid ? row : a.M - 1;
+    uint16_t* dxrow = a.dx + srow * a.dxs + col;
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float o[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = i * 8 + e;
+        const float xh = xf[j] * r;
+        const float gg = df[j] * wf[j];
+        o[e] = (gg - xh * cN) * r;
+        const float na = fmaf(df[j], xh, acc[j]);
+        acc[j] = valid ? na : acc[j];
+      }
+      u32x4 ov = pack8(o);
+      if constexpr (RES) ov = add_bf8(rr.v[0][i], ov);
+      st16_stream(dxrow + i * 512, ov);
+    }
+    return;
+  }
   if (valid) {
     if constexpr (FWD) {
       uint16_t* yrow = a.y + row * a.ys + col;
@@ -493,6 +518,7 @@ __device__ __forceinline__ void trace_block(const RmsBwdArgs& a, unsigned long l
 template <int VPL, int WPR, int NX, int NDY, bool RES, int NW, bool FWD>
 __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   constexpr int RB = NW / WPR;
+  constexpr bool kExact = NW == 4 && !FWD;  // exact wait counts (see the row loop)
   constexpr int SEG = 512 * VPL;
   extern __shared__ float smem[];  // [RB / 2][WPR][SEG] weight-gradient combine (only when a.partial)
   __shared__ float red[2][NW][2];
@@ -524,26 +550,55 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
 #define KP_LOAD(S, g)                                                                       \
   bwd_load<VPL, NX, NDY, RES, FWD>(x##S, d##S, r##S, q##S, a, clamp_row(KP_ROW(g), a.M), col); \
   __builtin_amdgcn_sched_barrier(0)
-#define KP_PROC(S, g)                                                                                               \
-  bwd_row<VPL, WPR, NX, NDY, RES, NW, FWD>(a, x##S, d##S, r##S, q##S, wf, acc, red, KP_ROW(g), col, lane, wave, rloc, \
-                                          it);                                                                         \
+#define KP_PROC(S, g)                                                                                             \
+  bwd_row<VPL, WPR, NX, NDY, RES, NW, FWD, false, kExact>(a, x##S, d##S, r##S, q##S, wf, acc, red, KP_ROW(g), col, \
+                                                          lane, wave, rloc, it);                                     \
   ++it
   // Exact trip count (see rms_fwd_vec): nb >= 1 groups per block.
   const int64_t nb = block_trips(ngroups, blockIdx.x, G);
   int64_t g = blockIdx.x, k = 0;
   KP_LOAD(0, g);
-  for (; k + 2 < nb; k += 2, g += 2 * G) {
-    KP_LOAD(1, g + G);
-    KP_PROC(0, g);
-    KP_LOAD(0, g + 2 * G);
-    KP_PROC(1, g + G);
-  }
-  if (k + 1 < nb) {
-    KP_LOAD(1, g + G);
-    KP_PROC(0, g);
-    KP_PROC(1, g + G);
+  if constexpr (kExact) {
+    // The loop is entered after the first group's stores, so that both paths
+    // into its header (from the prologue and from the loop's end) hold the
+    // same loads and stores in flight; with the row stores unbranched as
+    // well, every wait for a group's loads is exact instead of also waiting
+    // for the previous group's stores (c2 kernel 34.7-34.9 -> 34.5-34.7 us).
+    // The 8-wave shapes (N = 8192) keep the other form: there the store
+    // waits pace the 3-read loop (c5b 174.7 against 180.9 us exact).
+    if (nb >= 2) {
+      KP_LOAD(1, g + G);
+      KP_PROC(0, g);
+      for (; k + 3 < nb; k += 2, g += 2 * G) {
+        KP_LOAD(0, g + 2 * G);
+        KP_PROC(1, g + G);
+        KP_LOAD(1, g + 3 * G);
+        KP_PROC(0, g + 2 * G);
+      }
+      if (k + 2 < nb) {
+        KP_LOAD(0, g + 2 * G);
+        KP_PROC(1, g + G);
+        KP_PROC(0, g + 2 * G);
+      } else {
+        KP_PROC(1, g + G);
+      }
+    } else {
+      KP_PROC(0, g);
+    }
   } else {
-    KP_PROC(0, g);
+    for (; k + 2 < nb; k += 2, g += 2 * G) {
+      KP_LOAD(1, g + G);
+      KP_PROC(0, g);
+      KP_LOAD(0, g + 2 * G);
+      KP_PROC(1, g + G);
+    }
+    if (k + 1 < nb) {
+      KP_LOAD(1, g + G);
+      KP_PROC(0, g);
+      KP_PROC(1, g + G);
+    } else {
+      KP_PROC(0, g);
+    }
   }
 #undef KP_ROW
 #undef KP_LOAD
