@@ -429,12 +429,9 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
   // sum(xhat * g) = r * sum(x * g);  dx = (g - xhat * sum/N) * r
   const float cN = (r * sxg) * inv_n;
   if constexpr (UNCOND && !FWD && !KEEP) {
-    // The stores are not under a branch (see rms_bwd_vec): a row past M --
-    // only in a block's last group -- was read as row M - 1, so its dx is row
-    // M - 1's bit for bit and is stored there again; only its weight-gradient
-    // contribution is dropped, by a select.
-    const int64_t srow = valid ? row : a.M - 1;
-    uint16_t* dxrow = a.dx + srow * a.dxs + col;
+    // The stores are not under a branch (see rms_bwd_vec): this form only
+    // runs rows below M.
+    uint16_t* dxrow = a.dx + row * a.dxs + col;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       float o[8];
@@ -444,8 +441,7 @@ __device__ __forceinline__ void bwd_row(const RmsBwdArgs& a, const RawRow<VPL, N
         const float xh = xf[j] * r;
         const float gg = df[j] * wf[j];
         o[e] = (gg - xh * cN) * r;
-        const float na = fmaf(df[j], xh, acc[j]);
-        acc[j] = valid ? na : acc[j];
+        acc[j] = fmaf(df[j], xh, acc[j]);
       }
       u32x4 ov = pack8(o);
       if constexpr (RES) ov = add_bf8(rr.v[0][i], ov);
@@ -554,19 +550,23 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
   bwd_row<VPL, WPR, NX, NDY, RES, NW, FWD, false, kExact>(a, x##S, d##S, r##S, q##S, wf, acc, red, KP_ROW(g), col, \
                                                           lane, wave, rloc, it);                                     \
   ++it
-  // Exact trip count (see rms_fwd_vec): nb >= 1 groups per block.
-  const int64_t nb = block_trips(ngroups, blockIdx.x, G);
   int64_t g = blockIdx.x, k = 0;
-  KP_LOAD(0, g);
   if constexpr (kExact) {
-    // The loop is entered after the first group's stores, so that both paths
+    // The loop walks the full row groups only, stores unbranched (every row
+    // < M), and is entered after the first group's stores, so that both paths
     // into its header (from the prologue and from the loop's end) hold the
-    // same loads and stores in flight; with the row stores unbranched as
-    // well, every wait for a group's loads is exact instead of also waiting
-    // for the previous group's stores (c2 kernel 34.7-34.9 -> 34.5-34.7 us).
-    // The 8-wave shapes (N = 8192) keep the other form: there the store
-    // waits pace the 3-read loop (c5b 174.7 against 180.9 us exact).
+    // same loads and stores in flight: every wait for a group's loads is
+    // exact instead of also waiting for the previous group's stores (c2
+    // kernel 34.7-34.8 -> 34.5-34.6 us).  A last group with rows past M is
+    // its owner's last group anyway and runs after the loop with guarded
+    // stores, so dw keeps its order and no row is written by a wave that did
+    // not read it (dx may alias its inputs).  The 8-wave shapes (N = 8192)
+    // keep the other form: there the store waits pace the 3-read loop (c5b
+    // 174.7 against 180.9 us exact).
+    const int64_t nfull = a.M / RB;
+    const int64_t nb = (int64_t)blockIdx.x < nfull ? block_trips(nfull, blockIdx.x, G) : 0;
     if (nb >= 2) {
+      KP_LOAD(0, g);
       KP_LOAD(1, g + G);
       KP_PROC(0, g);
       for (; k + 3 < nb; k += 2, g += 2 * G) {
@@ -582,10 +582,20 @@ __global__ __launch_bounds__(NW * 64) void rms_bwd_vec(RmsBwdArgs a) {
       } else {
         KP_PROC(1, g + G);
       }
-    } else {
+    } else if (nb == 1) {
+      KP_LOAD(0, g);
       KP_PROC(0, g);
     }
+    if (nfull < ngroups && (ngroups - 1) % G == (int64_t)blockIdx.x) {
+      const int64_t gl = ngroups - 1;
+      KP_LOAD(0, gl);
+      bwd_row<VPL, WPR, NX, NDY, RES, NW, FWD>(a, x0, d0, r0, q0, wf, acc, red, KP_ROW(gl), col, lane, wave, rloc, it);
+      ++it;
+    }
   } else {
+    // Exact trip count (see rms_fwd_vec): nb >= 1 groups per block.
+    const int64_t nb = block_trips(ngroups, blockIdx.x, G);
+    KP_LOAD(0, g);
     for (; k + 2 < nb; k += 2, g += 2 * G) {
       KP_LOAD(1, g + G);
       KP_PROC(0, g);

@@ -239,3 +239,42 @@ def test_block_trace_hook_records_every_block_and_changes_nothing(gpu, M, N, res
     assert bool((r[:, 0] <= r[:, 1]).all()) and bool((r[:, 1] <= r[:, 2]).all())
     assert bool((r[:, 3] >= 0).all()) and bool((r[:, 3] < 8).all())
     assert bool((buf[cap * 4:] == 0).all()), "nothing may be written past the records"
+
+
+@pytest.mark.parametrize("M,N", [(8191, 4096), (8192, 4096), (1001, 1024), (3, 512), (16383, 8192)])
+@pytest.mark.parametrize("alias", ["dx_residual", "dy"])
+def test_rmsnorm_bwd_in_place(gpu, M, N, alias):
+    """dx may be the residual-gradient input (out = res + dx accumulated in
+    place) or the dy input: every row is read by the waves that write it, so
+    the in-place call gives the bits of the out-of-place one -- also at row
+    counts that leave a block's last row group ragged."""
+    import ctypes as C
+    from kernelproblems_amd import _lib as L
+    print(f"[rms bwd in place] [{M},{N}] dx = {alias}", flush=True)
+    lib = L.lib()
+    g = gen(M + N)
+    x, dy, res = (randn_bf16((M, N), g).to(gpu) for _ in range(3))
+    w = randn_bf16(N, g, 1.0, 0.02).to(gpu)
+    ws = torch.empty(int(lib.kp_rmsnorm_bwd_workspace_size(M, N)), dtype=torch.uint8, device=gpu)
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(dy_t, res_t, dx_t, dw_t):
+        st = lib.kp_rmsnorm_bwd_bf16(L.ptr_array([dy_t.data_ptr()]), L.i64_array([N]), 1,
+                                     L.ptr_array([x.data_ptr()]), L.i64_array([N]), 1, None, w.data_ptr(), N, N,
+                                     res_t.data_ptr(), N, dx_t.data_ptr(), N, dw_t.data_ptr(), None, 0, M, N, 1e-5,
+                                     ws.data_ptr(), ws.numel(), stream)
+        assert st == 0, lib.kp_last_error_message().decode()
+
+    dx_ref = torch.empty_like(x)
+    dw_ref = torch.empty(N, dtype=torch.float32, device=gpu)
+    call(dy, res, dx_ref, dw_ref)
+    dw = torch.empty_like(dw_ref)
+    if alias == "dx_residual":
+        buf = res.clone()
+        call(dy, buf, buf, dw)
+    else:
+        buf = dy.clone()
+        call(buf, res, buf, dw)
+    torch.cuda.synchronize()
+    assert torch.equal(buf, dx_ref)
+    assert torch.equal(dw, dw_ref)
