@@ -126,6 +126,9 @@ int kp_rmsnorm_fwd_bf16(const void* const* x_terms, const int64_t* x_strides, in
  *   (fp32 [N]; rounded to bf16 first when dw_f32_round_bf16 != 0, the
  *   reference's bf16 -> _to_copy(f32)) and/or dw_bf16 (bf16 [N]).  Both may be
  *   NULL; weight must be non-NULL whenever either is requested.
+ * dx may be one of the bf16 inputs itself (a dy term or dx_residual, same
+ *   base and row stride: the residual gradient accumulated in place); each
+ *   row is read by the waves that write it.  Partial overlap is undefined.
  * workspace: at least kp_rmsnorm_bwd_workspace_size(M, N) bytes, 16-byte aligned.
  */
 size_t kp_rmsnorm_bwd_workspace_size(int64_t M, int64_t N);
