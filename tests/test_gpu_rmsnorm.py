@@ -241,13 +241,14 @@ def test_block_trace_hook_records_every_block_and_changes_nothing(gpu, M, N, res
     assert bool((buf[cap * 4:] == 0).all()), "nothing may be written past the records"
 
 
-@pytest.mark.parametrize("M,N", [(8191, 4096), (8192, 4096), (1001, 1024), (3, 512), (16383, 8192)])
+@pytest.mark.parametrize("M,N", [(8191, 4096), (8192, 4096), (1001, 1024), (3, 512), (16383, 8192), (37, 1000)])
 @pytest.mark.parametrize("alias", ["dx_residual", "dy"])
 def test_rmsnorm_bwd_in_place(gpu, M, N, alias):
     """dx may be the residual-gradient input (out = res + dx accumulated in
     place) or the dy input: every row is read by the waves that write it, so
     the in-place call gives the bits of the out-of-place one -- also at row
-    counts that leave a block's last row group ragged."""
+    counts that leave a block's last row group ragged, and on the generic
+    kernel (N = 1000)."""
     import ctypes as C
     from kernelproblems_amd import _lib as L
     print(f"[rms bwd in place] [{M},{N}] dx = {alias}", flush=True)
